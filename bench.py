@@ -1,0 +1,183 @@
+"""Benchmark driver: SpMM TFLOPS (2*nnz*colB/t) and % of the MI355X HBM
+roofline for one synthetic configuration, on one GPU.
+
+A step is one full tiled SpMM C = A*B (the three row-block class kernels,
+each on its own stream, joined on the null stream) with A's tiles, the
+schedule, B and C already resident in HBM.  Default workload: configuration 2
+(5-point Laplacian 512x512, fp16, colB 128).  Prints ONE JSON line.
+
+  python bench.py [--steps K] [--warmup W] [--config 1..5] [--prec fp16|tf32]
+                  [--colB N] [--no-cpu] [--no-vendor] [--gpus 1]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+NAMES = {1: "C1 uniform 4096^2 8/row", 2: "C2 5-pt Laplacian 512x512", 3: "C3 power-law 2^20 mean 16",
+         4: "C4 block-sparse 65536^2", 5: "C5 RMAT scale 22"}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def alg_bytes(rows, nnz, s_a, k_rows, n, s_b):
+    """Compulsory bytes: CSR A (rowptr + colidx + values), the B rows the
+    product touches read once, C written once in fp32."""
+    return 4 * (rows + 1) + nnz * (4 + s_a) + k_rows * n * s_b + rows * n * 4
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--prec", choices=["fp16", "tf32"], default=None)
+    ap.add_argument("--colB", type=int, default=-1)
+    ap.add_argument("--gamma", type=float, default=None)
+    ap.add_argument("--delta", type=float, default=None)
+    ap.add_argument("--no-tune", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-vendor", action="store_true")
+    ap.add_argument("--class-reps", type=int, default=200)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the SpMM is not split across GPUs", file=sys.stderr)
+        sys.exit(2)
+
+    import tilespmm_amd as tsp
+    hip, host = tsp.load()
+    if not tsp.device_available():
+        raise SystemExit("bench.py: no gfx950 device")
+
+    prec = {"fp16": 0, "tf32": 1, None: -1}[args.prec]
+    t0 = time.time()
+    A, B, colB, cbp = tsp.gen_config(args.config, prec, args.colB)
+    prec = A.prec
+    s = 2 if prec == 0 else 4
+    log(f"generated {NAMES[args.config]}: {A.rows} rows, nnz {A.nnz}, colB {colB} ({time.time() - t0:.1f}s)")
+
+    t0 = time.time()
+    f = tsp.features(A, 9.5, colB)
+    g, d = tsp.predict(f, prec)
+    if args.gamma is not None:
+        g = args.gamma
+    if args.delta is not None:
+        d = args.delta
+    subs = tsp.matrix_split(A, g, d)
+    tiles = [tsp.tile_create(sb, A.cols, bm, prec) for sb, bm in zip(subs, (64, 16, 8))]
+    pre_ms = (time.time() - t0) * 1e3
+    log(f"split+tiles gamma={g} delta={d}: tilenum {[t.tilenum for t in tiles]} ({pre_ms:.0f} ms)")
+
+    plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
+    th, model_ms, tune_ms = plan.tune(not args.no_tune)
+    log(f"thresholds {th} (model {model_ms:.1f} ms, tuning {tune_ms:.1f} ms)")
+
+    # warmup, then K timed steps bracketed by device syncs and null-stream events
+    plan.warmup(args.warmup)
+    plan.run(zero_c=True)
+    hip.tsp_device_sync()
+    ms = plan.time(args.steps)
+    hip.tsp_device_sync()
+    tflops = 2.0 * A.nnz * colB / (ms * 1e-3) / 1e12
+
+    # per-class kernel time (each class alone on its own stream)
+    cls = {}
+    for t, sb, bm in zip(tiles, subs, (64, 16, 8)):
+        if t.tilenum == 0:
+            continue
+        cms = plan.time_class(bm, args.class_reps)
+        k_rows = int(np.unique(t.arrays()["tile_colidx"]).size)
+        b = alg_bytes(sb.rows, sb.nnz, s, k_rows, colB, s)
+        cls[bm] = {"ms": cms, "rows": sb.rows, "nnz": int(sb.nnz), "tiles": t.tilenum,
+                   "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9}
+    dom = max(cls, key=lambda k: cls[k]["ms"])
+    k_all = int(np.unique(A.colidx).size)
+    step_bytes = alg_bytes(A.rows, A.nnz, s, k_all, colB, s)
+    step_gbs = step_bytes / (ms * 1e-3) / 1e9
+
+    traffic = None
+    prof = os.path.join(ROOT, "profiles", f"traffic_config{args.config}_{'fp16' if prec == 0 else 'tf32'}_{colB}.json")
+    if os.path.exists(prof):
+        with open(prof) as fh:
+            tr = json.load(fh)
+        traffic = tr.get(f"bm{dom}", {}).get("hbm_bytes_per_launch")
+
+    roof = {"bound": "hbm", "achieved": round(cls[dom]["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(cls[dom]["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": f"spmm_kernel<BM={dom}>", "kernel_ms": round(cls[dom]["ms"], 5),
+            "alg_bytes_per_launch": cls[dom]["alg_bytes"],
+            "step_achieved": round(step_gbs, 2), "step_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+            "step_alg_bytes": step_bytes}
+
+    vendor = None
+    if not args.no_vendor:
+        import ctypes as C
+        vp, vm = C.c_double(), C.c_double()
+        Cv = np.zeros((A.rows, colB), dtype=np.float32)
+        st = hip.tsp_vendor_spmm(prec, A.rows, A.cols, A.nnz, A.rowptr.ctypes.data_as(C.c_void_p),
+                                 A.colidx.ctypes.data_as(C.c_void_p), A.val.ctypes.data_as(C.c_void_p), colB, cbp,
+                                 np.ascontiguousarray(B).ctypes.data_as(C.c_void_p),
+                                 Cv.ctypes.data_as(C.c_void_p), 20, 200, C.byref(vp), C.byref(vm))
+        if st == 0:
+            vendor = {"lib": "rocSPARSE spmm (CSR, alg default)", "ms": round(vm.value, 5),
+                      "tflops": round(2.0 * A.nnz * colB / (vm.value * 1e-3) / 1e12, 4)}
+        else:
+            vendor = {"lib": "rocSPARSE", "status": st}
+        del Cv
+
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        a32 = oracle.values_f64(A.val, prec).astype(np.float32)
+        b32 = oracle.values_f64(B[:, :colB].reshape(-1), prec).astype(np.float32).reshape(A.cols, colB)
+        # bounded sample: the first rows holding ~min(nnz, 4M) entries
+        lim = min(A.nnz, 4_000_000)
+        r_end = int(np.searchsorted(A.rowptr, lim, side="right")) - 1
+        r_end = max(1, min(A.rows, r_end))
+        nz = int(A.rowptr[r_end])
+        out = np.zeros((r_end, colB), dtype=np.float32)
+        oracle.spmm_f32_omp(r_end, A.rowptr[:r_end + 1], A.colidx, a32, b32, colB, out)   # warmup
+        times = []
+        used = 1
+        for _ in range(5):
+            t1 = time.perf_counter()
+            _, used = oracle.spmm_f32_omp(r_end, A.rowptr[:r_end + 1], A.colidx, a32, b32, colB, out)
+            times.append(time.perf_counter() - t1)
+        tm = float(np.median(times))
+        cpu = {"value": round(2.0 * nz * colB / tm / 1e12, 5), "unit": "TFLOPS", "cores": int(used), "kind": "port",
+               "sample": f"rows 0..{r_end} ({nz} of {A.nnz} nnz), colB {colB}, fp32 accumulate, "
+                         f"OpenMP dynamic(64), median of 5 after 1 warmup, {tm * 1e3:.2f} ms"}
+
+    line = {
+        "metric": "SpMM TFLOPS (2*nnz*colB/t) + % HBM roofline",
+        "value": round(tflops, 4), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16" if prec == 0 else "tf32", "data": "synthetic",
+        "config": {"workload": f"{NAMES[args.config]}, {'fp16' if prec == 0 else 'tf32'}, colB {colB}",
+                   "config_id": args.config, "rows": A.rows, "nnz": A.nnz, "colB": colB, "colB_padded": cbp,
+                   "gamma": g, "delta": d, "th": list(th), "tilenum": [t.tilenum for t in tiles],
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "classes": {f"bm{k}": {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in cls.items()},
+        "vendor": vendor,
+        "cpu_baseline": cpu,
+        "pre_ms": {"split_tiles": round(pre_ms, 1), "model": round(model_ms, 2), "tune": round(tune_ms, 1)},
+    }
+    plan.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,207 @@
+/*
+ * tilespmm.h -- C ABI of the TileSpMM host library, libtilespmm_host.so.
+ *
+ * This is the reference's host-side surface (CSR -> matrix_split -> csr2tile
+ * tiles -> task schedule -> launch), kept with the reference's names and
+ * argument meanings so code written against it drops in.  Values travel as
+ * raw bit patterns of the precision's storage type: binary16 (uint16) for
+ * TSP_PREC_FP16, binary32 (float) for TSP_PREC_TF32.
+ *
+ * Errors: every function returns an int status (0 = success; TSP_E* codes or
+ * a HIP status from tilespmm_hip.h otherwise) instead of calling exit(); the
+ * CLI turns a non-zero status into exit(1) as src/common.h:75-94 does.
+ */
+#ifndef TILESPMM_H
+#define TILESPMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "tilespmm_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TSP_ENOMEM 1003     /* host allocation failed */
+#define TSP_EIO 1004        /* file missing or malformed */
+
+/* Tile format of one row-block class.  Field names and meanings follow the
+ * reference's Tile_matrix (src/format.h:4-21):
+ *   tile_ptr[tilem+1]       tiles per row-block, exclusive prefix sum
+ *   tile_nnz[tilenum+1]     CSR entries per tile, exclusive prefix sum
+ *   tile_colidx[tilenum*BN] sorted distinct columns, last tile padded with
+ *                           the last valid column
+ *   Blockdense_Val          tilenum * BM * BN values.  Layout differs from the
+ *                           reference on purpose: canonical ROW-MAJOR tiles
+ *                           (the reference stores NVIDIA mma.sync fragment
+ *                           order, src/csr2tile.h:255-372); the values are the
+ *                           same bits once that permutation is inverted.
+ *   rowblkblock, blkcoostylerowidx, blkcoostylerowidx_colstart: the current
+ *                           task schedule (tile_pretreatment).
+ *   orig_tile_row_idx[tilem] first original row of each row-block.
+ * Added for MI355X: bm, bn, prec, and the occupancy bitmap (bit r*BN+c of a
+ * tile is set when some CSR entry lands at row r, slot c; bitmap_words
+ * uint64 words per tile). */
+typedef struct {
+    int tilem;
+    int tilen;
+    int tilenum;
+    int *tile_ptr;
+    int *tile_nnz;
+    int *tile_colidx;
+    void *Blockdense_Val;
+    size_t dnssize;
+    int rowblkblock;
+    unsigned int *blkcoostylerowidx;
+    int *blkcoostylerowidx_colstart;
+    int *orig_tile_row_idx;
+    int bm, bn, prec;
+    int bitmap_words;
+    uint64_t *tile_bitmap;
+} Tile_matrix;
+
+/* One row class of the split (build_sub_csr outputs, src/hetero_split.h:86). */
+typedef struct {
+    int rows;
+    long long nnz;
+    int *ptr;
+    int *idx;
+    void *val;
+    int *orig_row;
+} tsp_sub_csr;
+
+/* ---- Matrix Market ------------------------------------------------------
+ * mmio_allinone semantics (src/mmio_highlevel.h:307-480): COO -> CSR in file
+ * order, symmetric/hermitian mirrored (diagonal once), pattern -> 1,
+ * complex -> real part, no sort, no dedupe.  Unlike the reference, a missing
+ * or malformed file is an error (TSP_EIO), not silently ignored.
+ * Values are returned as doubles; free arrays with tsp_free_host. */
+int tsp_mm_read(const char *path, int *rows, int *cols, long long *nnz, int *is_symmetric,
+                int **rowptr, int **colidx, double **val);
+void tsp_free_host(void *p);
+
+/* ---- Row split (matrix_split, src/hetero_split.h:144-291) --------------- */
+int tsp_matrix_split(int rowA, int colA, long long nnzA, const int *rowptr, const int *colidx,
+                     const void *val, int prec, float gamma, float delta,
+                     tsp_sub_csr *out64, tsp_sub_csr *out16, tsp_sub_csr *out8);
+/* Only the per-row class (0 = 64-row, 1 = 16-row, 2 = 8-row). */
+int tsp_split_classes(int rowA, int colA, const int *rowptr, const int *colidx, float gamma,
+                      float delta, int *row_class);
+void tsp_sub_csr_free(tsp_sub_csr *s);
+
+/* ---- CSR -> tiles (Tile_create, src/csr2tile.h:724-795) ----------------- */
+int tsp_tile_create(Tile_matrix *m, int rows, int colA, long long nnz, const int *ptr,
+                    const int *idx, const void *val, const int *orig_row, int BM, int BN,
+                    int prec);
+/* Frees every array of the tile matrix (including orig_tile_row_idx, which
+ * the reference frees separately) and zeroes the struct. */
+void tsp_tile_destroy(Tile_matrix *m);
+/* BN the reference uses for (BM, precision) (src/main.cu:267-275). */
+int tsp_tile_bn(int bm, int prec);
+
+/* ---- Task schedule (tile_pretreatment, src/csr2tile.h:383-434) ---------
+ * Writes a fresh schedule into *rows / *colstart (malloc'd; caller frees
+ * with tsp_free_host) and the task count into *rowblkblock. */
+int tsp_tile_pretreatment(const Tile_matrix *m, int TH, int *rowblkblock, unsigned **rows,
+                          int **colstart);
+
+/* ---- Threshold cost model (get_optimal_prefetch_th, :437-642) ----------
+ * Resource inputs of the analytic model; tsp_th_params_probe fills them
+ * from the device and the kernel that will run (hipDeviceProp_t +
+ * hipFuncGetAttributes), lambda_atom from the MI355X calibration table. */
+typedef struct {
+    int sm_count, threads_per_sm, registers_per_sm, blocks_per_sm;
+    long long shared_bytes_per_sm, l2_bytes;
+    int kernel_threads, kernel_registers;
+    long long kernel_shared_bytes;
+    int iteration_bytes;
+    float lambda_atom;
+    /* launch geometry: tasks one block runs, output columns one task
+     * covers.  The reference's CUDA kernels are (4, 32) for 8/16-row tiles
+     * at colB_p = 32, (1, 32) for 64-row tiles at 32, and (1, 64) otherwise
+     * (src/csr2tile.h:588-601); the MI355X kernels report theirs through
+     * tsp_kernel_probe. */
+    int tasks_per_block, cols_per_task;
+} tsp_th_params;
+int tsp_th_params_probe(int device_id, int bm, int prec, int colB_p, tsp_th_params *out);
+/* Fills top4 (cheapest first); returns the number of distinct candidates
+ * evaluated (>= 1), or a negative value when the resources do not fit. */
+int tsp_optimal_th(int BM, int colB, int tilem, const int *tile_ptr, const tsp_th_params *p,
+                   int top4[4]);
+
+/* ---- Threshold policy (src/model_features.h, src/ml_predict.h:8-15) ----
+ * 11 features: [0, 0, rows, cols, nnz, 1-nnz/(rows*cols), nnz/rows,
+ * max_row_nnz, min_row_nnz, capability, colB].  On MI355X the capability
+ * slot holds the gfx target as major + minor/10 (gfx950 -> 9.5). */
+#define TILESPMM_ML_FEATURE_COUNT 11
+int tsp_features_from_csr(int rows, int cols, long long nnz, const int *rowptr,
+                          double capability, int colB, double *features);
+void tilespmm_predict_fp16(const double *features, float *gamma, float *delta);
+void tilespmm_predict_tf32(const double *features, float *gamma, float *delta);
+
+/* ---- Synthetic inputs (the five benchmark configurations) ---------------
+ * config 1..5 as in the benchmark definition; prec/colB < 0 select the
+ * configuration's own; seed 0 selects 20260000 + config.  Produces CSR A
+ * (values in prec's storage type) and row-major B [cols][colB_p] with the
+ * padded columns zero.  Arrays are malloc'd; free with tsp_free_host. */
+int tsp_gen_config(int config, int prec, int colB, unsigned long long seed, int *rows, int *cols,
+                   long long *nnz, int **rowptr, int **colidx, void **val, int *colB_p,
+                   void **B);
+/* Only the structure of config (no values). */
+int tsp_gen_structure(int config, unsigned long long seed, int *rows, int *cols, long long *nnz,
+                      int **rowptr, int **colidx);
+/* Fill n values of prec from seed: dist 0 = U[-1,1), 1 = N(0,1). */
+int tsp_gen_values(int prec, int dist, unsigned long long seed, size_t n, void *out);
+/* padded width the kernels see: colB <= 32 ? 32 : roundup(colB, 64). */
+int tsp_colB_padded(int colB);
+
+/* ---- Device plan: the orchestration of call_tilespmm_cuda -------------
+ * (src/csr2tile.h:826-1093) split into steps so both the CLI and benchmark
+ * drivers use it.  A plan owns device copies of the three classes, B, C, one
+ * stream per class and the timing events. */
+typedef struct tsp_plan tsp_plan;
+int tsp_plan_create(tsp_plan **plan, int device_id, Tile_matrix *m64, Tile_matrix *m16,
+                    Tile_matrix *m8, int rowA, int colA, int colB_p, int prec, const void *h_B);
+/* Build + upload schedules for the three classes (a TH <= 0 keeps the
+ * current one). */
+int tsp_plan_set_th(tsp_plan *plan, int th64, int th16, int th8);
+/* Cost-model top-4 per class, then runtime tuning over the cross product
+ * (5 untimed + 10 timed runs each, src/csr2tile.h:962-1014).  Leaves the best
+ * schedule installed; outputs the thresholds and the two timing parts. */
+int tsp_plan_tune(tsp_plan *plan, int tune, int th_out[3], double *model_ms, double *tune_ms);
+/* Launch the three classes once (each on its own stream, joined on the null
+ * stream).  zero_c != 0 clears C first. */
+int tsp_plan_run(tsp_plan *plan, int zero_c);
+/* Clock-stabilising warmup (src/csr2tile.h:798-823 analogue). */
+int tsp_plan_warmup(tsp_plan *plan, int max_iters);
+/* Time `reps` back-to-back runs bracketed by events on the null stream. */
+int tsp_plan_time(tsp_plan *plan, int reps, double *ms_per_iter);
+/* Time one class alone on its stream (reps launches). */
+int tsp_plan_time_class(tsp_plan *plan, int bm, int reps, double *ms_per_launch);
+int tsp_plan_download_c(tsp_plan *plan, float *h_C);
+/* Device pointers of the plan (for external drivers). */
+int tsp_plan_device_c(tsp_plan *plan, float **d_C);
+int tsp_plan_destroy(tsp_plan *plan);
+
+/* ---- One-call orchestration (call_tilespmm_cuda) -----------------------
+ * Plan + tune + warmup + result run + download + timed loop.  Writes CSV
+ * fields 11-16 to csv when non-NULL, with the reference's formats. */
+typedef struct {
+    int th64, th16, th8;
+    double pre_time_ms;      /* cpu_pre_time + model + tuning */
+    double time_ms;          /* per iteration */
+    double tflops;           /* 2 * nnz * logical_colB / t */
+    double model_ms, tune_ms;
+} tsp_run_result;
+int tsp_call_tilespmm(int device_id, Tile_matrix *m64, Tile_matrix *m16, Tile_matrix *m8, int rowA,
+                      int colA, int colB_p, long long total_nnz, int prec, const void *h_B,
+                      float *h_C, double cpu_pre_time_ms, int logical_colB, int repeat, int tune,
+                      FILE *csv, tsp_run_result *out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TILESPMM_H */

@@ -1,0 +1,144 @@
+/*
+ * tilespmm_hip.h -- C ABI of the MI355X (gfx950) TileSpMM device library,
+ * libtilespmm_hip.so.  Plain pointers and sizes only; every function returns
+ * an int status (0 = success, otherwise a hipError_t value or one of the
+ * TSP_E* codes below) instead of exiting, so a caller maps failures to its
+ * own policy.  The CLI maps any non-zero status to exit(1), which is the
+ * reference's fail-fast behaviour (src/common.h:75-94).
+ *
+ * Data layout expected in device memory (all row-major, 4-byte indices):
+ *   B    [colA][colB_p]            value type (fp16 bits or fp32)
+ *   C    [c_rows][colB_p]          fp32
+ *   val  [tilenum][BM][BN]         value type, canonical row-major tiles
+ *   colidx [tilenum][BN]           int32, sorted distinct columns per row-block
+ *   rows [rowblkblock]             uint32 start row, bit 31 = split task
+ *   colstart [rowblkblock + 1]     int32 tile range of each task
+ * colB_p is 32 or a multiple of 64, as the reference pads it
+ * (src/main.cu:173).  BN is fixed by (BM, precision): fp16 64->32, 16->16,
+ * 8->16; tf32 64->16, 16->8, 8->8 (src/main.cu:267-275).
+ */
+#ifndef TILESPMM_HIP_H
+#define TILESPMM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TSP_PREC_FP16 0
+#define TSP_PREC_TF32 1
+
+#define TSP_OK 0
+#define TSP_EINVAL 1001      /* bad argument (class, width, pointer) */
+#define TSP_ENODEV 1002      /* no usable gfx950 device */
+
+/* Library version string and the offload target it was built for. */
+const char *tsp_hip_version(void);
+
+/* Last error text of this thread (static storage). */
+const char *tsp_hip_error_string(int status);
+
+/* Select the device and check that it is a gfx950 part.
+ * Replaces cudaSetDevice + cudaGetDeviceProperties + prefetch_device_matches
+ * (src/main.cu:210-219). */
+int tsp_device_init(int device_id);
+
+/* Device resource probe: the fields the reference's generated
+ * PrefetchDeviceInfo carries (pre/prefetch_probe.cu:62-95), read from
+ * hipDeviceProp_t.  Any pointer may be NULL. */
+typedef struct {
+    int cu_count;               /* multiProcessorCount */
+    int max_threads_per_cu;
+    int regs_per_cu;            /* 32-bit registers per CU */
+    int max_blocks_per_cu;
+    long long lds_bytes_per_cu;
+    long long l2_bytes;
+    int wavefront_size;
+    int clock_khz;
+    int memory_clock_khz;
+    int memory_bus_width;
+    char name[256];
+    char gcn_arch[64];
+} tsp_device_info;
+int tsp_device_probe(int device_id, tsp_device_info *out);
+
+/* Kernel resource probe for one (BM, precision, colB_p) kernel: the fields of
+ * the reference's PrefetchKernelInfo (pre/prefetch_probe.cu:15-27), read with
+ * hipFuncGetAttributes.  iteration_bytes = tasks per block x
+ * (BM*BN + BN*cols) x value size. */
+typedef struct {
+    int threads;                /* threads per block */
+    int tasks_per_block;        /* independent tasks one block runs */
+    int registers_per_thread;   /* VGPRs (arch + acc) per lane */
+    long long shared_bytes;     /* static LDS per block */
+    int iteration_bytes;
+    int cols_per_task;          /* output columns one task covers */
+} tsp_kernel_info;
+int tsp_kernel_probe(int bm, int prec, int colB_p, tsp_kernel_info *out);
+
+/* Memory and copies (hipMalloc / hipMemcpy / hipMemset wrappers). */
+int tsp_malloc(void **ptr, size_t bytes);
+int tsp_free(void *ptr);
+int tsp_memcpy_h2d(void *dst, const void *src, size_t bytes);
+int tsp_memcpy_d2h(void *dst, const void *src, size_t bytes);
+int tsp_memcpy_h2d_async(void *dst, const void *src, size_t bytes, void *stream);
+int tsp_memset(void *dst, int value, size_t bytes);
+int tsp_memset_async(void *dst, int value, size_t bytes, void *stream);
+
+/* Streams and events.  Streams are created at the default priority. */
+int tsp_stream_create(void **stream);
+int tsp_stream_destroy(void *stream);
+int tsp_stream_sync(void *stream);
+int tsp_device_sync(void);
+int tsp_event_create(void **event);
+int tsp_event_destroy(void *event);
+int tsp_event_record(void *event, void *stream);   /* stream NULL = null stream */
+int tsp_event_sync(void *event);
+int tsp_event_elapsed_ms(float *ms, void *start, void *stop);
+
+/* Tile SpMM launch, one row-block class:
+ *   C[rows of task][cols] (=, or += atomically for split tasks)
+ *       sum over the task's tiles of  A_tile (BM x BN) * B[colidx[tile]][cols]
+ * Replaces switch_tilespmm_cuda_v64 / _v16 / _v8
+ * (src/tilespmm_cuda.h:1634-1744); same arguments plus c_rows, the number of
+ * rows of C that may be written (rows >= c_rows of a short last row-block are
+ * skipped instead of relying on padding rows).  Asynchronous on `stream`;
+ * returns the launch status.  C must be zeroed first when any task is split
+ * (bit 31 of its row word). */
+int tsp_spmm_launch(int bm, int prec, int rowblkblock, int colB_p,
+                    const void *d_val, const unsigned *d_rows, const int *d_colstart,
+                    const void *d_B, float *d_C, const int *d_colidx,
+                    int c_rows, void *stream);
+
+/* Per-class entry points with the reference dispatcher names
+ * (src/tilespmm_cuda.h:1634, :1672, :1710) and argument order. */
+int tsp_switch_v64(int prec, int rowblkblock, int colB_p, const void *d_val,
+                   const unsigned *d_rows, const int *d_colstart, const void *d_B,
+                   float *d_C, const int *d_colidx, int c_rows, void *stream);
+int tsp_switch_v16(int prec, int rowblkblock, int colB_p, const void *d_val,
+                   const unsigned *d_rows, const int *d_colstart, const void *d_B,
+                   float *d_C, const int *d_colidx, int c_rows, void *stream);
+int tsp_switch_v8(int prec, int rowblkblock, int colB_p, const void *d_val,
+                  const unsigned *d_rows, const int *d_colstart, const void *d_B,
+                  float *d_C, const int *d_colidx, int c_rows, void *stream);
+
+/* Vendor SpMM baseline on rocSPARSE, the counterpart of cusparse_spmm_all
+ * (src/main.cu:16-134): host CSR A (prec values), host B [k][ldb] row-major
+ * (first n columns used), host C [m][n] fp32 out.  pre_ms = descriptor and
+ * buffer set-up (wall clock), ms = mean of `repeat` timed calls after
+ * `warmup` untimed ones.  Allocates and frees its own device memory. */
+int tsp_vendor_spmm(int prec, int m, int k, long long nnz, const int *rowptr, const int *colidx,
+                    const void *val, int n, int ldb, const void *h_B, float *h_C, int warmup,
+                    int repeat, double *pre_ms, double *ms);
+
+/* A plain streaming copy kernel (dst = src, 16-byte vectors), used to
+ * calibrate HBM byte counters and the achievable copy bandwidth. */
+int tsp_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TILESPMM_HIP_H */

@@ -1,0 +1,80 @@
+"""The C-ABI libraries load and export every function include/*.h declares
+(no compute calls: this runs without a GPU)."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+
+HEADERS = ["include/tilespmm_hip.h", "include/tilespmm.h"]
+
+
+def declared(header):
+    text = open(os.path.join(ROOT, header)).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(", text, flags=re.M)
+    return sorted(set(n for n in names if n not in ("if", "defined")))
+
+
+def exported(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", lib], capture_output=True, text=True, check=True).stdout
+    return {l.split()[-1] for l in out.splitlines() if l.strip()}
+
+
+def test_headers_declare_expected_entry_points():
+    hip = declared(HEADERS[0])
+    host = declared(HEADERS[1])
+    for n in ("tsp_spmm_launch", "tsp_switch_v64", "tsp_switch_v16", "tsp_switch_v8", "tsp_device_init"):
+        assert n in hip
+    for n in ("tsp_matrix_split", "tsp_tile_create", "tsp_tile_pretreatment", "tsp_optimal_th",
+              "tilespmm_predict_fp16", "tilespmm_predict_tf32", "tsp_call_tilespmm"):
+        assert n in host
+
+
+def test_libraries_export_every_declared_symbol(tsp):
+    libdir = os.path.join(ROOT, "tilespmm_amd", "lib")
+    hip_syms = exported(os.path.join(libdir, "libtilespmm_hip.so"))
+    host_syms = exported(os.path.join(libdir, "libtilespmm_host.so"))
+    missing = [n for n in declared(HEADERS[0]) if n not in hip_syms]
+    missing += [n for n in declared(HEADERS[1]) if n not in host_syms]
+    assert not missing, missing
+
+
+def test_python_binding_covers_headers(tsp):
+    bound = set(tsp.HIP_SYMBOLS) | set(tsp.HOST_SYMBOLS)
+    missing = [n for h in HEADERS for n in declared(h) if n not in bound]
+    assert not missing, missing
+
+
+def test_kernels_built_for_gfx950():
+    lib = os.path.join(ROOT, "tilespmm_amd", "lib", "libtilespmm_hip.so")
+    # the embedded offload bundle names its target triple
+    data = open(lib, "rb").read()
+    assert b"amdgcn-amd-amdhsa--gfx950" in data
+
+
+def test_error_strings_and_arg_checks(tsp):
+    hip, _ = tsp.load()
+    assert b"gfx950" in hip.tsp_hip_version()
+    assert hip.tsp_hip_error_string(1001)
+    # invalid class / width are rejected on the host before any launch
+    assert hip.tsp_spmm_launch(32, 0, 1, 128, None, None, None, None, None, None, 0, None) == 1001
+    assert hip.tsp_spmm_launch(16, 0, 1, 96, None, None, None, None, None, None, 0, None) == 1001
+    assert hip.tsp_spmm_launch(16, 2, 1, 128, None, None, None, None, None, None, 0, None) == 1001
+    assert hip.tsp_spmm_launch(16, 0, 1, 128, None, None, None, None, None, None, 0, None) == 1001
+    assert hip.tsp_spmm_launch(16, 0, 0, 128, None, None, None, None, None, None, 0, None) == 0
+
+
+def test_cli_usage_and_errors(tmp_path):
+    exe = os.path.join(ROOT, "tilespmm_amd", "bin", "tilespmm_fp16")
+    r = subprocess.run([exe], capture_output=True, text=True)
+    assert r.returncode == 1 and "Usage" in r.stdout
+    r = subprocess.run([exe, "-d", "0", str(tmp_path / "nope.mtx"), "32"], capture_output=True, text=True)
+    assert r.returncode == 1
+    p = tmp_path / "a.mtx"
+    p.write_text("%%MatrixMarket matrix coordinate pattern general\n2 2 1\n1 1\n")
+    r = subprocess.run([exe, "-d", "0", str(p), "0"], capture_output=True, text=True)
+    assert r.returncode == 1 and "colB" in r.stderr

@@ -1,0 +1,230 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Tolerances (element-wise, normalised by the magnitude sum |A|.|B| of the
+entry): fp16 path 1e-3, tf32 path 1e-4 -- the north-star bounds.  Inputs are
+exact in the kernels' arithmetic (fp16 values; tf32-rounded fp32 values), so
+the only error is fp32 accumulation.  With the CLI's integer value stream the
+result is an exact integer and the comparison is exact equality.
+"""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = {0: 1e-3, 1: 1e-4}
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def gpu(tsp):
+    if not tsp.device_available():
+        pytest.fail("no gfx950 device: GPU tests need an MI355X")
+    return tsp
+
+
+def run_tiles(tsp, A, B, colB_p, gamma, delta, th=(8, 8, 8), tune=False):
+    subs = tsp.matrix_split(A, gamma, delta)
+    tiles = [tsp.tile_create(s, A.cols, bm, A.prec) for s, bm in zip(subs, (64, 16, 8))]
+    plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, colB_p, A.prec, B)
+    try:
+        if tune:
+            plan.tune(True)
+        else:
+            plan.set_th(*th)
+        plan.run(zero_c=True)
+        Cg = plan.download_c()
+    finally:
+        plan.close()
+    return Cg, tiles
+
+
+def reference(orc, A, B, colB, rows=None):
+    """fp64 CSR SpMM of the kernel's exact inputs; optionally a row subset."""
+    tf = A.prec == 1
+    a = orc.values_f64(A.val, A.prec, tf32_round=tf)
+    b = orc.values_f64(B[:, :colB].reshape(-1), A.prec, tf32_round=tf).reshape(B.shape[0], colB)
+    rp, ci = A.rowptr, A.colidx
+    if rows is not None:
+        rows = np.asarray(rows)
+        lens = rp[rows + 1] - rp[rows]
+        sel = np.concatenate([np.arange(rp[r], rp[r + 1]) for r in rows]) if len(rows) else np.zeros(0, int)
+        rp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        ci, a = ci[sel], a[sel]
+    n = len(rp) - 1
+    Cref = orc.spmm_f64(n, rp, ci, a, b, colB)
+    Cabs = orc.spmm_f64(n, rp, ci, np.abs(a), np.abs(b), colB)
+    return Cref, Cabs
+
+
+def assert_close(Cg, Cref, Cabs, prec, what=""):
+    err = np.abs(Cg.astype(np.float64) - Cref)
+    bound = TOL[prec] * Cabs + 1e-30
+    bad = err > bound
+    assert np.isfinite(Cg).all(), what
+    if bad.any():
+        i = np.argwhere(bad)[0]
+        pytest.fail(f"{what}: {bad.sum()} entries out of tolerance, first {tuple(i)}: "
+                    f"gpu={Cg[tuple(i)]!r} ref={Cref[tuple(i)]!r} bound={bound[tuple(i)]!r}")
+
+
+def random_matrix(tsp, rng, rows, cols, maxlen, prec, empty_frac=0.1, heavy_rows=0):
+    lens = rng.integers(0, maxlen + 1, rows)
+    lens[rng.random(rows) < empty_frac] = 0
+    if heavy_rows:
+        lens[rng.choice(rows, heavy_rows, replace=False)] = min(cols, 40 * maxlen)
+    rp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    ci = np.concatenate([rng.choice(cols, size=int(l), replace=False) for l in lens]).astype(np.int32) \
+        if rp[-1] else np.zeros(0, np.int32)
+    v = rng.uniform(-1, 1, rp[-1]).astype(np.float32)
+    val = v.astype(np.float16).view(np.uint16) if prec == 0 else v
+    return tsp.Csr(rows, cols, rp, ci, val, prec)
+
+
+def random_b(tsp, rng, cols, colB, prec):
+    cbp = tsp.colB_padded(colB)
+    b = np.zeros((cols, cbp), dtype=np.float32)
+    b[:, :colB] = rng.uniform(-1, 1, (cols, colB))
+    return (b.astype(np.float16).view(np.uint16) if prec == 0 else b), cbp
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+@pytest.mark.parametrize("colB", [8, 32, 64, 100, 128, 192, 256])
+def test_random_all_classes(gpu, orc, prec, colB):
+    tsp = gpu
+    rng = np.random.default_rng(prec * 1000 + colB)
+    A = random_matrix(tsp, rng, 777, 613, 40, prec, heavy_rows=5)
+    B, cbp = random_b(tsp, rng, A.cols, colB, prec)
+    Cref, Cabs = reference(orc, A, B, colB)
+    for g, d in [(2.0, 1.5), (0.0, 1.5), (5.0, 0.0), (5.0, 3.0), (1.0, 1.0)]:
+        for th in ((8, 8, 8), (128, 128, 128)):
+            say(f"random prec={prec} colB={colB} gamma={g} delta={d} th={th}")
+            Cg, _ = run_tiles(tsp, A, B, cbp, g, d, th)
+            assert_close(Cg[:, :colB], Cref, Cabs, prec, f"g={g} d={d} th={th}")
+            if colB < cbp:
+                assert (Cg[:, colB:] == 0).all()
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+@pytest.mark.parametrize("colB", [32, 128])
+def test_cli_integer_stream_dc2_exact(gpu, orc, dc2_path, prec, colB):
+    """The reference CLI's inputs on its shipped matrix: exact integers."""
+    tsp = gpu
+    m, n, rp, ci, _, _ = tsp.mm_read(dc2_path)
+    libc = C.CDLL("libc.so.6")
+    libc.srand(1325)
+    a = np.array([1 + libc.rand() % 3 for _ in range(len(ci))], dtype=np.float32)
+    cbp = tsp.colB_padded(colB)
+    b = np.zeros((n, cbp), dtype=np.float32)
+    draws = np.array([1 + libc.rand() % 3 for _ in range(n * colB)], dtype=np.float32)
+    b[:, :colB] = draws.reshape(n, colB)
+    val = a.astype(np.float16).view(np.uint16) if prec == 0 else a
+    B = b.astype(np.float16).view(np.uint16) if prec == 0 else b
+    A = tsp.Csr(m, n, rp, ci, val, prec)
+    Cref = orc.spmm_f64(m, rp, ci, a.astype(np.float64), b[:, :colB].astype(np.float64), colB)
+    for g, d in [(2.0, 1.5), (1.0, 1.0), (5.0, 3.0)]:
+        say(f"dc2 prec={prec} colB={colB} gamma={g} delta={d}")
+        Cg, _ = run_tiles(tsp, A, B, cbp, g, d, th=(16, 16, 16))
+        assert np.array_equal(Cg[:, :colB].astype(np.float64), Cref)
+
+
+def test_direct_kernel_boundary(gpu, orc):
+    """tsp_switch_v16 called directly on device buffers (the kernel ABI)."""
+    tsp = gpu
+    hip, _ = tsp.load()
+    rng = np.random.default_rng(2)
+    A = random_matrix(tsp, rng, 64, 300, 30, 0)
+    colB = 64
+    B, cbp = random_b(tsp, rng, A.cols, colB, 0)
+    sub = tsp.Csr(A.rows, A.cols, A.rowptr, A.colidx, A.val, 0)
+    sub.orig_row = np.arange(A.rows, dtype=np.int32)
+    t = tsp.tile_create(sub, A.cols, 16, 0)
+    arr = t.arrays()
+    rows, cs = tsp.pretreatment(t, 3)          # small TH: several split tasks
+    assert (rows & 0x80000000).any()
+    bufs = {}
+
+    def up(name, a):
+        p = C.c_void_p()
+        assert hip.tsp_malloc(C.byref(p), max(a.nbytes, 4)) == 0
+        assert hip.tsp_memcpy_h2d(p, a.ctypes.data_as(C.c_void_p), a.nbytes) == 0
+        bufs[name] = p
+        return p
+
+    try:
+        up("val", arr["dense"]); up("col", arr["tile_colidx"]); up("rows", rows); up("cs", cs); up("B", B)
+        Cz = np.zeros((A.rows, cbp), dtype=np.float32)
+        up("C", Cz)
+        st = hip.tsp_switch_v16(0, len(rows), cbp, bufs["val"], bufs["rows"], bufs["cs"], bufs["B"], bufs["C"],
+                                bufs["col"], A.rows, None)
+        assert st == 0
+        assert hip.tsp_device_sync() == 0
+        out = np.zeros_like(Cz)
+        assert hip.tsp_memcpy_d2h(out.ctypes.data_as(C.c_void_p), bufs["C"], out.nbytes) == 0
+    finally:
+        for p in bufs.values():
+            hip.tsp_free(p)
+    Cref, Cabs = reference(orc, A, B, colB)
+    assert_close(out[:, :colB], Cref, Cabs, 0, "direct v16")
+
+
+def test_edge_shapes(gpu, orc):
+    tsp = gpu
+    rng = np.random.default_rng(9)
+    for rows, cols, maxlen in [(1, 1, 1), (7, 3, 3), (65, 1000, 0), (129, 17, 17), (1000, 5, 5)]:
+        for prec in (0, 1):
+            A = random_matrix(tsp, rng, rows, cols, maxlen, prec, empty_frac=0.3)
+            B, cbp = random_b(tsp, rng, cols, 32, prec)
+            Cref, Cabs = reference(orc, A, B, 32)
+            for g, d in [(2.0, 1.5), (0.0, 1.5), (5.0, 0.0), (5.0, 3.0)]:
+                say(f"edge rows={rows} cols={cols} prec={prec} g={g} d={d}")
+                Cg, _ = run_tiles(tsp, A, B, cbp, g, d, th=(8, 8, 8))
+                assert_close(Cg[:, :32], Cref, Cabs, prec, f"edge {rows}x{cols}")
+
+
+def test_tuned_plan_and_determinism(gpu, orc):
+    tsp = gpu
+    A, B, colB, cbp = tsp.gen_config(1)
+    Cref, Cabs = reference(orc, A, B, colB)
+    C1, _ = run_tiles(tsp, A, B, cbp, 2.0, 1.5, tune=True)
+    assert_close(C1[:, :colB], Cref, Cabs, 0, "C1 tuned")
+    C2, _ = run_tiles(tsp, A, B, cbp, 2.0, 1.5, th=(128, 128, 128))
+    # no split tasks at TH=128 here -> plain stores -> bit-identical reruns
+    C3, _ = run_tiles(tsp, A, B, cbp, 2.0, 1.5, th=(128, 128, 128))
+    assert np.array_equal(C2, C3)
+
+
+@pytest.mark.parametrize("config", [2, 3])
+def test_config_full_parity(gpu, orc, config):
+    tsp = gpu
+    say(f"config {config}: generating")
+    A, B, colB, cbp = tsp.gen_config(config)
+    Cref, Cabs = reference(orc, A, B, colB)
+    g, d = tsp.predict(tsp.features(A, 9.5, colB), A.prec)
+    for gd in [(g, d), (1.0, 1.0), (5.0, 3.0)]:
+        say(f"config {config}: gamma/delta {gd}")
+        Cg, _ = run_tiles(tsp, A, B, cbp, *gd, tune=True)
+        assert_close(Cg[:, :colB], Cref, Cabs, A.prec, f"config {config} {gd}")
+
+
+@pytest.mark.parametrize("config,prec,colB", [(4, -1, -1), (5, -1, -1), (3, 0, 128), (5, 0, 128)])
+def test_config_sampled_rows(gpu, orc, config, prec, colB):
+    """Large configurations: full GPU run, oracle on a row sample that includes
+    the heaviest rows and a uniform stride."""
+    tsp = gpu
+    say(f"config {config} prec {prec} colB {colB}: generating")
+    A, B, colB, cbp = tsp.gen_config(config, prec, colB)
+    g, d = tsp.predict(tsp.features(A, 9.5, colB), A.prec)
+    say(f"config {config}: split+tiles+run gamma={g} delta={d}")
+    Cg, _ = run_tiles(tsp, A, B, cbp, g, d, tune=False, th=(32, 32, 32))
+    lens = np.diff(A.rowptr)
+    rows = np.unique(np.concatenate([np.argsort(lens)[-64:], np.arange(0, A.rows, max(1, A.rows // 3000))]))
+    Cref, Cabs = reference(orc, A, B, colB, rows)
+    assert_close(Cg[rows, :colB], Cref, Cabs, A.prec, f"config {config} sampled")

@@ -1,0 +1,193 @@
+// tsp_capi.hip -- the extern "C" boundary of libtilespmm_hip.so.
+//
+// Thin wrappers over the HIP runtime plus the kernel dispatch.  Every entry
+// point returns an int status; none of them exits the process.  Argument
+// checks happen here, on the host, before anything is launched: a launch whose
+// shapes do not match what the kernels assume is refused with TSP_EINVAL.
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/tilespmm_hip.h"
+#include "tsp_kernels.h"
+
+#ifndef TSP_VERSION
+#define TSP_VERSION "0.1.0"
+#endif
+
+extern "C" {
+
+const char *tsp_hip_version(void) { return "tilespmm_hip " TSP_VERSION " gfx950"; }
+
+const char *tsp_hip_error_string(int status)
+{
+    switch (status) {
+    case TSP_OK: return "success";
+    case TSP_EINVAL: return "invalid argument (class, width or pointer)";
+    case TSP_ENODEV: return "no usable gfx950 device";
+    default: return hipGetErrorString((hipError_t)status);
+    }
+}
+
+int tsp_device_init(int device_id)
+{
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess) return (int)e;
+    if (device_id < 0 || device_id >= n) return TSP_ENODEV;
+    e = hipSetDevice(device_id);
+    if (e != hipSuccess) return (int)e;
+    hipDeviceProp_t p;
+    e = hipGetDeviceProperties(&p, device_id);
+    if (e != hipSuccess) return (int)e;
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0) return TSP_ENODEV;
+    return TSP_OK;
+}
+
+int tsp_device_probe(int device_id, tsp_device_info *out)
+{
+    if (!out) return TSP_EINVAL;
+    hipDeviceProp_t p;
+    hipError_t e = hipGetDeviceProperties(&p, device_id);
+    if (e != hipSuccess) return (int)e;
+    memset(out, 0, sizeof *out);
+    out->cu_count = p.multiProcessorCount;
+    out->max_threads_per_cu = p.maxThreadsPerMultiProcessor;
+    out->regs_per_cu = p.regsPerMultiprocessor;
+    out->max_blocks_per_cu = p.maxBlocksPerMultiProcessor;
+    out->lds_bytes_per_cu = (long long)p.maxSharedMemoryPerMultiProcessor;
+    out->l2_bytes = (long long)p.l2CacheSize;
+    out->wavefront_size = p.warpSize;
+    out->clock_khz = p.clockRate;
+    out->memory_clock_khz = p.memoryClockRate;
+    out->memory_bus_width = p.memoryBusWidth;
+    strncpy(out->name, p.name, sizeof out->name - 1);
+    strncpy(out->gcn_arch, p.gcnArchName, sizeof out->gcn_arch - 1);
+    return TSP_OK;
+}
+
+int tsp_kernel_probe(int bm, int prec, int colB_p, tsp_kernel_info *out)
+{
+    if (!out || (bm != 64 && bm != 16 && bm != 8) || (prec != 0 && prec != 1)) return TSP_EINVAL;
+    if (colB_p != 32 && (colB_p <= 0 || colB_p % 64)) return TSP_EINVAL;
+    const int w = tsp::chunk_width(bm, colB_p);
+    const void *k = tsp::select_kernel(bm, prec, w);
+    if (!k) return TSP_EINVAL;
+    hipFuncAttributes a;
+    hipError_t e = hipFuncGetAttributes(&a, k);
+    if (e != hipSuccess) return (int)e;
+    const int bn = tsp::tile_bn(bm, prec);
+    out->threads = tsp::kBlockThreads;
+    out->tasks_per_block = tsp::kWavesPerBlock;
+    out->registers_per_thread = a.numRegs;
+    out->shared_bytes = (long long)a.sharedSizeBytes;
+    out->cols_per_task = w;
+    out->iteration_bytes = tsp::kWavesPerBlock * (bm * bn + bn * w) * (prec == TSP_PREC_FP16 ? 2 : 4);
+    return TSP_OK;
+}
+
+int tsp_malloc(void **ptr, size_t bytes)
+{
+    if (!ptr) return TSP_EINVAL;
+    *ptr = nullptr;
+    if (bytes == 0) return TSP_OK;
+    return (int)hipMalloc(ptr, bytes);
+}
+int tsp_free(void *ptr) { return ptr ? (int)hipFree(ptr) : TSP_OK; }
+int tsp_memcpy_h2d(void *dst, const void *src, size_t bytes)
+{
+    return bytes ? (int)hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice) : TSP_OK;
+}
+int tsp_memcpy_d2h(void *dst, const void *src, size_t bytes)
+{
+    return bytes ? (int)hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost) : TSP_OK;
+}
+int tsp_memcpy_h2d_async(void *dst, const void *src, size_t bytes, void *stream)
+{
+    return bytes ? (int)hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream)
+                 : TSP_OK;
+}
+int tsp_memset(void *dst, int value, size_t bytes)
+{
+    return bytes ? (int)hipMemset(dst, value, bytes) : TSP_OK;
+}
+int tsp_memset_async(void *dst, int value, size_t bytes, void *stream)
+{
+    return bytes ? (int)hipMemsetAsync(dst, value, bytes, (hipStream_t)stream) : TSP_OK;
+}
+
+int tsp_stream_create(void **stream)
+{
+    if (!stream) return TSP_EINVAL;
+    hipStream_t s = nullptr;
+    hipError_t e = hipStreamCreate(&s);
+    *stream = (void *)s;
+    return (int)e;
+}
+int tsp_stream_destroy(void *stream) { return stream ? (int)hipStreamDestroy((hipStream_t)stream) : TSP_OK; }
+int tsp_stream_sync(void *stream) { return (int)hipStreamSynchronize((hipStream_t)stream); }
+int tsp_device_sync(void) { return (int)hipDeviceSynchronize(); }
+int tsp_event_create(void **event)
+{
+    if (!event) return TSP_EINVAL;
+    hipEvent_t ev = nullptr;
+    hipError_t e = hipEventCreate(&ev);
+    *event = (void *)ev;
+    return (int)e;
+}
+int tsp_event_destroy(void *event) { return event ? (int)hipEventDestroy((hipEvent_t)event) : TSP_OK; }
+int tsp_event_record(void *event, void *stream)
+{
+    return (int)hipEventRecord((hipEvent_t)event, (hipStream_t)stream);
+}
+int tsp_event_sync(void *event) { return (int)hipEventSynchronize((hipEvent_t)event); }
+int tsp_event_elapsed_ms(float *ms, void *start, void *stop)
+{
+    if (!ms) return TSP_EINVAL;
+    return (int)hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop);
+}
+
+int tsp_spmm_launch(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
+                    const unsigned *d_rows, const int *d_colstart, const void *d_B, float *d_C,
+                    const int *d_colidx, int c_rows, void *stream)
+{
+    if (bm != 64 && bm != 16 && bm != 8) return TSP_EINVAL;
+    if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
+    if (colB_p != 32 && (colB_p <= 0 || colB_p % 64 != 0)) return TSP_EINVAL;
+    if (rowblkblock < 0 || c_rows < 0) return TSP_EINVAL;
+    if (rowblkblock == 0) return TSP_OK;
+    if (!d_val || !d_rows || !d_colstart || !d_B || !d_C || !d_colidx) return TSP_EINVAL;
+    return tsp::launch(bm, prec, rowblkblock, colB_p, d_val, d_rows, d_colstart, d_B, d_C,
+                       d_colidx, c_rows, (hipStream_t)stream);
+}
+
+int tsp_switch_v64(int prec, int rowblkblock, int colB_p, const void *d_val, const unsigned *d_rows,
+                   const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,
+                   int c_rows, void *stream)
+{
+    return tsp_spmm_launch(64, prec, rowblkblock, colB_p, d_val, d_rows, d_colstart, d_B, d_C,
+                           d_colidx, c_rows, stream);
+}
+int tsp_switch_v16(int prec, int rowblkblock, int colB_p, const void *d_val, const unsigned *d_rows,
+                   const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,
+                   int c_rows, void *stream)
+{
+    return tsp_spmm_launch(16, prec, rowblkblock, colB_p, d_val, d_rows, d_colstart, d_B, d_C,
+                           d_colidx, c_rows, stream);
+}
+int tsp_switch_v8(int prec, int rowblkblock, int colB_p, const void *d_val, const unsigned *d_rows,
+                  const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,
+                  int c_rows, void *stream)
+{
+    return tsp_spmm_launch(8, prec, rowblkblock, colB_p, d_val, d_rows, d_colstart, d_B, d_C,
+                           d_colidx, c_rows, stream);
+}
+
+int tsp_copy_kernel(void *dst, const void *src, size_t bytes, void *stream)
+{
+    if ((!dst || !src) && bytes) return TSP_EINVAL;
+    if (((uintptr_t)dst | (uintptr_t)src | bytes) & 15) return TSP_EINVAL;
+    return tsp::launch_copy(dst, src, bytes, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,26 @@
+// tsp_kernels.h -- internal declarations shared by the kernel and C-ABI
+// translation units of libtilespmm_hip.so.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+namespace tsp {
+
+constexpr int kWavesPerBlock = 4;
+constexpr int kBlockThreads = 64 * kWavesPerBlock;
+
+// Tile width BN for a row-block height BM and precision (fp16: 64->32,
+// 16->16, 8->16; tf32: 64->16, 16->8, 8->8), as src/main.cu:267-275 fixes it.
+constexpr __host__ __device__ int tile_bn(int bm, int prec)
+{
+    return prec == 0 ? (bm == 64 ? 32 : 16) : (bm == 64 ? 16 : 8);
+}
+
+int chunk_width(int bm, int colB_p);
+const void *select_kernel(int bm, int prec, int w);
+int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const unsigned *rows,
+           const int *colstart, const void *B, float *C, const int *colidx, int c_rows,
+           hipStream_t s);
+int launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
+
+}  // namespace tsp

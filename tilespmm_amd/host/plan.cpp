@@ -1,0 +1,316 @@
+// plan.cpp -- device orchestration of one SpMM problem (call_tilespmm_cuda,
+// src/csr2tile.h:826-1093), split into steps that the CLI and the benchmark
+// driver share.  All device work goes through the C ABI of
+// libtilespmm_hip.so; this file never touches the HIP runtime directly.
+//
+// Per row-block class the plan holds the tiles (values + column indices) and
+// the current schedule in device memory, a host-side cache of schedules by
+// threshold (the reference caches four, src/csr2tile.h:657-711), and one
+// stream.  The three classes write disjoint rows of C and run concurrently;
+// every join point is an event on the null stream, which orders after all
+// three (blocking) class streams, as the reference's legacy-stream events do.
+#include <string.h>
+
+#include <chrono>
+#include <map>
+#include <memory>
+#include <utility>
+#include <vector>
+
+#include "common.hpp"
+
+namespace {
+
+struct ClassDev {
+    Tile_matrix *m = nullptr;
+    int bm = 0;
+    void *d_val = nullptr;
+    int *d_colidx = nullptr;
+    unsigned *d_rows = nullptr;
+    int *d_colstart = nullptr;
+    long long cap_tasks = 0;
+    int th = 0;
+    int ntasks = 0;
+    void *stream = nullptr;
+    std::map<int, std::pair<std::vector<unsigned>, std::vector<int>>> cache;
+    bool active() const { return m && m->tilenum > 0; }
+};
+
+double now_ms()
+{
+    return std::chrono::duration<double, std::milli>(
+               std::chrono::steady_clock::now().time_since_epoch())
+        .count();
+}
+
+}  // namespace
+
+struct tsp_plan {
+    int dev = 0, prec = 0, rowA = 0, colA = 0, colB_p = 0;
+    void *d_B = nullptr;
+    float *d_C = nullptr;
+    ClassDev cls[3];
+    void *ev0 = nullptr, *ev1 = nullptr;
+};
+
+#define TSP_TRY(x)                  \
+    do {                            \
+        int st_ = (x);              \
+        if (st_) return st_;        \
+    } while (0)
+
+static int upload_schedule(tsp_plan *p, ClassDev &c, int th)
+{
+    auto it = c.cache.find(th);
+    if (it == c.cache.end()) {
+        int n = 0;
+        unsigned *rows = nullptr;
+        int *cs = nullptr;
+        TSP_TRY(tsp_tile_pretreatment(c.m, th, &n, &rows, &cs));
+        std::pair<std::vector<unsigned>, std::vector<int>> e;
+        e.first.assign(rows, rows + n);
+        e.second.assign(cs, cs + n + 1);
+        free(rows);
+        free(cs);
+        it = c.cache.emplace(th, std::move(e)).first;
+    }
+    const int n = (int)it->second.first.size();
+    if (n > c.cap_tasks) return TSP_EINVAL;
+    TSP_TRY(tsp_memcpy_h2d(c.d_rows, it->second.first.data(), sizeof(unsigned) * (size_t)n));
+    TSP_TRY(tsp_memcpy_h2d(c.d_colstart, it->second.second.data(), sizeof(int) * ((size_t)n + 1)));
+    c.th = th;
+    c.ntasks = n;
+    // Mirror the schedule into the tile matrix, as update_metadata does.
+    free(c.m->blkcoostylerowidx);
+    free(c.m->blkcoostylerowidx_colstart);
+    c.m->blkcoostylerowidx = tsph::alloc_n<unsigned>((size_t)n);
+    c.m->blkcoostylerowidx_colstart = tsph::alloc_n<int>((size_t)n + 1);
+    memcpy(c.m->blkcoostylerowidx, it->second.first.data(), sizeof(unsigned) * (size_t)n);
+    memcpy(c.m->blkcoostylerowidx_colstart, it->second.second.data(), sizeof(int) * ((size_t)n + 1));
+    c.m->rowblkblock = n;
+    (void)p;
+    return TSP_OK;
+}
+
+static int launch_class(tsp_plan *p, ClassDev &c)
+{
+    if (!c.active() || c.ntasks == 0) return TSP_OK;
+    return tsp_spmm_launch(c.bm, p->prec, c.ntasks, p->colB_p, c.d_val, c.d_rows, c.d_colstart,
+                           p->d_B, p->d_C, c.d_colidx, p->rowA, c.stream);
+}
+
+extern "C" int tsp_plan_destroy(tsp_plan *p)
+{
+    if (!p) return TSP_OK;
+    for (ClassDev &c : p->cls) {
+        tsp_free(c.d_val);
+        tsp_free(c.d_colidx);
+        tsp_free(c.d_rows);
+        tsp_free(c.d_colstart);
+        tsp_stream_destroy(c.stream);
+    }
+    tsp_free(p->d_B);
+    tsp_free(p->d_C);
+    tsp_event_destroy(p->ev0);
+    tsp_event_destroy(p->ev1);
+    delete p;
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_create(tsp_plan **out, int device_id, Tile_matrix *m64, Tile_matrix *m16,
+                               Tile_matrix *m8, int rowA, int colA, int colB_p, int prec,
+                               const void *h_B)
+{
+    if (!out || rowA < 0 || colA < 0 || (prec != 0 && prec != 1)) return TSP_EINVAL;
+    if (colB_p != 32 && (colB_p <= 0 || colB_p % 64)) return TSP_EINVAL;
+    *out = nullptr;
+    TSP_TRY(tsp_device_init(device_id));
+    std::unique_ptr<tsp_plan> p(new tsp_plan);
+    p->dev = device_id;
+    p->prec = prec;
+    p->rowA = rowA;
+    p->colA = colA;
+    p->colB_p = colB_p;
+    const size_t vs = tsph::val_size(prec);
+    Tile_matrix *ms[3] = {m64, m16, m8};
+    const int bms[3] = {64, 16, 8};
+    int st = TSP_OK;
+    auto fail = [&](int s) { tsp_plan_destroy(p.release()); return s; };
+    const size_t bbytes = vs * (size_t)colA * colB_p, cbytes = sizeof(float) * (size_t)rowA * colB_p;
+    if ((st = tsp_malloc(&p->d_B, bbytes))) return fail(st);
+    if ((st = tsp_malloc((void **)&p->d_C, cbytes))) return fail(st);
+    if (h_B && (st = tsp_memcpy_h2d(p->d_B, h_B, bbytes))) return fail(st);
+    if ((st = tsp_memset(p->d_C, 0, cbytes))) return fail(st);
+    for (int i = 0; i < 3; ++i) {
+        ClassDev &c = p->cls[i];
+        c.m = ms[i];
+        c.bm = bms[i];
+        if (!c.active()) continue;
+        if (c.m->bm != bms[i] || c.m->prec != prec || c.m->bn != tsp_tile_bn(bms[i], prec)) return fail(TSP_EINVAL);
+        const size_t nt = (size_t)c.m->tilenum;
+        if ((st = tsp_malloc(&c.d_val, vs * c.m->dnssize))) return fail(st);
+        if ((st = tsp_memcpy_h2d(c.d_val, c.m->Blockdense_Val, vs * c.m->dnssize))) return fail(st);
+        if ((st = tsp_malloc((void **)&c.d_colidx, sizeof(int) * nt * c.m->bn))) return fail(st);
+        if ((st = tsp_memcpy_h2d(c.d_colidx, c.m->tile_colidx, sizeof(int) * nt * c.m->bn))) return fail(st);
+        c.cap_tasks = (long long)c.m->tilem + c.m->tilenum;
+        if ((st = tsp_malloc((void **)&c.d_rows, sizeof(unsigned) * (size_t)c.cap_tasks))) return fail(st);
+        if ((st = tsp_malloc((void **)&c.d_colstart, sizeof(int) * ((size_t)c.cap_tasks + 1)))) return fail(st);
+        if ((st = tsp_stream_create(&c.stream))) return fail(st);
+    }
+    if ((st = tsp_event_create(&p->ev0))) return fail(st);
+    if ((st = tsp_event_create(&p->ev1))) return fail(st);
+    *out = p.release();
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_set_th(tsp_plan *p, int th64, int th16, int th8)
+{
+    if (!p) return TSP_EINVAL;
+    const int th[3] = {th64, th16, th8};
+    for (int i = 0; i < 3; ++i) {
+        ClassDev &c = p->cls[i];
+        if (!c.active() || th[i] <= 0) continue;
+        TSP_TRY(upload_schedule(p, c, th[i]));
+    }
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_run(tsp_plan *p, int zero_c)
+{
+    if (!p) return TSP_EINVAL;
+    if (zero_c) TSP_TRY(tsp_memset(p->d_C, 0, sizeof(float) * (size_t)p->rowA * p->colB_p));
+    for (ClassDev &c : p->cls) TSP_TRY(launch_class(p, c));
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_time(tsp_plan *p, int reps, double *ms)
+{
+    if (!p || reps <= 0 || !ms) return TSP_EINVAL;
+    TSP_TRY(tsp_event_record(p->ev0, nullptr));
+    for (int r = 0; r < reps; ++r) TSP_TRY(tsp_plan_run(p, 0));
+    TSP_TRY(tsp_event_record(p->ev1, nullptr));
+    TSP_TRY(tsp_event_sync(p->ev1));
+    float t = 0.f;
+    TSP_TRY(tsp_event_elapsed_ms(&t, p->ev0, p->ev1));
+    *ms = (double)t / reps;
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_time_class(tsp_plan *p, int bm, int reps, double *ms)
+{
+    if (!p || reps <= 0 || !ms) return TSP_EINVAL;
+    ClassDev *c = nullptr;
+    for (ClassDev &x : p->cls)
+        if (x.bm == bm) c = &x;
+    if (!c || !c->active()) { *ms = 0.0; return TSP_OK; }
+    TSP_TRY(tsp_event_record(p->ev0, c->stream));
+    for (int r = 0; r < reps; ++r) TSP_TRY(launch_class(p, *c));
+    TSP_TRY(tsp_event_record(p->ev1, c->stream));
+    TSP_TRY(tsp_event_sync(p->ev1));
+    float t = 0.f;
+    TSP_TRY(tsp_event_elapsed_ms(&t, p->ev0, p->ev1));
+    *ms = (double)t / reps;
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_warmup(tsp_plan *p, int iters)
+{
+    if (!p) return TSP_EINVAL;
+    for (int i = 0; i < iters; ++i) TSP_TRY(tsp_plan_run(p, 0));
+    return tsp_device_sync();
+}
+
+extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model_ms, double *tune_ms)
+{
+    if (!p) return TSP_EINVAL;
+    const double t0 = now_ms();
+    std::vector<int> opts[3];
+    for (int i = 0; i < 3; ++i) {
+        ClassDev &c = p->cls[i];
+        if (!c.active()) { opts[i].push_back(0); continue; }
+        tsp_th_params prm;
+        TSP_TRY(tsp_th_params_probe(p->dev, c.bm, p->prec, p->colB_p, &prm));
+        int top4[4];
+        if (tsp_optimal_th(c.bm, p->colB_p, c.m->tilem, c.m->tile_ptr, &prm, top4) < 0) return TSP_EINVAL;
+        for (int k = 0; k < 4; ++k) {
+            bool dup = false;
+            for (int v : opts[i]) dup |= v == top4[k];
+            if (!dup) opts[i].push_back(top4[k]);
+        }
+    }
+    const double t1 = now_ms();
+    if (model_ms) *model_ms = t1 - t0;
+    int best[3] = {opts[0][0], opts[1][0], opts[2][0]};
+    TSP_TRY(tsp_plan_set_th(p, best[0], best[1], best[2]));
+    double t2 = now_ms(), t3 = t2;
+    const size_t combos = opts[0].size() * opts[1].size() * opts[2].size();
+    if (tune && combos > 1) {
+        double best_ms = 1e30;
+        for (int a : opts[0])
+            for (int b : opts[1])
+                for (int c : opts[2]) {
+                    TSP_TRY(tsp_plan_set_th(p, a, b, c));
+                    for (int w = 0; w < 5; ++w) TSP_TRY(tsp_plan_run(p, 0));
+                    double ms = 0;
+                    TSP_TRY(tsp_plan_time(p, 10, &ms));
+                    if (ms < best_ms) {
+                        best_ms = ms;
+                        best[0] = a; best[1] = b; best[2] = c;
+                    }
+                }
+        t3 = now_ms();
+        TSP_TRY(tsp_plan_set_th(p, best[0], best[1], best[2]));
+    }
+    if (tune_ms) *tune_ms = t3 - t2;
+    if (th_out) for (int i = 0; i < 3; ++i) th_out[i] = best[i];
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_download_c(tsp_plan *p, float *h_C)
+{
+    if (!p || !h_C) return TSP_EINVAL;
+    TSP_TRY(tsp_device_sync());
+    return tsp_memcpy_d2h(h_C, p->d_C, sizeof(float) * (size_t)p->rowA * p->colB_p);
+}
+
+extern "C" int tsp_plan_device_c(tsp_plan *p, float **d_C)
+{
+    if (!p || !d_C) return TSP_EINVAL;
+    *d_C = p->d_C;
+    return TSP_OK;
+}
+
+extern "C" int tsp_call_tilespmm(int device_id, Tile_matrix *m64, Tile_matrix *m16, Tile_matrix *m8,
+                                 int rowA, int colA, int colB_p, long long total_nnz, int prec,
+                                 const void *h_B, float *h_C, double cpu_pre_ms, int logical_colB,
+                                 int repeat, int tune, FILE *csv, tsp_run_result *out)
+{
+    tsp_plan *p = nullptr;
+    TSP_TRY(tsp_plan_create(&p, device_id, m64, m16, m8, rowA, colA, colB_p, prec, h_B));
+    std::unique_ptr<tsp_plan, int (*)(tsp_plan *)> guard(p, tsp_plan_destroy);
+    int th[3];
+    double model_ms = 0, tune_ms = 0;
+    TSP_TRY(tsp_plan_tune(p, tune, th, &model_ms, &tune_ms));
+    TSP_TRY(tsp_plan_warmup(p, 100));
+    TSP_TRY(tsp_plan_run(p, 1));
+    if (h_C) TSP_TRY(tsp_plan_download_c(p, h_C));
+    TSP_TRY(tsp_plan_warmup(p, 100));
+    TSP_TRY(tsp_plan_run(p, 1));
+    double ms = 0;
+    TSP_TRY(tsp_plan_time(p, repeat > 0 ? repeat : 1000, &ms));
+    const double tflops = 2.0 * (double)total_nnz * 1.0e-6 / ms * logical_colB / 1000.0;
+    const double pre = cpu_pre_ms + model_ms + tune_ms;
+    if (csv) {
+        fprintf(csv, "%d,%d,%d,%.9g,%.9g,%.9g,", th[0], th[1], th[2], pre, ms, tflops);
+        fflush(csv);
+    }
+    if (out) {
+        out->th64 = th[0]; out->th16 = th[1]; out->th8 = th[2];
+        out->pre_time_ms = pre;
+        out->time_ms = ms;
+        out->tflops = tflops;
+        out->model_ms = model_ms;
+        out->tune_ms = tune_ms;
+    }
+    return TSP_OK;
+}
