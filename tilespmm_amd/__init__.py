@@ -185,7 +185,7 @@ HOST_SYMBOLS = {
                                   C.POINTER(Tile_matrix), C.POINTER(Tile_matrix), C.c_int, C.c_int,
                                   C.c_int, C.c_int, _P]),
     "tsp_plan_set_th": (C.c_int, [_P, C.c_int, C.c_int, C.c_int]),
-    "tsp_plan_tune": (C.c_int, [_P, C.c_int, _IP, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "tsp_plan_tune": (C.c_int, [_P, C.c_int, _P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "tsp_plan_run": (C.c_int, [_P, C.c_int]),
     "tsp_plan_warmup": (C.c_int, [_P, C.c_int]),
     "tsp_plan_time": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double)]),
