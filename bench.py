@@ -35,6 +35,34 @@ def alg_bytes(rows, nnz, s_a, k_rows, n, s_b):
     return 4 * (rows + 1) + nnz * (4 + s_a) + k_rows * n * s_b + rows * n * 4
 
 
+def copy_calibration(hip, nbytes, reps):
+    """Plain 16-byte-vector copy of nbytes (dst = src): its FETCH_SIZE /
+    WRITE_SIZE per dispatch calibrate the HBM byte counters, its time gives the
+    achievable copy bandwidth."""
+    import ctypes as C
+    nbytes = (nbytes + 15) // 16 * 16
+    src, dst = C.c_void_p(), C.c_void_p()
+    assert hip.tsp_malloc(C.byref(src), nbytes) == 0 and hip.tsp_malloc(C.byref(dst), nbytes) == 0
+    hip.tsp_memset(src, 1, nbytes)
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    hip.tsp_event_create(C.byref(e0))
+    hip.tsp_event_create(C.byref(e1))
+    for _ in range(3):
+        hip.tsp_copy_kernel(dst, src, nbytes, None)
+    hip.tsp_event_record(e0, None)
+    for _ in range(reps):
+        hip.tsp_copy_kernel(dst, src, nbytes, None)
+    hip.tsp_event_record(e1, None)
+    hip.tsp_event_sync(e1)
+    ms = C.c_float()
+    hip.tsp_event_elapsed_ms(C.byref(ms), e0, e1)
+    t = ms.value / reps
+    print(json.dumps({"copy_bytes": nbytes, "ms": round(t, 5),
+                      "gbs_read_plus_write": round(2 * nbytes / (t * 1e-3) / 1e9, 1)}), flush=True)
+    hip.tsp_free(src)
+    hip.tsp_free(dst)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -49,6 +77,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-vendor", action="store_true")
     ap.add_argument("--class-reps", type=int, default=200)
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="only run the plain copy kernel on this many bytes (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -59,6 +89,9 @@ def main():
     hip, host = tsp.load()
     if not tsp.device_available():
         raise SystemExit("bench.py: no gfx950 device")
+    if args.copy_bytes:
+        copy_calibration(hip, args.copy_bytes, args.steps)
+        return
 
     prec = {"fp16": 0, "tf32": 1, None: -1}[args.prec]
     t0 = time.time()
