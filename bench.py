@@ -63,6 +63,29 @@ def copy_calibration(hip, nbytes, reps):
     hip.tsp_free(dst)
 
 
+def sweep(plan, tiles, cbp, args):
+    """Time every kernel variant (chunk width W, pipeline stages S, tasks per
+    wave) of each active class; one JSON line per class."""
+    for t, bm in zip(tiles, (64, 16, 8)):
+        if t.tilenum == 0:
+            continue
+        widths = [w for w in ((32, 64) if bm == 64 else (32, 64, 128)) if cbp % w == 0]
+        res = {}
+        plan.set_variant(bm)
+        res["default"] = plan.time_class(bm, args.class_reps)
+        for w in widths:
+            for s in (1, 2, 3, 4):
+                for tpw in (1, 4, 16, 0):
+                    plan.set_variant(bm, w, s, tpw)
+                    plan.time_class(bm, 3)
+                    res[f"w{w}_s{s}_t{tpw}"] = plan.time_class(bm, args.class_reps)
+        plan.set_variant(bm)
+        best = min(res, key=res.get)
+        print(json.dumps({"sweep": args.config, "bm": bm, "tiles": t.tilenum, "best": best,
+                          "best_ms": round(res[best], 5), "default_ms": round(res["default"], 5),
+                          "ms": {k: round(v, 5) for k, v in res.items()}}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -77,6 +100,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-vendor", action="store_true")
     ap.add_argument("--class-reps", type=int, default=200)
+    ap.add_argument("--sweep", action="store_true", help="time every kernel variant per class instead")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run the plain copy kernel on this many bytes (counter calibration)")
     args = ap.parse_args()
@@ -115,6 +139,11 @@ def main():
     plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
     th, model_ms, tune_ms = plan.tune(not args.no_tune)
     log(f"thresholds {th} (model {model_ms:.1f} ms, tuning {tune_ms:.1f} ms)")
+
+    if args.sweep:
+        sweep(plan, tiles, cbp, args)
+        plan.close()
+        return
 
     # warmup, then K timed steps bracketed by device syncs and null-stream events
     plan.warmup(args.warmup)

@@ -97,6 +97,10 @@ int tsp_event_destroy(void *event);
 int tsp_event_record(void *event, void *stream);   /* stream NULL = null stream */
 int tsp_event_sync(void *event);
 int tsp_event_elapsed_ms(float *ms, void *start, void *stop);
+/* Non-blocking stream (no implicit ordering with the null stream) and an
+ * explicit stream -> event dependency, used to join class streams. */
+int tsp_stream_create_nonblocking(void **stream);
+int tsp_stream_wait_event(void *stream, void *event);
 
 /* Tile SpMM launch, one row-block class:
  *   C[rows of task][cols] (=, or += atomically for split tasks)
@@ -111,6 +115,17 @@ int tsp_spmm_launch(int bm, int prec, int rowblkblock, int colB_p,
                     const void *d_val, const unsigned *d_rows, const int *d_colstart,
                     const void *d_B, float *d_C, const int *d_colidx,
                     int c_rows, void *stream);
+
+/* Same launch with an explicit kernel variant, for tuning drivers: chunk
+ * width w (output columns per wave: 32, 64 or 128; 64-row tiles 32 or 64),
+ * software-pipeline depth stages (1-4 tiles in flight per wave) and
+ * tasks_per_wave (consecutive tasks one wave streams).  Values <= 0 pick the
+ * defaults tsp_spmm_launch uses.  No counterpart in the reference (its
+ * kernels have one fixed shape per class). */
+int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p,
+                            const void *d_val, const unsigned *d_rows, const int *d_colstart,
+                            const void *d_B, float *d_C, const int *d_colidx,
+                            int c_rows, void *stream, int w, int stages, int tasks_per_wave);
 
 /* Per-class entry points with the reference dispatcher names
  * (src/tilespmm_cuda.h:1634, :1672, :1710) and argument order. */

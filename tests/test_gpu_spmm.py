@@ -113,6 +113,34 @@ def test_random_all_classes(gpu, orc, prec, colB):
 
 
 @pytest.mark.parametrize("prec", [0, 1])
+def test_every_kernel_variant(gpu, orc, prec):
+    """Every (chunk width, pipeline depth, tasks per wave) variant of every
+    class gives the oracle's result, split tasks included."""
+    tsp = gpu
+    rng = np.random.default_rng(50 + prec)
+    A = random_matrix(tsp, rng, 611, 509, 45, prec, heavy_rows=4)
+    colB = 128
+    B, cbp = random_b(tsp, rng, A.cols, colB, prec)
+    Cref, Cabs = reference(orc, A, B, colB)
+    for g, d, bm in [(0.0, 1.5, 64), (5.0, 0.0, 16), (5.0, 3.0, 8)]:
+        subs = tsp.matrix_split(A, g, d)
+        tiles = [tsp.tile_create(s, A.cols, b, prec) for s, b in zip(subs, (64, 16, 8))]
+        plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
+        try:
+            plan.set_th(8, 8, 8)
+            for w in ((32, 64) if bm == 64 else (32, 64, 128)):
+                for s in (1, 2, 3, 4):
+                    for tpw in (1, 3, 0):
+                        say(f"variant prec={prec} bm={bm} w={w} s={s} tpw={tpw}")
+                        plan.set_variant(bm, w, s, tpw)
+                        plan.run(zero_c=True)
+                        Cg = plan.download_c()
+                        assert_close(Cg[:, :colB], Cref, Cabs, prec, f"bm={bm} w={w} s={s} tpw={tpw}")
+        finally:
+            plan.close()
+
+
+@pytest.mark.parametrize("prec", [0, 1])
 @pytest.mark.parametrize("colB", [32, 128])
 def test_cli_integer_stream_dc2_exact(gpu, orc, dc2_path, prec, colB):
     """The reference CLI's inputs on its shipped matrix: exact integers."""
@@ -133,6 +161,25 @@ def test_cli_integer_stream_dc2_exact(gpu, orc, dc2_path, prec, colB):
         say(f"dc2 prec={prec} colB={colB} gamma={g} delta={d}")
         Cg, _ = run_tiles(tsp, A, B, cbp, g, d, th=(16, 16, 16))
         assert np.array_equal(Cg[:, :colB].astype(np.float64), Cref)
+
+
+@pytest.mark.parametrize("exe", ["tilespmm_fp16", "tilespmm_tf32"])
+@pytest.mark.parametrize("colB", [32, 128])
+def test_cli_end_to_end(gpu, dc2_path, tmp_path, exe, colB):
+    """The reference's test.sh run: CLI on dc2, check passes, 19-field CSV row."""
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    binary = os.path.join(root, "tilespmm_amd", "bin", exe)
+    say(f"cli {exe} colB={colB}")
+    r = subprocess.run([binary, "-d", "0", dc2_path, str(colB)], cwd=tmp_path, capture_output=True, text=True,
+                       timeout=240)
+    assert r.returncode == 0, r.stderr
+    assert "Check... PASS!" in r.stdout, r.stdout[-2000:]
+    csv = tmp_path / ("TileSpMM-FP16.csv" if exe.endswith("fp16") else "TileSpMM-TF32.csv")
+    fields = csv.read_text().strip().split(",")
+    assert len(fields) == 19 and fields[0] == dc2_path
+    assert int(fields[1]) == 116835 and int(fields[3]) == 766396 and int(fields[4]) == colB
+    assert all(float(x) > 0 for x in (fields[14], fields[15], fields[17], fields[18]))
 
 
 def test_direct_kernel_boundary(gpu, orc):

@@ -143,8 +143,12 @@ HIP_SYMBOLS = {
     "tsp_event_record": (C.c_int, [_P, _P]),
     "tsp_event_sync": (C.c_int, [_P]),
     "tsp_event_elapsed_ms": (C.c_int, [C.POINTER(C.c_float), _P, _P]),
+    "tsp_stream_create_nonblocking": (C.c_int, [C.POINTER(C.c_void_p)]),
+    "tsp_stream_wait_event": (C.c_int, [_P, _P]),
     "tsp_spmm_launch": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P,
                                   C.c_int, _P]),
+    "tsp_spmm_launch_variant": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P,
+                                          C.c_int, _P, C.c_int, C.c_int, C.c_int]),
     "tsp_switch_v64": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v16": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v8": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
@@ -186,6 +190,7 @@ HOST_SYMBOLS = {
                                   C.c_int, C.c_int, _P]),
     "tsp_plan_set_th": (C.c_int, [_P, C.c_int, C.c_int, C.c_int]),
     "tsp_plan_tune": (C.c_int, [_P, C.c_int, _P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "tsp_plan_set_variant": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.c_int]),
     "tsp_plan_run": (C.c_int, [_P, C.c_int]),
     "tsp_plan_warmup": (C.c_int, [_P, C.c_int]),
     "tsp_plan_time": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double)]),
@@ -489,6 +494,9 @@ class Plan:
         mm, tm = C.c_double(), C.c_double()
         _check("tsp_plan_tune", load()[1].tsp_plan_tune(self.p, int(tune), _ptr(th), C.byref(mm), C.byref(tm)))
         return tuple(int(x) for x in th), mm.value, tm.value
+
+    def set_variant(self, bm: int, w: int = 0, stages: int = 0, tasks_per_wave: int = 0):
+        _check("tsp_plan_set_variant", load()[1].tsp_plan_set_variant(self.p, bm, w, stages, tasks_per_wave))
 
     def run(self, zero_c: bool = True):
         _check("tsp_plan_run", load()[1].tsp_plan_run(self.p, int(zero_c)))

@@ -70,8 +70,8 @@ int tsp_kernel_probe(int bm, int prec, int colB_p, tsp_kernel_info *out)
 {
     if (!out || (bm != 64 && bm != 16 && bm != 8) || (prec != 0 && prec != 1)) return TSP_EINVAL;
     if (colB_p != 32 && (colB_p <= 0 || colB_p % 64)) return TSP_EINVAL;
-    const int w = tsp::chunk_width(bm, colB_p);
-    const void *k = tsp::select_kernel(bm, prec, w);
+    const int w = tsp::default_chunk_width(bm, colB_p);
+    const void *k = tsp::select_kernel(bm, prec, w, tsp::default_stages(bm, prec, w));
     if (!k) return TSP_EINVAL;
     hipFuncAttributes a;
     hipError_t e = hipFuncGetAttributes(&a, k);
@@ -141,6 +141,18 @@ int tsp_event_record(void *event, void *stream)
     return (int)hipEventRecord((hipEvent_t)event, (hipStream_t)stream);
 }
 int tsp_event_sync(void *event) { return (int)hipEventSynchronize((hipEvent_t)event); }
+int tsp_stream_create_nonblocking(void **stream)
+{
+    if (!stream) return TSP_EINVAL;
+    hipStream_t s = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    *stream = (void *)s;
+    return (int)e;
+}
+int tsp_stream_wait_event(void *stream, void *event)
+{
+    return (int)hipStreamWaitEvent((hipStream_t)stream, (hipEvent_t)event, 0);
+}
 int tsp_event_elapsed_ms(float *ms, void *start, void *stop)
 {
     if (!ms) return TSP_EINVAL;
@@ -158,7 +170,23 @@ int tsp_spmm_launch(int bm, int prec, int rowblkblock, int colB_p, const void *d
     if (rowblkblock == 0) return TSP_OK;
     if (!d_val || !d_rows || !d_colstart || !d_B || !d_C || !d_colidx) return TSP_EINVAL;
     return tsp::launch(bm, prec, rowblkblock, colB_p, d_val, d_rows, d_colstart, d_B, d_C,
-                       d_colidx, c_rows, (hipStream_t)stream);
+                       d_colidx, c_rows, (hipStream_t)stream, 0, 0, 0);
+}
+
+int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
+                            const unsigned *d_rows, const int *d_colstart, const void *d_B,
+                            float *d_C, const int *d_colidx, int c_rows, void *stream, int w,
+                            int stages, int tasks_per_wave)
+{
+    if (bm != 64 && bm != 16 && bm != 8) return TSP_EINVAL;
+    if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
+    if (colB_p != 32 && (colB_p <= 0 || colB_p % 64 != 0)) return TSP_EINVAL;
+    if (rowblkblock < 0 || c_rows < 0) return TSP_EINVAL;
+    if (w > 0 && (colB_p % w != 0 || !tsp::valid_variant(bm, w, stages > 0 ? stages : 1))) return TSP_EINVAL;
+    if (rowblkblock == 0) return TSP_OK;
+    if (!d_val || !d_rows || !d_colstart || !d_B || !d_C || !d_colidx) return TSP_EINVAL;
+    return tsp::launch(bm, prec, rowblkblock, colB_p, d_val, d_rows, d_colstart, d_B, d_C,
+                       d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave);
 }
 
 int tsp_switch_v64(int prec, int rowblkblock, int colB_p, const void *d_val, const unsigned *d_rows,

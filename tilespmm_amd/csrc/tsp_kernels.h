@@ -16,11 +16,16 @@ constexpr __host__ __device__ int tile_bn(int bm, int prec)
     return prec == 0 ? (bm == 64 ? 32 : 16) : (bm == 64 ? 16 : 8);
 }
 
-int chunk_width(int bm, int colB_p);
-const void *select_kernel(int bm, int prec, int w);
+// Kernel variant = (chunk width W, pipeline stages S, tasks per wave).
+int default_chunk_width(int bm, int colB_p);
+int default_stages(int bm, int prec, int w);
+int default_tasks_per_wave(int ntasks, int nchunks);
+bool valid_variant(int bm, int w, int s);
+const void *select_kernel(int bm, int prec, int w, int s);
+// w, s, tpw <= 0 select the defaults.
 int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const unsigned *rows,
            const int *colstart, const void *B, float *C, const int *colidx, int c_rows,
-           hipStream_t s);
+           hipStream_t st, int w, int s, int tpw);
 int launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
 
 }  // namespace tsp

@@ -7,11 +7,19 @@
 // which is what the reference's stir_spmm_cuda_kernel_v{8,16,64}[_tf32][_32]
 // compute (src/tilespmm_cuda.h:12-1632).  The design is CDNA4-first, not a
 // translation:
-//   * one wave64 owns one (task, column chunk of W columns); a 256-thread
-//     block runs four independent waves, so no block barrier exists at all;
-//   * the gathered B row panel (BN rows x W columns) is loaded with 16-byte
-//     vector loads and staged in a wave-private LDS slice; one wave's LDS
-//     operations execute in issue order, so a single buffer is safe;
+//   * a wave64 owns a contiguous RANGE of tasks for one column chunk of W
+//     columns.  The tiles of consecutive tasks are contiguous in memory, so
+//     the wave streams them through one software pipeline that never drains
+//     at task boundaries; at a boundary it only flushes its accumulators to C
+//     (plain stores, or fp32 atomics for split tasks) and clears them.  A
+//     256-thread block runs four independent waves: there is no block barrier;
+//   * S tiles are in flight per wave: the B row panel (BN rows x W columns,
+//     16-byte vector loads) and the A fragment of tile t+S are loaded while
+//     tile t is computed, and the column indices of tile t+S+1 one step
+//     earlier still (they feed the B addresses);
+//   * the B panel is staged in a wave-private LDS slice (one wave's LDS
+//     operations execute in issue order, so one buffer is safe) and read back
+//     in MFMA operand order;
 //   * A tiles are canonical row-major BM x BN blocks read straight into MFMA
 //     operand registers (8 or 16 bytes per lane);
 //   * fp16: v_mfma_f32_16x16x16_f16 (BN = 16) and v_mfma_f32_16x16x32_f16
@@ -21,10 +29,8 @@
 //     registers and multiplied with v_mfma_f32_16x16x4_f32 -- a tf32 product
 //     is exact in fp32, so this is tf32 arithmetic with fp32 accumulate
 //     (CDNA4 has no xf32 MFMA);
-//   * the column indices of tile t+1 are loaded while tile t is computed, the
-//     B panel and A fragment of tile t+1 are in flight during tile t's MFMAs;
-//   * block ids are remapped so that consecutive tasks (which tend to share B
-//     rows) run on the same XCD and share its L2.
+//   * block ids are remapped so that consecutive task ranges (which tend to
+//     share B rows) run on the same XCD and share its L2.
 //
 // The MFMA K index of (lane group q = lane/16, operand element j) is a free
 // permutation as long as A and B use the same one; this file uses
@@ -44,7 +50,6 @@ namespace tsp {
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
-typedef float f2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
@@ -53,9 +58,17 @@ __device__ __forceinline__ uint32_t round_tf32_bits(uint32_t x)
     return (x + 0xfffu + ((x >> 13) & 1u)) & 0xffffe000u;
 }
 
-__device__ __forceinline__ float round_tf32(float f)
+// Wave-uniform read-only data (schedule, column indices) is read through the
+// constant address space so the loads become scalar (SMEM) loads into SGPRs:
+// they are counted by lgkmcnt and never make a wave wait on its in-flight
+// vector loads.
+template <typename T>
+using cptr = const __attribute__((address_space(4))) T *;
+
+template <typename T>
+__device__ __forceinline__ T uload(const T *p, size_t i)
 {
-    return __uint_as_float(round_tf32_bits(__float_as_uint(f)));
+    return ((cptr<T>)p)[i];
 }
 
 // Block id -> logical block id such that each XCD (blocks are dealt to the 8
@@ -67,11 +80,12 @@ __device__ __forceinline__ int xcd_remap(int b, int nb)
     return x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
 }
 
-template <int BM, int W, int PREC>
+template <int BM, int W, int PREC, int S>
 __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
-    int ntasks, int nchunks, const void *__restrict__ val_, const unsigned *__restrict__ rows,
-    const int *__restrict__ colstart, const void *__restrict__ B_, float *__restrict__ C,
-    const int *__restrict__ colidx, int ld, int c_rows)
+    int ntasks, int nchunks, int tasks_per_wave, const void *__restrict__ val_,
+    const unsigned *__restrict__ rows, const int *__restrict__ colstart,
+    const void *__restrict__ B_, float *__restrict__ C, const int *__restrict__ colidx, int ld,
+    int c_rows)
 {
     constexpr bool F16 = PREC == TSP_PREC_FP16;
     constexpr int BN = tile_bn(BM, PREC);
@@ -83,22 +97,26 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     constexpr int RG = BM >= 16 ? BM / 16 : 1;   // 16-row MFMA row groups
     constexpr int CB = W / 16;                   // 16-column MFMA blocks
     constexpr int KS = F16 ? 1 : BN / 4;         // tf32 MFMA steps per tile
+    constexpr int AW = F16 ? (BN == 32 ? 4 : 2) : KS;   // A words per row group
     using VT = typename std::conditional<F16, _Float16, float>::type;
 
     __shared__ __attribute__((aligned(16))) VT lds_all[kWavesPerBlock][BN * LDSW];
 
     const int lane = threadIdx.x & 63;
-    const int wid = threadIdx.x >> 6;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform per wave
     const int lb = xcd_remap(blockIdx.x, gridDim.x);
     const long long gw = (long long)lb * kWavesPerBlock + wid;
-    if (gw >= (long long)ntasks * nchunks) return;
-    const int task = (int)(gw / nchunks);
-    const int chunk = (int)(gw - (long long)task * nchunks);
-    const int ts = colstart[task], te = colstart[task + 1];
-    if (ts >= te) return;
-    const unsigned rw = rows[task];
-    const bool split = (rw & 0x80000000u) != 0;
-    const int row0 = (int)(rw & 0x7fffffffu);
+    const long long nranges = ((long long)ntasks + tasks_per_wave - 1) / tasks_per_wave;
+    if (gw >= nranges * nchunks) return;
+    const int range = (int)(gw / nchunks);
+    const int chunk = (int)(gw - (long long)range * nchunks);
+    const int k0 = range * tasks_per_wave;
+    const int k1 = min(ntasks, k0 + tasks_per_wave);
+    const int tb = uload(colstart, k0), te = uload(colstart, k1);
+    if (tb >= te) return;                        // every task of the range is empty
+    int k = k0;
+    int kend = uload(colstart, k0 + 1);
+    while (kend <= tb) kend = uload(colstart, ++k + 1);  // skip leading empty tasks
     const int col0 = chunk * W;
 
     VT *lds = lds_all[wid];
@@ -107,7 +125,6 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     const int ln = lane & 15;        // MFMA row (A) / column (B, D) index
     const int lq = lane >> 4;        // MFMA lane group
 
-    // Per-lane geometry of the B panel vectors.
     int prow[NV], pcol[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
@@ -121,11 +138,6 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     for (int g = 0; g < RG; ++g)
 #pragma unroll
         for (int c = 0; c < CB; ++c) acc[g][c] = f4{0.f, 0.f, 0.f, 0.f};
-
-    // A operand registers: fp16 -> 4 halves (BN=16) or 8 halves (BN=32) per
-    // row group; tf32 -> KS floats per row group.
-    constexpr int AW = F16 ? (BN == 32 ? 4 : 2) : KS;   // 32-bit words per row group
-    uint32_t areg[RG][AW];
 
     auto load_a = [&](int t, uint32_t (&dst)[RG][AW]) {
         const VT *tile = val + (size_t)t * (BM * BN);
@@ -157,32 +169,93 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
             }
         }
     };
-
-    int cid[NV];
-    u4 bv[NV];
-    auto load_cid = [&](int t) {
-#pragma unroll
-        for (int i = 0; i < NV; ++i) cid[i] = colidx[(size_t)t * BN + prow[i]];
-    };
-    auto load_b = [&]() {
+    // Column indices are wave-uniform: read them with scalar loads (counted
+    // by lgkmcnt, so waiting for them never waits for the vector loads of
+    // the B/A ring), then each lane picks the index of its panel row.
+    constexpr int RPI = 64 / VPR;                // panel rows one vector instruction covers
+    const int lrow = lane / VPR;
+    using CSV = int __attribute__((ext_vector_type(BN)));
+    auto load_cs = [&](int t, CSV &cs) { cs = *(cptr<CSV>)(colidx + (size_t)t * BN); };
+    auto select_cid = [&](const CSV &cs, int (&dst)[NV]) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const char *p = Bb + ((size_t)cid[i] * ld + col0 + pcol[i]) * sizeof(VT);
-            bv[i] = *(const u4 *)p;
+            int v = cs[i * RPI];
+#pragma unroll
+            for (int r = 1; r < RPI; ++r) v = lrow == r ? cs[i * RPI + r] : v;
+            dst[i] = v;
         }
     };
-
-    // Prologue: tile ts in flight, column indices of ts+1 in flight.
-    load_cid(ts);
-    load_b();
-    load_a(ts, areg);
-    if (ts + 1 < te) load_cid(ts + 1);
-
-    for (int t = ts; t < te; ++t) {
-        // Stage tile t's B panel in LDS (tf32 operands rounded on the way).
+    auto load_b = [&](const int (&cid)[NV], u4 (&dst)[NV]) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            dst[i] = *(const u4 *)(Bb + ((size_t)cid[i] * ld + col0 + pcol[i]) * sizeof(VT));
+    };
+    auto flush = [&](int task) {
+        const unsigned rw = uload(rows, task);
+        const bool split = (rw & 0x80000000u) != 0;
+        const int row0 = (int)(rw & 0x7fffffffu);
+#pragma unroll
+        for (int g = 0; g < RG; ++g) {
+            if (BM == 8 && lq >= 2) break;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int r = row0 + 16 * g + 4 * lq + j;
+                if (r >= c_rows) continue;
+                float *crow = C + (size_t)r * ld + col0 + ln;
+#pragma unroll
+                for (int c = 0; c < CB; ++c) {
+                    if (split) unsafeAtomicAdd(crow + 16 * c, acc[g][c][j]);
+                    else __builtin_nontemporal_store(acc[g][c][j], crow + 16 * c);
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < RG; ++g)
+#pragma unroll
+            for (int c = 0; c < CB; ++c) acc[g][c] = f4{0.f, 0.f, 0.f, 0.f};
+    };
+    auto compute = [&](const uint32_t (&a)[RG][AW]) {
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+            const int col = 16 * c + ln;
+            if constexpr (F16) {
+                if constexpr (BN == 16) {
+                    h4 b;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) b[j] = lds[(4 * lq + j) * LDSW + col];
+#pragma unroll
+                    for (int g = 0; g < RG; ++g) {
+                        const h4 av = __builtin_bit_cast(h4, u2{a[g][0], a[g][1]});
+                        acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, b, acc[g][c], 0, 0, 0);
+                    }
+                } else {
+                    h8 b;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) b[j] = lds[(4 * lq + j) * LDSW + col];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) b[4 + j] = lds[(16 + 4 * lq + j) * LDSW + col];
+#pragma unroll
+                    for (int g = 0; g < RG; ++g) {
+                        const h8 av = __builtin_bit_cast(h8, u4{a[g][0], a[g][1], a[g][2], a[g][3]});
+                        acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[g][c], 0, 0, 0);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < KS; ++s) {
+                    const float b = lds[(KS * lq + s) * LDSW + col];
+#pragma unroll
+                    for (int g = 0; g < RG; ++g)
+                        acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[g][s]), b,
+                                                                          acc[g][c], 0, 0, 0);
+                }
+            }
+        }
+    };
+    auto stage_b = [&](const u4 (&src)[NV]) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            u4 x = bv[i];
+            u4 x = src[i];
             if constexpr (!F16) {
                 x.x = round_tf32_bits(x.x); x.y = round_tf32_bits(x.y);
                 x.z = round_tf32_bits(x.z); x.w = round_tf32_bits(x.w);
@@ -195,78 +268,51 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
                 *(u4 *)d = x;
             }
         }
-        uint32_t acur[RG][AW];
-#pragma unroll
-        for (int g = 0; g < RG; ++g)
-#pragma unroll
-            for (int w = 0; w < AW; ++w) acur[g][w] = areg[g][w];
+    };
 
-        // Issue tile t+1's loads, and the column indices of t+2.
-        if (t + 1 < te) {
-            load_b();
-            load_a(t + 1, areg);
-            if (t + 2 < te) load_cid(t + 2);
+    // Prologue: B panels and A fragments of the first S tiles in flight, the
+    // column indices of tile tb+S in SGPRs.
+    u4 bv[S][NV];
+    uint32_t ar[S][RG][AW];
+    CSV cs;
+    int cid[NV];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+        if (tb + s < te) {
+            load_cs(tb + s, cs);
+            select_cid(cs, cid);
+            load_b(cid, bv[s]);
+            load_a(tb + s, ar[s]);
         }
+    if (tb + S < te) load_cs(tb + S, cs);
 
-        // MFMAs on tile t.
+    for (int t0 = tb; t0 < te; t0 += S) {
 #pragma unroll
-        for (int c = 0; c < CB; ++c) {
-            const int col = 16 * c + ln;
-            if constexpr (F16) {
-                if constexpr (BN == 16) {
-                    h4 b;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) b[j] = lds[(4 * lq + j) * LDSW + col];
-#pragma unroll
-                    for (int g = 0; g < RG; ++g) {
-                        h4 a;
-                        u2 ab = u2{acur[g][0], acur[g][1]};
-                        a = __builtin_bit_cast(h4, ab);
-                        acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, acc[g][c], 0, 0, 0);
-                    }
-                } else {
-                    h8 b;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) b[j] = lds[(4 * lq + j) * LDSW + col];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) b[4 + j] = lds[(16 + 4 * lq + j) * LDSW + col];
-#pragma unroll
-                    for (int g = 0; g < RG; ++g) {
-                        u4 ab = u4{acur[g][0], acur[g][1], acur[g][2], acur[g][3]};
-                        h8 a = __builtin_bit_cast(h8, ab);
-                        acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[g][c], 0, 0, 0);
-                    }
+        for (int s = 0; s < S; ++s) {
+            const int t = t0 + s;
+            if (t < te) {
+                if (t >= kend) {                 // task k is complete
+                    flush(k);
+                    do kend = uload(colstart, ++k + 1);
+                    while (kend <= t);           // skip empty tasks
                 }
-            } else {
+                stage_b(bv[s]);
+                uint32_t acur[RG][AW];
 #pragma unroll
-                for (int s = 0; s < KS; ++s) {
-                    const float b = lds[(KS * lq + s) * LDSW + col];
+                for (int g = 0; g < RG; ++g)
 #pragma unroll
-                    for (int g = 0; g < RG; ++g) {
-                        acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                            __uint_as_float(acur[g][s]), b, acc[g][c], 0, 0, 0);
-                    }
+                    for (int w = 0; w < AW; ++w) acur[g][w] = ar[s][g][w];
+                if (t + S < te) {
+                    select_cid(cs, cid);
+                    load_b(cid, bv[s]);
+                    load_a(t + S, ar[s]);
+                    if (t + S + 1 < te) load_cs(t + S + 1, cs);
                 }
+                compute(acur);
             }
         }
     }
-
-    // Epilogue: lane (ln, lq) holds D[4*lq + j][ln] of every 16x16 block.
-#pragma unroll
-    for (int g = 0; g < RG; ++g) {
-        if (BM == 8 && lq >= 2) break;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int r = row0 + 16 * g + 4 * lq + j;
-            if (r >= c_rows) continue;
-            float *crow = C + (size_t)r * ld + col0 + ln;
-#pragma unroll
-            for (int c = 0; c < CB; ++c) {
-                if (split) unsafeAtomicAdd(crow + 16 * c, acc[g][c][j]);
-                else crow[16 * c] = acc[g][c][j];
-            }
-        }
-    }
+    flush(k);
 }
 
 __global__ __launch_bounds__(256) void copy_kernel(u4 *__restrict__ dst, const u4 *__restrict__ src, size_t n)
@@ -279,65 +325,103 @@ __global__ __launch_bounds__(256) void copy_kernel(u4 *__restrict__ dst, const u
 // ---------------------------------------------------------------------------
 // Dispatch.
 // ---------------------------------------------------------------------------
-int chunk_width(int bm, int colB_p)
+// Defaults from the MI355X variant sweep (bench.py --sweep over configs 1-5):
+// one task per wave always won (the hardware dispatcher then balances tasks
+// and the resident waves cover a narrow window of rows, which keeps C writes
+// and shared B rows local); 8-row tiles prefer 64-column chunks with a single
+// prefetch stage (higher occupancy), 16-row tiles 128-column chunks with
+// three stages.
+int default_chunk_width(int bm, int colB_p)
 {
     if (colB_p == 32) return 32;
-    if (bm == 64) return 64;
-    return (colB_p % 128 == 0) ? 128 : 64;
+    if (bm == 16 && colB_p % 128 == 0) return 128;
+    return 64;
 }
 
-template <int BM, int W, int PREC>
-static const void *kernel_ptr()
+int default_stages(int bm, int prec, int w)
 {
-    return (const void *)&spmm_kernel<BM, W, PREC>;
+    (void)prec;
+    (void)w;
+    return bm == 16 ? 3 : 1;
 }
 
-const void *select_kernel(int bm, int prec, int w)
+bool valid_variant(int bm, int w, int s)
 {
-#define TSP_K(BMv, Wv)                                                              \
-    if (bm == BMv && w == Wv)                                                      \
-        return prec == TSP_PREC_FP16 ? kernel_ptr<BMv, Wv, TSP_PREC_FP16>()        \
-                                     : kernel_ptr<BMv, Wv, TSP_PREC_TF32>();
-    TSP_K(64, 32) TSP_K(64, 64)
-    TSP_K(16, 32) TSP_K(16, 64) TSP_K(16, 128)
-    TSP_K(8, 32) TSP_K(8, 64) TSP_K(8, 128)
+    if (s < 1 || s > 4) return false;
+    if (bm == 64) return w == 32 || w == 64;
+    return w == 32 || w == 64 || w == 128;
+}
+
+#define TSP_FOR_EACH_VARIANT(X)                                                                \
+    X(64, 32, 1) X(64, 32, 2) X(64, 32, 3) X(64, 32, 4)                                        \
+    X(64, 64, 1) X(64, 64, 2) X(64, 64, 3) X(64, 64, 4)                                        \
+    X(16, 32, 1) X(16, 32, 2) X(16, 32, 3) X(16, 32, 4)                                        \
+    X(16, 64, 1) X(16, 64, 2) X(16, 64, 3) X(16, 64, 4)                                        \
+    X(16, 128, 1) X(16, 128, 2) X(16, 128, 3) X(16, 128, 4)                                    \
+    X(8, 32, 1) X(8, 32, 2) X(8, 32, 3) X(8, 32, 4)                                            \
+    X(8, 64, 1) X(8, 64, 2) X(8, 64, 3) X(8, 64, 4)                                            \
+    X(8, 128, 1) X(8, 128, 2) X(8, 128, 3) X(8, 128, 4)
+
+const void *select_kernel(int bm, int prec, int w, int s)
+{
+#define TSP_K(BMv, Wv, Sv)                                                                     \
+    if (bm == BMv && w == Wv && s == Sv)                                                       \
+        return prec == TSP_PREC_FP16 ? (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv>  \
+                                     : (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv>;
+    TSP_FOR_EACH_VARIANT(TSP_K)
 #undef TSP_K
     return nullptr;
 }
 
-template <int BM, int W, int PREC>
-static void launch_t(dim3 grid, hipStream_t s, int ntasks, int nchunks, const void *val,
-                     const unsigned *rows, const int *colstart, const void *B, float *C,
-                     const int *colidx, int ld, int c_rows)
+static int cu_count()
 {
-    spmm_kernel<BM, W, PREC><<<grid, kBlockThreads, 0, s>>>(ntasks, nchunks, val, rows, colstart,
-                                                            B, C, colidx, ld, c_rows);
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            n = v;
+        else
+            n = 256;
+    }
+    return n;
+}
+
+int default_tasks_per_wave(int ntasks, int nchunks)
+{
+    (void)ntasks;
+    (void)nchunks;
+    (void)cu_count;
+    return 1;
 }
 
 int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const unsigned *rows,
            const int *colstart, const void *B, float *C, const int *colidx, int c_rows,
-           hipStream_t s)
+           hipStream_t st, int w, int s, int tpw)
 {
-    const int w = chunk_width(bm, colB_p);
+    if (w <= 0) w = default_chunk_width(bm, colB_p);
+    if (colB_p % w != 0) return TSP_EINVAL;
+    if (s <= 0) s = default_stages(bm, prec, w);
+    if (!valid_variant(bm, w, s)) return TSP_EINVAL;
     const int nchunks = colB_p / w;
-    const long long waves = (long long)ntasks * nchunks;
+    if (tpw <= 0) tpw = default_tasks_per_wave(ntasks, nchunks);
+    const long long ranges = ((long long)ntasks + tpw - 1) / tpw;
+    const long long waves = ranges * nchunks;
     const long long blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
     if (blocks <= 0) return 0;
     if (blocks > 0x7fffffffLL) return TSP_EINVAL;
-    dim3 grid((unsigned)blocks);
-#define TSP_L(BMv, Wv)                                                                         \
-    if (bm == BMv && w == Wv) {                                                                \
-        if (prec == TSP_PREC_FP16)                                                             \
-            launch_t<BMv, Wv, TSP_PREC_FP16>(grid, s, ntasks, nchunks, val, rows, colstart, B, C, \
-                                            colidx, colB_p, c_rows);                          \
-        else                                                                                   \
-            launch_t<BMv, Wv, TSP_PREC_TF32>(grid, s, ntasks, nchunks, val, rows, colstart, B, C, \
-                                            colidx, colB_p, c_rows);                          \
-        return (int)hipGetLastError();                                                         \
+    const dim3 grid((unsigned)blocks);
+#define TSP_L(BMv, Wv, Sv)                                                                      \
+    if (bm == BMv && w == Wv && s == Sv) {                                                      \
+        if (prec == TSP_PREC_FP16)                                                              \
+            spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv><<<grid, kBlockThreads, 0, st>>>(             \
+                ntasks, nchunks, tpw, val, rows, colstart, B, C, colidx, colB_p, c_rows);        \
+        else                                                                                    \
+            spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv><<<grid, kBlockThreads, 0, st>>>(             \
+                ntasks, nchunks, tpw, val, rows, colstart, B, C, colidx, colB_p, c_rows);        \
+        return (int)hipGetLastError();                                                          \
     }
-    TSP_L(64, 32) TSP_L(64, 64)
-    TSP_L(16, 32) TSP_L(16, 64) TSP_L(16, 128)
-    TSP_L(8, 32) TSP_L(8, 64) TSP_L(8, 128)
+    TSP_FOR_EACH_VARIANT(TSP_L)
 #undef TSP_L
     return TSP_EINVAL;
 }

@@ -31,6 +31,7 @@ struct ClassDev {
     long long cap_tasks = 0;
     int th = 0;
     int ntasks = 0;
+    int var_w = 0, var_s = 0, var_tpw = 0;   // kernel variant, 0 = library default
     void *stream = nullptr;
     std::map<int, std::pair<std::vector<unsigned>, std::vector<int>>> cache;
     bool active() const { return m && m->tilenum > 0; }
@@ -45,12 +46,19 @@ double now_ms()
 
 }  // namespace
 
+// Streams: one non-blocking stream per class plus a non-blocking "main"
+// stream.  A run records a start event on main, every class stream waits for
+// it, launches, records its own done event, and main waits for all three done
+// events -- an explicit fork/join that never touches the null stream, so no
+// launch pays an implicit null-stream synchronisation.
 struct tsp_plan {
     int dev = 0, prec = 0, rowA = 0, colA = 0, colB_p = 0;
     void *d_B = nullptr;
     float *d_C = nullptr;
     ClassDev cls[3];
+    void *main = nullptr;
     void *ev0 = nullptr, *ev1 = nullptr;
+    void *done[3] = {nullptr, nullptr, nullptr};
 };
 
 #define TSP_TRY(x)                  \
@@ -76,6 +84,8 @@ static int upload_schedule(tsp_plan *p, ClassDev &c, int th)
     }
     const int n = (int)it->second.first.size();
     if (n > c.cap_tasks) return TSP_EINVAL;
+    // kernels of an earlier run may still read the schedule buffers
+    TSP_TRY(tsp_device_sync());
     TSP_TRY(tsp_memcpy_h2d(c.d_rows, it->second.first.data(), sizeof(unsigned) * (size_t)n));
     TSP_TRY(tsp_memcpy_h2d(c.d_colstart, it->second.second.data(), sizeof(int) * ((size_t)n + 1)));
     c.th = th;
@@ -95,13 +105,32 @@ static int upload_schedule(tsp_plan *p, ClassDev &c, int th)
 static int launch_class(tsp_plan *p, ClassDev &c)
 {
     if (!c.active() || c.ntasks == 0) return TSP_OK;
+    if (c.var_w || c.var_s || c.var_tpw)
+        return tsp_spmm_launch_variant(c.bm, p->prec, c.ntasks, p->colB_p, c.d_val, c.d_rows,
+                                       c.d_colstart, p->d_B, p->d_C, c.d_colidx, p->rowA, c.stream,
+                                       c.var_w, c.var_s, c.var_tpw);
     return tsp_spmm_launch(c.bm, p->prec, c.ntasks, p->colB_p, c.d_val, c.d_rows, c.d_colstart,
                            p->d_B, p->d_C, c.d_colidx, p->rowA, c.stream);
+}
+
+extern "C" int tsp_plan_set_variant(tsp_plan *p, int bm, int w, int stages, int tasks_per_wave)
+{
+    if (!p) return TSP_EINVAL;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) {
+            if (w > 0 && p->colB_p % w != 0) return TSP_EINVAL;
+            c.var_w = w;
+            c.var_s = stages;
+            c.var_tpw = tasks_per_wave;
+            return TSP_OK;
+        }
+    return TSP_EINVAL;
 }
 
 extern "C" int tsp_plan_destroy(tsp_plan *p)
 {
     if (!p) return TSP_OK;
+    tsp_device_sync();
     for (ClassDev &c : p->cls) {
         tsp_free(c.d_val);
         tsp_free(c.d_colidx);
@@ -113,6 +142,8 @@ extern "C" int tsp_plan_destroy(tsp_plan *p)
     tsp_free(p->d_C);
     tsp_event_destroy(p->ev0);
     tsp_event_destroy(p->ev1);
+    for (void *e : p->done) tsp_event_destroy(e);
+    tsp_stream_destroy(p->main);
     delete p;
     return TSP_OK;
 }
@@ -155,10 +186,13 @@ extern "C" int tsp_plan_create(tsp_plan **out, int device_id, Tile_matrix *m64, 
         c.cap_tasks = (long long)c.m->tilem + c.m->tilenum;
         if ((st = tsp_malloc((void **)&c.d_rows, sizeof(unsigned) * (size_t)c.cap_tasks))) return fail(st);
         if ((st = tsp_malloc((void **)&c.d_colstart, sizeof(int) * ((size_t)c.cap_tasks + 1)))) return fail(st);
-        if ((st = tsp_stream_create(&c.stream))) return fail(st);
+        if ((st = tsp_stream_create_nonblocking(&c.stream))) return fail(st);
     }
+    if ((st = tsp_stream_create_nonblocking(&p->main))) return fail(st);
     if ((st = tsp_event_create(&p->ev0))) return fail(st);
     if ((st = tsp_event_create(&p->ev1))) return fail(st);
+    for (void *&e : p->done)
+        if ((st = tsp_event_create(&e))) return fail(st);
     *out = p.release();
     return TSP_OK;
 }
@@ -175,23 +209,44 @@ extern "C" int tsp_plan_set_th(tsp_plan *p, int th64, int th16, int th8)
     return TSP_OK;
 }
 
-extern "C" int tsp_plan_run(tsp_plan *p, int zero_c)
+// Fork from main (event ev0), `reps` launches per class on its own stream,
+// join back on main.
+static int fork_join(tsp_plan *p, int reps)
 {
-    if (!p) return TSP_EINVAL;
-    if (zero_c) TSP_TRY(tsp_memset(p->d_C, 0, sizeof(float) * (size_t)p->rowA * p->colB_p));
-    for (ClassDev &c : p->cls) TSP_TRY(launch_class(p, c));
+    TSP_TRY(tsp_event_record(p->ev0, p->main));
+    for (int i = 0; i < 3; ++i) {
+        ClassDev &c = p->cls[i];
+        if (!c.active() || c.ntasks == 0) continue;
+        TSP_TRY(tsp_stream_wait_event(c.stream, p->ev0));
+        for (int r = 0; r < reps; ++r) TSP_TRY(launch_class(p, c));
+        TSP_TRY(tsp_event_record(p->done[i], c.stream));
+        TSP_TRY(tsp_stream_wait_event(p->main, p->done[i]));
+    }
     return TSP_OK;
 }
 
+extern "C" int tsp_plan_run(tsp_plan *p, int zero_c)
+{
+    if (!p) return TSP_EINVAL;
+    if (zero_c) TSP_TRY(tsp_memset_async(p->d_C, 0, sizeof(float) * (size_t)p->rowA * p->colB_p, p->main));
+    return fork_join(p, 1);
+}
+
+// K steps: the three classes each run K back-to-back launches concurrently,
+// bracketed by events on main (as the reference times 1000 repetitions of
+// the three class streams between two events, src/csr2tile.h:1043-1055).
 extern "C" int tsp_plan_time(tsp_plan *p, int reps, double *ms)
 {
     if (!p || reps <= 0 || !ms) return TSP_EINVAL;
-    TSP_TRY(tsp_event_record(p->ev0, nullptr));
-    for (int r = 0; r < reps; ++r) TSP_TRY(tsp_plan_run(p, 0));
-    TSP_TRY(tsp_event_record(p->ev1, nullptr));
+    void *start = nullptr;
+    TSP_TRY(tsp_event_create(&start));
+    std::unique_ptr<void, int (*)(void *)> guard(start, tsp_event_destroy);
+    TSP_TRY(tsp_event_record(start, p->main));
+    TSP_TRY(fork_join(p, reps));
+    TSP_TRY(tsp_event_record(p->ev1, p->main));
     TSP_TRY(tsp_event_sync(p->ev1));
     float t = 0.f;
-    TSP_TRY(tsp_event_elapsed_ms(&t, p->ev0, p->ev1));
+    TSP_TRY(tsp_event_elapsed_ms(&t, start, p->ev1));
     *ms = (double)t / reps;
     return TSP_OK;
 }

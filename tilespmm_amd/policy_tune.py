@@ -1,0 +1,386 @@
+"""Retrain the (gamma, delta) split policy for MI355X by exhaustive tuning.
+
+The reference ships a decision tree trained on NVIDIA GPUs
+(src/model.h:14-3499); its training code is not part of the reference.  This
+tool rebuilds the policy for gfx950:
+
+  sweep  -- for each matrix of a corpus and each colB / precision, time the
+            full tiled SpMM (split + tiles + cost-model thresholds + runtime
+            threshold tuning, then 200 timed steps) for every one of the 66
+            (gamma, delta) candidates; candidates that give the same row split
+            share one measurement.  One JSON line per (matrix, colB, prec).
+  fit    -- fit a regret-minimising decision tree on the sweep results: every
+            leaf holds the candidate with the lowest mean normalised time
+            (time / best time of that matrix) over its training matrices.  The
+            tree is written as tilespmm_amd/host/policy_model.h in the node
+            layout of the reference's tilespmm_policy_node (binary nodes:
+            left_feature = right_feature = -1).
+  check  -- report, per swept matrix, the policy's pick vs the exhaustive
+            optimum (the "checked against exhaustive tuning" figure).
+
+  python -m tilespmm_amd.policy_tune sweep --corpus small --out gpurun_out/policy.jsonl
+  python -m tilespmm_amd.policy_tune fit --inp gpurun_out/policy.jsonl
+  python -m tilespmm_amd.policy_tune check --inp gpurun_out/policy.jsonl
+"""
+from __future__ import annotations
+
+import argparse
+import hashlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(HERE))
+
+import tilespmm_amd as tsp  # noqa: E402
+
+FEATURE_NAMES = ["rows", "cols", "nnz", "sparsity", "avg_row_nnz", "max_row_nnz", "min_row_nnz",
+                 "capability", "colB"]
+
+
+# ---------------------------------------------------------------------------
+# corpus: seeded synthetic structures of several families
+# ---------------------------------------------------------------------------
+def _csr_from_rows(n_rows, n_cols, rows_cols):
+    lens = np.array([len(c) for c in rows_cols], dtype=np.int64)
+    rp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    ci = np.concatenate([np.sort(np.asarray(c, dtype=np.int64)) for c in rows_cols]).astype(np.int32) \
+        if lens.sum() else np.zeros(0, np.int32)
+    return n_rows, n_cols, rp, ci
+
+
+def _coo_to_csr(n_rows, n_cols, r, c):
+    key = np.unique(r.astype(np.int64) * n_cols + c.astype(np.int64))
+    r, c = (key // n_cols).astype(np.int32), (key % n_cols).astype(np.int32)
+    rp = np.zeros(n_rows + 1, dtype=np.int64)
+    np.add.at(rp, r + 1, 1)
+    return n_rows, n_cols, np.cumsum(rp).astype(np.int32), c
+
+
+def gen_uniform(rng, n, k):
+    r = np.repeat(np.arange(n), k)
+    c = rng.integers(0, n, n * k)
+    return _coo_to_csr(n, n, r, c)
+
+
+def gen_stencil2d(nx, nine=False):
+    y, x = np.divmod(np.arange(nx * nx), nx)
+    rs, cs = [], []
+    offs = [(dy, dx) for dy in (-1, 0, 1) for dx in (-1, 0, 1) if nine or abs(dy) + abs(dx) <= 1]
+    for dy, dx in offs:
+        ok = (y + dy >= 0) & (y + dy < nx) & (x + dx >= 0) & (x + dx < nx)
+        rs.append(np.nonzero(ok)[0])
+        cs.append((y[ok] + dy) * nx + x[ok] + dx)
+    return _coo_to_csr(nx * nx, nx * nx, np.concatenate(rs), np.concatenate(cs))
+
+
+def gen_stencil3d(n):
+    z, rem = np.divmod(np.arange(n ** 3), n * n)
+    y, x = np.divmod(rem, n)
+    rs, cs = [], []
+    for dz, dy, dx in [(0, 0, 0), (-1, 0, 0), (1, 0, 0), (0, -1, 0), (0, 1, 0), (0, 0, -1), (0, 0, 1)]:
+        ok = (z + dz >= 0) & (z + dz < n) & (y + dy >= 0) & (y + dy < n) & (x + dx >= 0) & (x + dx < n)
+        rs.append(np.nonzero(ok)[0])
+        cs.append(((z[ok] + dz) * n + y[ok] + dy) * n + x[ok] + dx)
+    return _coo_to_csr(n ** 3, n ** 3, np.concatenate(rs), np.concatenate(cs))
+
+
+def gen_blocks(rng, n, bs, density, singles=0.0):
+    nb = n // bs
+    nblk = int(density * nb * nb)
+    ids = np.unique(rng.integers(0, nb * nb, nblk))
+    br, bc = ids // nb, ids % nb
+    ii, jj = np.meshgrid(np.arange(bs), np.arange(bs), indexing="ij")
+    r = (br[:, None] * bs + ii.reshape(1, -1)).reshape(-1)
+    c = (bc[:, None] * bs + jj.reshape(1, -1)).reshape(-1)
+    ns = int(singles * n * n)
+    if ns:
+        r = np.concatenate([r, rng.integers(0, n, ns)])
+        c = np.concatenate([c, rng.integers(0, n, ns)])
+    return _coo_to_csr(n, n, r, c)
+
+
+def gen_banded(rng, n, bw, k):
+    r = np.repeat(np.arange(n), k)
+    c = np.clip(r + rng.integers(-bw, bw + 1, n * k), 0, n - 1)
+    return _coo_to_csr(n, n, r, c)
+
+
+def gen_powerlaw(rng, n, mean, alpha):
+    u = rng.random(n) + 1e-12
+    lo, hi = 0.05, float(mean)
+    for _ in range(50):
+        xm = 0.5 * (lo + hi)
+        L = np.clip(np.round(xm * u ** (-1.0 / (alpha - 1.0))), 1, min(n, 10000))
+        if L.mean() < mean:
+            lo = xm
+        else:
+            hi = xm
+    L = L.astype(np.int64)
+    r = np.repeat(np.arange(n), L)
+    c = rng.integers(0, n, L.sum())
+    return _coo_to_csr(n, n, r, c)
+
+
+def gen_rmat(rng, scale, ef, a=0.57, b=0.19, c=0.19):
+    n = 1 << scale
+    m = n * ef
+    u = np.zeros(m, dtype=np.int64)
+    v = np.zeros(m, dtype=np.int64)
+    for _ in range(scale):
+        p = rng.random(m)
+        bu = (p >= a + b).astype(np.int64)
+        bv = (((p >= a) & (p < a + b)) | (p >= a + b + c)).astype(np.int64)
+        u = (u << 1) | bu
+        v = (v << 1) | bv
+    return _coo_to_csr(n, n, np.concatenate([u, v]), np.concatenate([v, u]))
+
+
+def corpus(which):
+    rng = np.random.default_rng(20260777)
+    items = []
+    if which in ("small", "full"):
+        items += [
+            ("uniform_2^16_k4", lambda: gen_uniform(rng, 1 << 16, 4)),
+            ("uniform_2^16_k32", lambda: gen_uniform(rng, 1 << 16, 32)),
+            ("uniform_2^18_k16", lambda: gen_uniform(rng, 1 << 18, 16)),
+            ("lap2d_512", lambda: gen_stencil2d(512)),
+            ("lap2d9_384", lambda: gen_stencil2d(384, nine=True)),
+            ("lap3d_48", lambda: gen_stencil3d(48)),
+            ("blocks16_2^15_d2", lambda: gen_blocks(rng, 1 << 15, 16, 0.02, 1e-4)),
+            ("blocks8_2^15_d1", lambda: gen_blocks(rng, 1 << 15, 8, 0.01)),
+            ("blocks32_2^14_d4", lambda: gen_blocks(rng, 1 << 14, 32, 0.04)),
+            ("blocks4_2^16_d05", lambda: gen_blocks(rng, 1 << 16, 4, 0.005)),
+            ("banded_2^18_bw64_k8", lambda: gen_banded(rng, 1 << 18, 64, 8)),
+            ("banded_2^17_bw512_k24", lambda: gen_banded(rng, 1 << 17, 512, 24)),
+            ("powerlaw_2^18_m16_a2.1", lambda: gen_powerlaw(rng, 1 << 18, 16, 2.1)),
+            ("powerlaw_2^18_m8_a1.8", lambda: gen_powerlaw(rng, 1 << 18, 8, 1.8)),
+            ("rmat_16_ef16", lambda: gen_rmat(rng, 16, 16)),
+            ("rmat_18_ef8", lambda: gen_rmat(rng, 18, 8)),
+            ("rmat_18_ef16_skew", lambda: gen_rmat(rng, 18, 16, 0.45, 0.15, 0.15)),
+        ]
+    if which == "full":
+        items += [
+            ("uniform_2^20_k8", lambda: gen_uniform(rng, 1 << 20, 8)),
+            ("lap2d_1024", lambda: gen_stencil2d(1024)),
+            ("blocks16_2^16_d1", lambda: gen_blocks(rng, 1 << 16, 16, 0.01)),
+            ("powerlaw_2^20_m16_a2.5", lambda: gen_powerlaw(rng, 1 << 20, 16, 2.5)),
+            ("rmat_20_ef16", lambda: gen_rmat(rng, 20, 16)),
+        ]
+    return items
+
+
+# ---------------------------------------------------------------------------
+# sweep
+# ---------------------------------------------------------------------------
+def time_candidate(A, B, colB, cbp, g, d, reps):
+    subs = tsp.matrix_split(A, g, d)
+    tiles = [tsp.tile_create(s, A.cols, bm, A.prec) for s, bm in zip(subs, (64, 16, 8))]
+    plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, A.prec, B)
+    try:
+        th, _, _ = plan.tune(True)
+        plan.warmup(10)
+        ms = plan.time(reps)
+    finally:
+        plan.close()
+    return ms, th, [t.tilenum for t in tiles]
+
+
+def sweep_matrix(name, A, colB, reps, out):
+    cbp = tsp.colB_padded(colB)
+    rng = np.random.default_rng(7)
+    b = np.zeros((A.cols, cbp), dtype=np.float32)
+    b[:, :colB] = rng.uniform(-1, 1, (A.cols, colB))
+    B = b.astype(np.float16).view(np.uint16) if A.prec == 0 else b
+    f = tsp.features(A, 9.5, colB)
+    gs, ds = tsp.policy_candidates()
+    seen = {}
+    times = []
+    for g, d in zip(gs.tolist(), ds.tolist()):
+        cls = tsp.split_classes(A, g, d)
+        sig = hashlib.sha1(cls.tobytes()).hexdigest()
+        if sig not in seen:
+            seen[sig] = time_candidate(A, B, colB, cbp, g, d, reps)
+        times.append(seen[sig][0])
+    best = int(np.argmin(times))
+    rec = {"matrix": name, "prec": A.prec, "colB": colB, "features": f.tolist(), "times_ms": times,
+           "best": best, "best_ms": times[best], "distinct_splits": len(seen),
+           "pred_default": tsp.predict(f, A.prec)}
+    out.write(json.dumps(rec) + "\n")
+    out.flush()
+    print(f"{name} prec={A.prec} colB={colB}: best cand {best} ({gs[best]:.2f},{ds[best]:.2f}) "
+          f"{times[best]:.4f} ms, worst {max(times):.4f} ms, {len(seen)} distinct splits", flush=True)
+
+
+def with_values(rows, cols, rp, ci, prec, seed):
+    n = len(ci)
+    v = np.random.default_rng(seed).uniform(-1, 1, n).astype(np.float32)
+    val = v.astype(np.float16).view(np.uint16) if prec == 0 else v
+    return tsp.Csr(rows, cols, rp, ci, val, prec)
+
+
+def cmd_sweep(args):
+    tsp.load()
+    if not tsp.device_available():
+        raise SystemExit("policy_tune sweep needs a gfx950 device")
+    with open(args.out, "a") as out:
+        mats = []
+        for cfg in args.configs:
+            mats.append((f"config{cfg}", lambda cfg=cfg: tsp.gen_structure(cfg)))
+        if args.corpus:
+            mats += corpus(args.corpus)
+        for name, make in mats:
+            t0 = time.time()
+            rows, cols, rp, ci = make()
+            print(f"-- {name}: {rows} rows, {int(rp[-1])} nnz ({time.time() - t0:.1f}s)", flush=True)
+            for prec in args.precs:
+                A = with_values(rows, cols, rp, ci, prec, 11)
+                for colB in args.colBs:
+                    sweep_matrix(name, A, colB, args.reps, out)
+
+
+# ---------------------------------------------------------------------------
+# fit + export
+# ---------------------------------------------------------------------------
+def load_results(path):
+    recs = [json.loads(l) for l in open(path) if l.strip()]
+    return [r for r in recs if "times_ms" in r]
+
+
+def fit_tree(recs, max_depth, min_leaf):
+    """Greedy binary tree over features; leaf = candidate with the lowest mean
+    normalised time among its matrices; splits maximise the drop in summed
+    regret."""
+    X = np.array([[r["features"][i + 2] for i in range(9)] for r in recs], dtype=np.float64)
+    T = np.array([np.array(r["times_ms"]) / r["best_ms"] for r in recs], dtype=np.float64)
+
+    def leaf_cost(idx):
+        m = T[idx].mean(axis=0)
+        a = int(np.argmin(m))
+        return a, float(T[idx, a].sum())
+
+    nodes = []
+
+    def build(idx, depth):
+        a, cost = leaf_cost(idx)
+        if depth >= max_depth or len(idx) < 2 * min_leaf:
+            return -1 - a
+        best = None
+        for f in range(X.shape[1]):
+            vals = np.unique(X[idx, f])
+            for lo, hi in zip(vals[:-1], vals[1:]):
+                cut = np.float32((lo + hi) / 2)
+                left = idx[X[idx, f].astype(np.float32) < cut]
+                right = idx[X[idx, f].astype(np.float32) >= cut]
+                if len(left) < min_leaf or len(right) < min_leaf:
+                    continue
+                c = leaf_cost(left)[1] + leaf_cost(right)[1]
+                if best is None or c < best[0] - 1e-9:
+                    best = (c, f, float(cut), left, right)
+        if best is None or best[0] >= cost - 1e-6:
+            return -1 - a
+        me = len(nodes)
+        nodes.append(None)
+        l_child = build(best[3], depth + 1)
+        r_child = build(best[4], depth + 1)
+        nodes[me] = {"feature": best[1], "cut": best[2], "left": l_child, "right": r_child}
+        return me
+
+    root = build(np.arange(len(recs)), 0)
+    return root, nodes
+
+
+def export_header(path, roots, nodes_all, note):
+    lines = [
+        "// policy_model.h -- (gamma, delta) policy table for MI355X.",
+        "//",
+        "// Node layout and walk semantics are those of the reference's exported",
+        "// decision tree (tilespmm_policy_node, src/model.h:9-13; walk",
+        "// src/model.h:3463-3491) so that a retrained table drops into the same",
+        "// tilespmm_predict_* C ABI.  Action a selects candidate a of the list built",
+        "// by policy_candidates(); a root or child < 0 is a leaf holding -1 - action.",
+        "//",
+        f"// GENERATED by tilespmm_amd/policy_tune.py fit ({note}).",
+        "#pragma once",
+        "",
+        "struct tsp_policy_node {",
+        "    int feature, left_feature, right_feature;",
+        "    int child0, child1, child2, child3, missing_left_mask;",
+        "    float cut, left_cut, right_cut;",
+        "};",
+        "",
+        "static const tsp_policy_node tsp_policy_nodes[] = {",
+    ]
+    for n in nodes_all:
+        lines.append(f"    {{{n['feature']}, -1, -1, {n['left']}, -1, {n['right']}, -1, 1, "
+                     f"{np.float32(n['cut']).item()!r}f, 0.0f, 0.0f}},")
+    if not nodes_all:
+        lines.append("    {4, -1, -1, -1, -1, -1, -1, 0, 0.0f, 0.0f, 0.0f},")
+    lines += ["};", "",
+              f"static const int tsp_policy_root_fp16 = {roots[0]};",
+              f"static const int tsp_policy_root_tf32 = {roots[1]};", ""]
+    open(path, "w").write("\n".join(lines))
+
+
+def cmd_fit(args):
+    recs = load_results(args.inp)
+    roots, allnodes = [], []
+    for prec in (0, 1):
+        rs = [r for r in recs if r["prec"] == prec] or recs
+        root, nodes = fit_tree(rs, args.depth, args.min_leaf)
+        off = len(allnodes)
+
+        def shift(x):
+            return x + off if x >= 0 else x
+        for n in nodes:
+            allnodes.append({"feature": n["feature"], "cut": n["cut"], "left": shift(n["left"]),
+                             "right": shift(n["right"])})
+        roots.append(shift(root))
+    note = f"{len(recs)} swept (matrix, colB, precision) cases, depth <= {args.depth}"
+    export_header(args.header, roots, allnodes, note)
+    print(f"wrote {args.header}: {len(allnodes)} nodes, roots {roots}")
+
+
+def cmd_check(args):
+    recs = load_results(args.inp)
+    tsp.load()
+    tot = []
+    for r in recs:
+        g, d = tsp.predict(np.array(r["features"]), r["prec"])
+        gs, ds = tsp.policy_candidates()
+        a = [i for i in range(len(gs)) if gs[i] == np.float32(g) and ds[i] == np.float32(d)][0]
+        slow = r["times_ms"][a] / r["best_ms"]
+        tot.append(slow)
+        print(f"{r['matrix']:28s} prec={r['prec']} colB={r['colB']:4d} policy ({g:.2f},{d:.2f}) "
+              f"{r['times_ms'][a]:.4f} ms vs best {r['best_ms']:.4f} ms -> x{slow:.3f}")
+    if tot:
+        print(f"mean slowdown vs exhaustive optimum: x{np.mean(tot):.3f}, worst x{np.max(tot):.3f}")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    s = sub.add_parser("sweep")
+    s.add_argument("--configs", type=int, nargs="*", default=[])
+    s.add_argument("--corpus", choices=["small", "full"], default=None)
+    s.add_argument("--precs", type=int, nargs="*", default=[0, 1])
+    s.add_argument("--colBs", type=int, nargs="*", default=[32, 128])
+    s.add_argument("--reps", type=int, default=50)
+    s.add_argument("--out", required=True)
+    f = sub.add_parser("fit")
+    f.add_argument("--inp", required=True)
+    f.add_argument("--header", default=os.path.join(HERE, "host", "policy_model.h"))
+    f.add_argument("--depth", type=int, default=4)
+    f.add_argument("--min-leaf", type=int, default=3)
+    c = sub.add_parser("check")
+    c.add_argument("--inp", required=True)
+    args = ap.parse_args()
+    {"sweep": cmd_sweep, "fit": cmd_fit, "check": cmd_check}[args.cmd](args)
+
+
+if __name__ == "__main__":
+    main()
