@@ -75,10 +75,11 @@ def sweep(plan, tiles, cbp, args):
         res["default"] = plan.time_class(bm, args.class_reps)
         for w in widths:
             for s in (1, 2, 3, 4):
-                for tpw in (1, 4, 16, 0):
-                    plan.set_variant(bm, w, s, tpw)
-                    plan.time_class(bm, 3)
-                    res[f"w{w}_s{s}_t{tpw}"] = plan.time_class(bm, args.class_reps)
+                for tpw in (1, 4):
+                    for order in ((1, 2) if cbp > w else (1,)):
+                        plan.set_variant(bm, w, s, tpw, order)
+                        plan.time_class(bm, 3)
+                        res[f"w{w}_s{s}_t{tpw}_o{order}"] = plan.time_class(bm, args.class_reps)
         plan.set_variant(bm)
         best = min(res, key=res.get)
         print(json.dumps({"sweep": args.config, "bm": bm, "tiles": t.tilenum, "best": best,

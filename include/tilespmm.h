@@ -173,7 +173,8 @@ int tsp_plan_set_th(tsp_plan *plan, int th64, int th16, int th8);
 int tsp_plan_tune(tsp_plan *plan, int tune, int th_out[3], double *model_ms, double *tune_ms);
 /* Pin the kernel variant one class launches with (see
  * tsp_spmm_launch_variant); zeros restore the library default. */
-int tsp_plan_set_variant(tsp_plan *plan, int bm, int w, int stages, int tasks_per_wave);
+int tsp_plan_set_variant(tsp_plan *plan, int bm, int w, int stages, int tasks_per_wave,
+                         int order);
 /* Launch the three classes once (each on its own stream, joined on the null
  * stream).  zero_c != 0 clears C first. */
 int tsp_plan_run(tsp_plan *plan, int zero_c);

@@ -119,13 +119,16 @@ int tsp_spmm_launch(int bm, int prec, int rowblkblock, int colB_p,
 /* Same launch with an explicit kernel variant, for tuning drivers: chunk
  * width w (output columns per wave: 32, 64 or 128; 64-row tiles 32 or 64),
  * software-pipeline depth stages (1-4 tiles in flight per wave) and
- * tasks_per_wave (consecutive tasks one wave streams).  Values <= 0 pick the
- * defaults tsp_spmm_launch uses.  No counterpart in the reference (its
- * kernels have one fixed shape per class). */
+ * tasks_per_wave (consecutive tasks one wave streams) and the order of the
+ * column chunks (1: the chunks of one task range run side by side, 2:
+ * chunk-major, every range of chunk 0 first).  Values <= 0 pick the defaults
+ * tsp_spmm_launch uses.  No counterpart in the reference (its kernels have
+ * one fixed shape per class). */
 int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p,
                             const void *d_val, const unsigned *d_rows, const int *d_colstart,
                             const void *d_B, float *d_C, const int *d_colidx,
-                            int c_rows, void *stream, int w, int stages, int tasks_per_wave);
+                            int c_rows, void *stream, int w, int stages, int tasks_per_wave,
+                            int order);
 
 /* Per-class entry points with the reference dispatcher names
  * (src/tilespmm_cuda.h:1634, :1672, :1710) and argument order. */

@@ -130,12 +130,13 @@ def test_every_kernel_variant(gpu, orc, prec):
             plan.set_th(8, 8, 8)
             for w in ((32, 64) if bm == 64 else (32, 64, 128)):
                 for s in (1, 2, 3, 4):
-                    for tpw in (1, 3, 0):
-                        say(f"variant prec={prec} bm={bm} w={w} s={s} tpw={tpw}")
-                        plan.set_variant(bm, w, s, tpw)
+                    for tpw, order in ((1, 1), (3, 2), (0, 0)):
+                        say(f"variant prec={prec} bm={bm} w={w} s={s} tpw={tpw} order={order}")
+                        plan.set_variant(bm, w, s, tpw, order)
                         plan.run(zero_c=True)
                         Cg = plan.download_c()
-                        assert_close(Cg[:, :colB], Cref, Cabs, prec, f"bm={bm} w={w} s={s} tpw={tpw}")
+                        assert_close(Cg[:, :colB], Cref, Cabs, prec,
+                                     f"bm={bm} w={w} s={s} tpw={tpw} order={order}")
         finally:
             plan.close()
 

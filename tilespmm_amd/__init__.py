@@ -148,7 +148,7 @@ HIP_SYMBOLS = {
     "tsp_spmm_launch": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P,
                                   C.c_int, _P]),
     "tsp_spmm_launch_variant": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P,
-                                          C.c_int, _P, C.c_int, C.c_int, C.c_int]),
+                                          C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int]),
     "tsp_switch_v64": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v16": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v8": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
@@ -190,7 +190,7 @@ HOST_SYMBOLS = {
                                   C.c_int, C.c_int, _P]),
     "tsp_plan_set_th": (C.c_int, [_P, C.c_int, C.c_int, C.c_int]),
     "tsp_plan_tune": (C.c_int, [_P, C.c_int, _P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
-    "tsp_plan_set_variant": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "tsp_plan_set_variant": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "tsp_plan_run": (C.c_int, [_P, C.c_int]),
     "tsp_plan_warmup": (C.c_int, [_P, C.c_int]),
     "tsp_plan_time": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double)]),
@@ -495,8 +495,9 @@ class Plan:
         _check("tsp_plan_tune", load()[1].tsp_plan_tune(self.p, int(tune), _ptr(th), C.byref(mm), C.byref(tm)))
         return tuple(int(x) for x in th), mm.value, tm.value
 
-    def set_variant(self, bm: int, w: int = 0, stages: int = 0, tasks_per_wave: int = 0):
-        _check("tsp_plan_set_variant", load()[1].tsp_plan_set_variant(self.p, bm, w, stages, tasks_per_wave))
+    def set_variant(self, bm: int, w: int = 0, stages: int = 0, tasks_per_wave: int = 0, order: int = 0):
+        _check("tsp_plan_set_variant", load()[1].tsp_plan_set_variant(self.p, bm, w, stages, tasks_per_wave,
+                                                                      order))
 
     def run(self, zero_c: bool = True):
         _check("tsp_plan_run", load()[1].tsp_plan_run(self.p, int(zero_c)))

@@ -170,13 +170,13 @@ int tsp_spmm_launch(int bm, int prec, int rowblkblock, int colB_p, const void *d
     if (rowblkblock == 0) return TSP_OK;
     if (!d_val || !d_rows || !d_colstart || !d_B || !d_C || !d_colidx) return TSP_EINVAL;
     return tsp::launch(bm, prec, rowblkblock, colB_p, d_val, d_rows, d_colstart, d_B, d_C,
-                       d_colidx, c_rows, (hipStream_t)stream, 0, 0, 0);
+                       d_colidx, c_rows, (hipStream_t)stream, 0, 0, 0, 0);
 }
 
 int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
                             const unsigned *d_rows, const int *d_colstart, const void *d_B,
                             float *d_C, const int *d_colidx, int c_rows, void *stream, int w,
-                            int stages, int tasks_per_wave)
+                            int stages, int tasks_per_wave, int order)
 {
     if (bm != 64 && bm != 16 && bm != 8) return TSP_EINVAL;
     if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
@@ -186,7 +186,7 @@ int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p, const
     if (rowblkblock == 0) return TSP_OK;
     if (!d_val || !d_rows || !d_colstart || !d_B || !d_C || !d_colidx) return TSP_EINVAL;
     return tsp::launch(bm, prec, rowblkblock, colB_p, d_val, d_rows, d_colstart, d_B, d_C,
-                       d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave);
+                       d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave, order);
 }
 
 int tsp_switch_v64(int prec, int rowblkblock, int colB_p, const void *d_val, const unsigned *d_rows,

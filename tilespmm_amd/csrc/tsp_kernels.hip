@@ -82,7 +82,7 @@ __device__ __forceinline__ int xcd_remap(int b, int nb)
 
 template <int BM, int W, int PREC, int S>
 __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
-    int ntasks, int nchunks, int tasks_per_wave, const void *__restrict__ val_,
+    int ntasks, int nchunks, int tasks_per_wave, int chunk_major, const void *__restrict__ val_,
     const unsigned *__restrict__ rows, const int *__restrict__ colstart,
     const void *__restrict__ B_, float *__restrict__ C, const int *__restrict__ colidx, int ld,
     int c_rows)
@@ -108,8 +108,11 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     const long long gw = (long long)lb * kWavesPerBlock + wid;
     const long long nranges = ((long long)ntasks + tasks_per_wave - 1) / tasks_per_wave;
     if (gw >= nranges * nchunks) return;
-    const int range = (int)(gw / nchunks);
-    const int chunk = (int)(gw - (long long)range * nchunks);
+    // chunk_major: all task ranges of chunk 0, then chunk 1, ... (the live
+    // B working set of a phase is one chunk's columns); otherwise the chunks
+    // of one range are neighbours (the A tiles are reused from L2).
+    const int range = chunk_major ? (int)(gw % nranges) : (int)(gw / nchunks);
+    const int chunk = chunk_major ? (int)(gw / nranges) : (int)(gw - (long long)range * nchunks);
     const int k0 = range * tasks_per_wave;
     const int k1 = min(ntasks, k0 + tasks_per_wave);
     const int tb = uload(colstart, k0), te = uload(colstart, k1);
@@ -395,9 +398,18 @@ int default_tasks_per_wave(int ntasks, int nchunks)
     return 1;
 }
 
+int default_chunk_major(int bm, int prec, int colB_p, int w)
+{
+    (void)bm;
+    (void)prec;
+    (void)colB_p;
+    (void)w;
+    return 0;
+}
+
 int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const unsigned *rows,
            const int *colstart, const void *B, float *C, const int *colidx, int c_rows,
-           hipStream_t st, int w, int s, int tpw)
+           hipStream_t st, int w, int s, int tpw, int order)
 {
     if (w <= 0) w = default_chunk_width(bm, colB_p);
     if (colB_p % w != 0) return TSP_EINVAL;
@@ -405,6 +417,7 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const unsi
     if (!valid_variant(bm, w, s)) return TSP_EINVAL;
     const int nchunks = colB_p / w;
     if (tpw <= 0) tpw = default_tasks_per_wave(ntasks, nchunks);
+    const int cm = order > 0 ? (order == 2 ? 1 : 0) : default_chunk_major(bm, prec, colB_p, w);
     const long long ranges = ((long long)ntasks + tpw - 1) / tpw;
     const long long waves = ranges * nchunks;
     const long long blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
@@ -415,10 +428,10 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const unsi
     if (bm == BMv && w == Wv && s == Sv) {                                                      \
         if (prec == TSP_PREC_FP16)                                                              \
             spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv><<<grid, kBlockThreads, 0, st>>>(             \
-                ntasks, nchunks, tpw, val, rows, colstart, B, C, colidx, colB_p, c_rows);        \
+                ntasks, nchunks, tpw, cm, val, rows, colstart, B, C, colidx, colB_p, c_rows);    \
         else                                                                                    \
             spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv><<<grid, kBlockThreads, 0, st>>>(             \
-                ntasks, nchunks, tpw, val, rows, colstart, B, C, colidx, colB_p, c_rows);        \
+                ntasks, nchunks, tpw, cm, val, rows, colstart, B, C, colidx, colB_p, c_rows);    \
         return (int)hipGetLastError();                                                          \
     }
     TSP_FOR_EACH_VARIANT(TSP_L)

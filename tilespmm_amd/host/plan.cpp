@@ -31,7 +31,7 @@ struct ClassDev {
     long long cap_tasks = 0;
     int th = 0;
     int ntasks = 0;
-    int var_w = 0, var_s = 0, var_tpw = 0;   // kernel variant, 0 = library default
+    int var_w = 0, var_s = 0, var_tpw = 0, var_order = 0;   // kernel variant, 0 = library default
     void *stream = nullptr;
     std::map<int, std::pair<std::vector<unsigned>, std::vector<int>>> cache;
     bool active() const { return m && m->tilenum > 0; }
@@ -105,15 +105,16 @@ static int upload_schedule(tsp_plan *p, ClassDev &c, int th)
 static int launch_class(tsp_plan *p, ClassDev &c)
 {
     if (!c.active() || c.ntasks == 0) return TSP_OK;
-    if (c.var_w || c.var_s || c.var_tpw)
+    if (c.var_w || c.var_s || c.var_tpw || c.var_order)
         return tsp_spmm_launch_variant(c.bm, p->prec, c.ntasks, p->colB_p, c.d_val, c.d_rows,
                                        c.d_colstart, p->d_B, p->d_C, c.d_colidx, p->rowA, c.stream,
-                                       c.var_w, c.var_s, c.var_tpw);
+                                       c.var_w, c.var_s, c.var_tpw, c.var_order);
     return tsp_spmm_launch(c.bm, p->prec, c.ntasks, p->colB_p, c.d_val, c.d_rows, c.d_colstart,
                            p->d_B, p->d_C, c.d_colidx, p->rowA, c.stream);
 }
 
-extern "C" int tsp_plan_set_variant(tsp_plan *p, int bm, int w, int stages, int tasks_per_wave)
+extern "C" int tsp_plan_set_variant(tsp_plan *p, int bm, int w, int stages, int tasks_per_wave,
+                                    int order)
 {
     if (!p) return TSP_EINVAL;
     for (ClassDev &c : p->cls)
@@ -122,6 +123,7 @@ extern "C" int tsp_plan_set_variant(tsp_plan *p, int bm, int w, int stages, int 
             c.var_w = w;
             c.var_s = stages;
             c.var_tpw = tasks_per_wave;
+            c.var_order = order;
             return TSP_OK;
         }
     return TSP_EINVAL;
