@@ -315,8 +315,29 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
                         best[0] = a; best[1] = b; best[2] = c;
                     }
                 }
-        t3 = now_ms();
         TSP_TRY(tsp_plan_set_th(p, best[0], best[1], best[2]));
+        t3 = now_ms();
+    }
+    if (tune) {
+        // Column-chunk order per class (MI355X addition): chunks of one task
+        // side by side share A tiles in L2, chunk-major shrinks the live B
+        // working set per phase; which wins depends on |B| against the
+        // MALL and on the tile class, so measure both.
+        for (ClassDev &c : p->cls) {
+            if (!c.active() || c.ntasks == 0 || c.var_w || c.var_order) continue;
+            tsp_kernel_info k;
+            TSP_TRY(tsp_kernel_probe(c.bm, p->prec, p->colB_p, &k));
+            if (p->colB_p / k.cols_per_task < 2) continue;
+            double ms[2] = {0, 0};
+            for (int o = 1; o <= 2; ++o) {
+                c.var_order = o;
+                double warm = 0;
+                TSP_TRY(tsp_plan_time_class(p, c.bm, 3, &warm));
+                TSP_TRY(tsp_plan_time_class(p, c.bm, 10, &ms[o - 1]));
+            }
+            c.var_order = ms[1] < ms[0] ? 2 : 1;
+        }
+        t3 = now_ms();
     }
     if (tune_ms) *tune_ms = t3 - t2;
     if (th_out) for (int i = 0; i < 3; ++i) th_out[i] = best[i];

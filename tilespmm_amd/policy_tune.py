@@ -177,20 +177,22 @@ def corpus(which):
 # ---------------------------------------------------------------------------
 # sweep
 # ---------------------------------------------------------------------------
-def time_candidate(A, B, colB, cbp, g, d, reps):
+def time_candidate(A, B, colB, cbp, g, d, reps, tune):
+    """Split + tiles + thresholds (cost-model top-1, or runtime-tuned) and the
+    mean time of `reps` full SpMM steps."""
     subs = tsp.matrix_split(A, g, d)
     tiles = [tsp.tile_create(s, A.cols, bm, A.prec) for s, bm in zip(subs, (64, 16, 8))]
     plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, A.prec, B)
     try:
-        th, _, _ = plan.tune(True)
-        plan.warmup(10)
+        th, _, _ = plan.tune(tune)
+        plan.warmup(5)
         ms = plan.time(reps)
     finally:
         plan.close()
     return ms, th, [t.tilenum for t in tiles]
 
 
-def sweep_matrix(name, A, colB, reps, out):
+def sweep_matrix(name, A, colB, reps, out, tune=False):
     cbp = tsp.colB_padded(colB)
     rng = np.random.default_rng(7)
     b = np.zeros((A.cols, cbp), dtype=np.float32)
@@ -204,7 +206,7 @@ def sweep_matrix(name, A, colB, reps, out):
         cls = tsp.split_classes(A, g, d)
         sig = hashlib.sha1(cls.tobytes()).hexdigest()
         if sig not in seen:
-            seen[sig] = time_candidate(A, B, colB, cbp, g, d, reps)
+            seen[sig] = time_candidate(A, B, colB, cbp, g, d, reps, tune)
         times.append(seen[sig][0])
     best = int(np.argmin(times))
     rec = {"matrix": name, "prec": A.prec, "colB": colB, "features": f.tolist(), "times_ms": times,
@@ -233,6 +235,8 @@ def cmd_sweep(args):
             mats.append((f"config{cfg}", lambda cfg=cfg: tsp.gen_structure(cfg)))
         if args.corpus:
             mats += corpus(args.corpus)
+        if args.only:
+            mats = [m for m in mats if any(o in m[0] for o in args.only)]
         for name, make in mats:
             t0 = time.time()
             rows, cols, rp, ci = make()
@@ -240,7 +244,7 @@ def cmd_sweep(args):
             for prec in args.precs:
                 A = with_values(rows, cols, rp, ci, prec, 11)
                 for colB in args.colBs:
-                    sweep_matrix(name, A, colB, args.reps, out)
+                    sweep_matrix(name, A, colB, args.reps, out, args.tune)
 
 
 # ---------------------------------------------------------------------------
@@ -369,7 +373,9 @@ def main():
     s.add_argument("--corpus", choices=["small", "full"], default=None)
     s.add_argument("--precs", type=int, nargs="*", default=[0, 1])
     s.add_argument("--colBs", type=int, nargs="*", default=[32, 128])
-    s.add_argument("--reps", type=int, default=50)
+    s.add_argument("--reps", type=int, default=30)
+    s.add_argument("--tune", action="store_true", help="runtime-tune thresholds for every candidate")
+    s.add_argument("--only", nargs="*", default=None, help="substrings of matrix names to keep")
     s.add_argument("--out", required=True)
     f = sub.add_parser("fit")
     f.add_argument("--inp", required=True)
