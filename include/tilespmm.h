@@ -175,6 +175,12 @@ int tsp_plan_tune(tsp_plan *plan, int tune, int th_out[3], double *model_ms, dou
  * tsp_spmm_launch_variant); zeros restore the library default. */
 int tsp_plan_set_variant(tsp_plan *plan, int bm, int w, int stages, int tasks_per_wave,
                          int order);
+/* A-tile format of one class on the device: 1 = dense canonical tiles,
+ * 2 = bitmap-packed (8- and 16-row classes), 0 = keep.  tsp_plan_create picks
+ * packed when it moves at most 3/4 of the dense bytes.  get returns the
+ * current format (0 for an empty class, -1 on a bad argument). */
+int tsp_plan_set_format(tsp_plan *plan, int bm, int fmt);
+int tsp_plan_get_format(tsp_plan *plan, int bm);
 /* Launch the three classes once (each on its own stream, joined on the null
  * stream).  zero_c != 0 clears C first. */
 int tsp_plan_run(tsp_plan *plan, int zero_c);

@@ -130,6 +130,19 @@ int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p,
                             int c_rows, void *stream, int w, int stages, int tasks_per_wave,
                             int order);
 
+/* Launch on the bitmap-packed A format (8- and 16-row classes only): for
+ * tile t, bit r*BN+c of d_bitmap[t*BM*BN/64 ...] marks slot (r, c), and the
+ * values of its set bits, in bit order, start at element d_vptr[t] of d_pval
+ * (d_pval must hold 4 readable elements past the last value).  Same result
+ * as tsp_spmm_launch on the dense tiles; variant arguments as in
+ * tsp_spmm_launch_variant.  No counterpart in the reference (it always
+ * streams dense zero-padded tiles). */
+int tsp_spmm_launch_packed(int bm, int prec, int rowblkblock, int colB_p, const void *d_pval,
+                           const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,
+                           const int *d_colstart, const void *d_B, float *d_C,
+                           const int *d_colidx, int c_rows, void *stream, int w, int stages,
+                           int tasks_per_wave, int order);
+
 /* Per-class entry points with the reference dispatcher names
  * (src/tilespmm_cuda.h:1634, :1672, :1710) and argument order. */
 int tsp_switch_v64(int prec, int rowblkblock, int colB_p, const void *d_val,

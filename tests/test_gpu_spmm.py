@@ -128,15 +128,18 @@ def test_every_kernel_variant(gpu, orc, prec):
         plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
         try:
             plan.set_th(8, 8, 8)
-            for w in ((32, 64) if bm == 64 else (32, 64, 128)):
-                for s in (1, 2, 3, 4):
-                    for tpw, order in ((1, 1), (3, 2), (0, 0)):
-                        say(f"variant prec={prec} bm={bm} w={w} s={s} tpw={tpw} order={order}")
-                        plan.set_variant(bm, w, s, tpw, order)
-                        plan.run(zero_c=True)
-                        Cg = plan.download_c()
-                        assert_close(Cg[:, :colB], Cref, Cabs, prec,
-                                     f"bm={bm} w={w} s={s} tpw={tpw} order={order}")
+            for fmt in ((1,) if bm == 64 else (1, 2)):
+                plan.set_format(bm, fmt)
+                assert plan.get_format(bm) == fmt
+                for w in ((32, 64) if bm == 64 else (32, 64, 128)):
+                    for s in (1, 2, 3, 4):
+                        for tpw, order in ((1, 1), (3, 2), (0, 0)):
+                            tag = f"prec={prec} bm={bm} fmt={fmt} w={w} s={s} tpw={tpw} order={order}"
+                            say("variant " + tag)
+                            plan.set_variant(bm, w, s, tpw, order)
+                            plan.run(zero_c=True)
+                            Cg = plan.download_c()
+                            assert_close(Cg[:, :colB], Cref, Cabs, prec, tag)
         finally:
             plan.close()
 

@@ -149,6 +149,8 @@ HIP_SYMBOLS = {
                                   C.c_int, _P]),
     "tsp_spmm_launch_variant": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P,
                                           C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "tsp_spmm_launch_packed": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P,
+                                         C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int]),
     "tsp_switch_v64": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v16": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v8": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
@@ -191,6 +193,8 @@ HOST_SYMBOLS = {
     "tsp_plan_set_th": (C.c_int, [_P, C.c_int, C.c_int, C.c_int]),
     "tsp_plan_tune": (C.c_int, [_P, C.c_int, _P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "tsp_plan_set_variant": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "tsp_plan_set_format": (C.c_int, [_P, C.c_int, C.c_int]),
+    "tsp_plan_get_format": (C.c_int, [_P, C.c_int]),
     "tsp_plan_run": (C.c_int, [_P, C.c_int]),
     "tsp_plan_warmup": (C.c_int, [_P, C.c_int]),
     "tsp_plan_time": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double)]),
@@ -498,6 +502,13 @@ class Plan:
     def set_variant(self, bm: int, w: int = 0, stages: int = 0, tasks_per_wave: int = 0, order: int = 0):
         _check("tsp_plan_set_variant", load()[1].tsp_plan_set_variant(self.p, bm, w, stages, tasks_per_wave,
                                                                       order))
+
+    def set_format(self, bm: int, fmt: int):
+        """1 = dense tiles, 2 = bitmap-packed (8-/16-row classes)."""
+        _check("tsp_plan_set_format", load()[1].tsp_plan_set_format(self.p, bm, fmt))
+
+    def get_format(self, bm: int) -> int:
+        return load()[1].tsp_plan_get_format(self.p, bm)
 
     def run(self, zero_c: bool = True):
         _check("tsp_plan_run", load()[1].tsp_plan_run(self.p, int(zero_c)))

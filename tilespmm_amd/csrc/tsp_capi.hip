@@ -71,7 +71,7 @@ int tsp_kernel_probe(int bm, int prec, int colB_p, tsp_kernel_info *out)
     if (!out || (bm != 64 && bm != 16 && bm != 8) || (prec != 0 && prec != 1)) return TSP_EINVAL;
     if (colB_p != 32 && (colB_p <= 0 || colB_p % 64)) return TSP_EINVAL;
     const int w = tsp::default_chunk_width(bm, colB_p);
-    const void *k = tsp::select_kernel(bm, prec, w, tsp::default_stages(bm, prec, w));
+    const void *k = tsp::select_kernel(bm, prec, w, tsp::default_stages(bm, prec, w), false);
     if (!k) return TSP_EINVAL;
     hipFuncAttributes a;
     hipError_t e = hipFuncGetAttributes(&a, k);
@@ -169,8 +169,26 @@ int tsp_spmm_launch(int bm, int prec, int rowblkblock, int colB_p, const void *d
     if (rowblkblock < 0 || c_rows < 0) return TSP_EINVAL;
     if (rowblkblock == 0) return TSP_OK;
     if (!d_val || !d_rows || !d_colstart || !d_B || !d_C || !d_colidx) return TSP_EINVAL;
-    return tsp::launch(bm, prec, rowblkblock, colB_p, d_val, d_rows, d_colstart, d_B, d_C,
-                       d_colidx, c_rows, (hipStream_t)stream, 0, 0, 0, 0);
+    return tsp::launch(bm, prec, rowblkblock, colB_p, d_val, nullptr, nullptr, d_rows, d_colstart,
+                       d_B, d_C, d_colidx, c_rows, (hipStream_t)stream, 0, 0, 0, 0);
+}
+
+int tsp_spmm_launch_packed(int bm, int prec, int rowblkblock, int colB_p, const void *d_pval,
+                           const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,
+                           const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,
+                           int c_rows, void *stream, int w, int stages, int tasks_per_wave, int order)
+{
+    if (bm != 16 && bm != 8) return TSP_EINVAL;
+    if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
+    if (colB_p != 32 && (colB_p <= 0 || colB_p % 64 != 0)) return TSP_EINVAL;
+    if (rowblkblock < 0 || c_rows < 0) return TSP_EINVAL;
+    if (w > 0 && (colB_p % w != 0 || !tsp::valid_variant(bm, w, stages > 0 ? stages : 1))) return TSP_EINVAL;
+    if (rowblkblock == 0) return TSP_OK;
+    if (!d_pval || !d_bitmap || !d_vptr || !d_rows || !d_colstart || !d_B || !d_C || !d_colidx)
+        return TSP_EINVAL;
+    return tsp::launch(bm, prec, rowblkblock, colB_p, d_pval, d_bitmap, d_vptr, d_rows, d_colstart,
+                       d_B, d_C, d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave,
+                       order);
 }
 
 int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
@@ -185,8 +203,9 @@ int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p, const
     if (w > 0 && (colB_p % w != 0 || !tsp::valid_variant(bm, w, stages > 0 ? stages : 1))) return TSP_EINVAL;
     if (rowblkblock == 0) return TSP_OK;
     if (!d_val || !d_rows || !d_colstart || !d_B || !d_C || !d_colidx) return TSP_EINVAL;
-    return tsp::launch(bm, prec, rowblkblock, colB_p, d_val, d_rows, d_colstart, d_B, d_C,
-                       d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave, order);
+    return tsp::launch(bm, prec, rowblkblock, colB_p, d_val, nullptr, nullptr, d_rows, d_colstart,
+                       d_B, d_C, d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave,
+                       order);
 }
 
 int tsp_switch_v64(int prec, int rowblkblock, int colB_p, const void *d_val, const unsigned *d_rows,

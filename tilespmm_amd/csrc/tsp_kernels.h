@@ -21,13 +21,14 @@ int default_chunk_width(int bm, int colB_p);
 int default_stages(int bm, int prec, int w);
 int default_tasks_per_wave(int ntasks, int nchunks);
 bool valid_variant(int bm, int w, int s);
-const void *select_kernel(int bm, int prec, int w, int s);
+const void *select_kernel(int bm, int prec, int w, int s, bool packed);
 int default_chunk_major(int bm, int prec, int colB_p, int w);
 // w, s, tpw <= 0 select the defaults; order 0 = default, 1 = chunks of one
-// task range adjacent, 2 = chunk-major.
-int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const unsigned *rows,
-           const int *colstart, const void *B, float *C, const int *colidx, int c_rows,
-           hipStream_t st, int w, int s, int tpw, int order);
+// task range adjacent, 2 = chunk-major.  bmp != nullptr selects the
+// bitmap-packed A format (val = packed values, vptr = per-tile offsets).
+int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint64_t *bmp,
+           const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
+           const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order);
 int launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
 
 }  // namespace tsp

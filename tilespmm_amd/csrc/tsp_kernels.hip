@@ -80,9 +80,15 @@ __device__ __forceinline__ int xcd_remap(int b, int nb)
     return x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
 }
 
-template <int BM, int W, int PREC, int S>
+// PK selects the bitmap-packed A format (8- and 16-row classes): per tile a
+// row-major occupancy bitmap (BM*BN bits, bit r*BN+c) in `bmp`, and the values
+// of its set bits, in bit order, at `val_` + vptr[tile].  Each lane expands its
+// slice of the tile into MFMA operand registers.  Without PK, `val_` holds
+// dense canonical tiles and `bmp` / `vptr` are unused.
+template <int BM, int W, int PREC, int S, bool PK>
 __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     int ntasks, int nchunks, int tasks_per_wave, int chunk_major, const void *__restrict__ val_,
+    const uint64_t *__restrict__ bmp, const int *__restrict__ vptr,
     const unsigned *__restrict__ rows, const int *__restrict__ colstart,
     const void *__restrict__ B_, float *__restrict__ C, const int *__restrict__ colidx, int ld,
     int c_rows)
@@ -142,7 +148,62 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
 #pragma unroll
         for (int c = 0; c < CB; ++c) acc[g][c] = f4{0.f, 0.f, 0.f, 0.f};
 
+    auto load_a_packed = [&](int t, uint32_t (&dst)[RG][AW]) {
+        static_assert(!PK || BM <= 16, "packed tiles are 8- or 16-row");
+        constexpr int WD = BM * BN / 64;         // bitmap words per tile
+        constexpr int NVAL = F16 ? 4 : KS;       // operand values per lane
+        uint64_t bw[WD];
+#pragma unroll
+        for (int w = 0; w < WD; ++w) bw[w] = uload(bmp, (size_t)t * WD + w);
+        const int vbase = uload(vptr, t);
+        if (BM == 8 && ln >= 8) {
+#pragma unroll
+            for (int w = 0; w < AW; ++w) dst[0][w] = 0u;
+            return;
+        }
+        // first bit of this lane's slots; NVAL-bit groups never straddle words
+        const int p = ln * BN + NVAL * lq;
+        int pre = 0;
+        uint64_t word = bw[0];
+#pragma unroll
+        for (int w = 0; w < WD; ++w) {
+            const int lo = 64 * w;
+            const uint64_t m = p >= lo + 64 ? ~0ull : (p <= lo ? 0ull : ((1ull << (p - lo)) - 1ull));
+            pre += __popcll(bw[w] & m);
+            if (p >= lo && p < lo + 64) word = bw[w];
+        }
+        const unsigned nib = (unsigned)(word >> (p & 63)) & ((1u << NVAL) - 1u);
+        // the lane's values are consecutive in the packed stream (the value
+        // array is padded, so reading NVAL of them is always in bounds)
+        const VT *pv = val + vbase + pre;
+        VT v[NVAL], o[NVAL];
+#pragma unroll
+        for (int j = 0; j < NVAL; ++j) v[j] = pv[j];
+        int idx = 0;
+#pragma unroll
+        for (int j = 0; j < NVAL; ++j) {
+            const bool b = (nib >> j) & 1u;
+            VT x = v[0];
+#pragma unroll
+            for (int q = 1; q < NVAL; ++q) x = idx == q ? v[q] : x;
+            o[j] = b ? x : (VT)0;
+            idx += b ? 1 : 0;
+        }
+        if constexpr (F16) {
+            const h4 hv = h4{o[0], o[1], o[2], o[3]};
+            const u2 bits = __builtin_bit_cast(u2, hv);
+            dst[0][0] = bits.x;
+            dst[0][1] = bits.y;
+        } else {
+#pragma unroll
+            for (int j = 0; j < NVAL; ++j) dst[0][j] = round_tf32_bits(__float_as_uint(o[j]));
+        }
+    };
     auto load_a = [&](int t, uint32_t (&dst)[RG][AW]) {
+        if constexpr (PK) {
+            load_a_packed(t, dst);
+            return;
+        }
         const VT *tile = val + (size_t)t * (BM * BN);
 #pragma unroll
         for (int g = 0; g < RG; ++g) {
@@ -365,13 +426,27 @@ bool valid_variant(int bm, int w, int s)
     X(8, 64, 1) X(8, 64, 2) X(8, 64, 3) X(8, 64, 4)                                            \
     X(8, 128, 1) X(8, 128, 2) X(8, 128, 3) X(8, 128, 4)
 
-const void *select_kernel(int bm, int prec, int w, int s)
+#define TSP_FOR_EACH_PACKED_VARIANT(X)                                                         \
+    X(16, 32, 1) X(16, 32, 2) X(16, 32, 3) X(16, 32, 4)                                        \
+    X(16, 64, 1) X(16, 64, 2) X(16, 64, 3) X(16, 64, 4)                                        \
+    X(16, 128, 1) X(16, 128, 2) X(16, 128, 3) X(16, 128, 4)                                    \
+    X(8, 32, 1) X(8, 32, 2) X(8, 32, 3) X(8, 32, 4)                                            \
+    X(8, 64, 1) X(8, 64, 2) X(8, 64, 3) X(8, 64, 4)                                            \
+    X(8, 128, 1) X(8, 128, 2) X(8, 128, 3) X(8, 128, 4)
+
+const void *select_kernel(int bm, int prec, int w, int s, bool packed)
 {
-#define TSP_K(BMv, Wv, Sv)                                                                     \
-    if (bm == BMv && w == Wv && s == Sv)                                                       \
-        return prec == TSP_PREC_FP16 ? (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv>  \
-                                     : (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv>;
+#define TSP_K(BMv, Wv, Sv)                                                                            \
+    if (!packed && bm == BMv && w == Wv && s == Sv)                                                   \
+        return prec == TSP_PREC_FP16 ? (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, false>  \
+                                     : (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, false>;
     TSP_FOR_EACH_VARIANT(TSP_K)
+#undef TSP_K
+#define TSP_K(BMv, Wv, Sv)                                                                            \
+    if (packed && bm == BMv && w == Wv && s == Sv)                                                    \
+        return prec == TSP_PREC_FP16 ? (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, true>   \
+                                     : (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, true>;
+    TSP_FOR_EACH_PACKED_VARIANT(TSP_K)
 #undef TSP_K
     return nullptr;
 }
@@ -407,10 +482,12 @@ int default_chunk_major(int bm, int prec, int colB_p, int w)
     return 0;
 }
 
-int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const unsigned *rows,
-           const int *colstart, const void *B, float *C, const int *colidx, int c_rows,
-           hipStream_t st, int w, int s, int tpw, int order)
+int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint64_t *bmp,
+           const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
+           const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order)
 {
+    const bool packed = bmp != nullptr;
+    if (packed && (bm == 64 || !vptr)) return TSP_EINVAL;
     if (w <= 0) w = default_chunk_width(bm, colB_p);
     if (colB_p % w != 0) return TSP_EINVAL;
     if (s <= 0) s = default_stages(bm, prec, w);
@@ -424,17 +501,24 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const unsi
     if (blocks <= 0) return 0;
     if (blocks > 0x7fffffffLL) return TSP_EINVAL;
     const dim3 grid((unsigned)blocks);
-#define TSP_L(BMv, Wv, Sv)                                                                      \
-    if (bm == BMv && w == Wv && s == Sv) {                                                      \
+#define TSP_L(BMv, Wv, Sv, PKv)                                                                 \
+    if (packed == PKv && bm == BMv && w == Wv && s == Sv) {                                     \
         if (prec == TSP_PREC_FP16)                                                              \
-            spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv><<<grid, kBlockThreads, 0, st>>>(             \
-                ntasks, nchunks, tpw, cm, val, rows, colstart, B, C, colidx, colB_p, c_rows);    \
+            spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, PKv><<<grid, kBlockThreads, 0, st>>>(        \
+                ntasks, nchunks, tpw, cm, val, bmp, vptr, rows, colstart, B, C, colidx, colB_p, \
+                c_rows);                                                                        \
         else                                                                                    \
-            spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv><<<grid, kBlockThreads, 0, st>>>(             \
-                ntasks, nchunks, tpw, cm, val, rows, colstart, B, C, colidx, colB_p, c_rows);    \
+            spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, PKv><<<grid, kBlockThreads, 0, st>>>(        \
+                ntasks, nchunks, tpw, cm, val, bmp, vptr, rows, colstart, B, C, colidx, colB_p, \
+                c_rows);                                                                        \
         return (int)hipGetLastError();                                                          \
     }
-    TSP_FOR_EACH_VARIANT(TSP_L)
+#define TSP_LD(BMv, Wv, Sv) TSP_L(BMv, Wv, Sv, false)
+#define TSP_LP(BMv, Wv, Sv) TSP_L(BMv, Wv, Sv, true)
+    TSP_FOR_EACH_VARIANT(TSP_LD)
+    TSP_FOR_EACH_PACKED_VARIANT(TSP_LP)
+#undef TSP_LD
+#undef TSP_LP
 #undef TSP_L
     return TSP_EINVAL;
 }

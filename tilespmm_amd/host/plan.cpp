@@ -32,6 +32,10 @@ struct ClassDev {
     int th = 0;
     int ntasks = 0;
     int var_w = 0, var_s = 0, var_tpw = 0, var_order = 0;   // kernel variant, 0 = library default
+    int fmt = 1;                  // A format on the device: 1 dense tiles, 2 bitmap-packed
+    void *d_pval = nullptr;       // packed values (+4 elements of padding)
+    uint64_t *d_bmp = nullptr;    // per-tile occupancy bitmaps
+    int *d_vptr = nullptr;        // per-tile offset into d_pval
     void *stream = nullptr;
     std::map<int, std::pair<std::vector<unsigned>, std::vector<int>>> cache;
     bool active() const { return m && m->tilenum > 0; }
@@ -102,15 +106,105 @@ static int upload_schedule(tsp_plan *p, ClassDev &c, int th)
     return TSP_OK;
 }
 
+// Bitmap-packed A: per tile the canonical tile's occupancy bitmap plus the
+// values at its set bits in bit (row-major) order.  Chosen for 8- and 16-row
+// classes when it moves fewer bytes than the dense zero-padded tiles.
+static size_t packed_bytes(const Tile_matrix *m, size_t vs, long long *nvals)
+{
+    const size_t words = (size_t)m->tilenum * m->bitmap_words;
+    long long n = 0;
+#pragma omp parallel for reduction(+ : n)
+    for (long long i = 0; i < (long long)words; ++i) n += __builtin_popcountll(m->tile_bitmap[i]);
+    *nvals = n;
+    return (size_t)n * vs + words * 8 + (size_t)m->tilenum * 4;
+}
+
+static int upload_packed(tsp_plan *p, ClassDev &c)
+{
+    if (c.d_pval) return TSP_OK;
+    const Tile_matrix *m = c.m;
+    const size_t vs = tsph::val_size(p->prec);
+    const int nt = m->tilenum, wd = m->bitmap_words, slots = m->bm * m->bn;
+    std::vector<int> vptr((size_t)nt + 1);
+    std::vector<int> cnt((size_t)nt);
+#pragma omp parallel for
+    for (int t = 0; t < nt; ++t) {
+        int k = 0;
+        for (int w = 0; w < wd; ++w) k += __builtin_popcountll(m->tile_bitmap[(size_t)t * wd + w]);
+        cnt[(size_t)t] = k;
+    }
+    long long run = 0;
+    for (int t = 0; t < nt; ++t) {
+        vptr[(size_t)t] = (int)run;
+        run += cnt[(size_t)t];
+    }
+    if (run > 0x7ffffff0LL) return TSP_EINVAL;
+    vptr[(size_t)nt] = (int)run;
+    std::vector<char> pv(vs * ((size_t)run + 4), 0);
+    const char *dense = (const char *)m->Blockdense_Val;
+#pragma omp parallel for schedule(dynamic, 1024)
+    for (int t = 0; t < nt; ++t) {
+        size_t o = (size_t)vptr[(size_t)t];
+        for (int s = 0; s < slots; ++s)
+            if ((m->tile_bitmap[(size_t)t * wd + s / 64] >> (s % 64)) & 1ull) {
+                memcpy(pv.data() + vs * o, dense + vs * ((size_t)t * slots + s), vs);
+                ++o;
+            }
+    }
+    TSP_TRY(tsp_malloc(&c.d_pval, pv.size()));
+    TSP_TRY(tsp_memcpy_h2d(c.d_pval, pv.data(), pv.size()));
+    TSP_TRY(tsp_malloc((void **)&c.d_bmp, sizeof(uint64_t) * (size_t)nt * wd));
+    TSP_TRY(tsp_memcpy_h2d(c.d_bmp, m->tile_bitmap, sizeof(uint64_t) * (size_t)nt * wd));
+    TSP_TRY(tsp_malloc((void **)&c.d_vptr, sizeof(int) * ((size_t)nt + 1)));
+    TSP_TRY(tsp_memcpy_h2d(c.d_vptr, vptr.data(), sizeof(int) * ((size_t)nt + 1)));
+    return TSP_OK;
+}
+
+static int upload_dense(tsp_plan *p, ClassDev &c)
+{
+    if (c.d_val) return TSP_OK;
+    const size_t vs = tsph::val_size(p->prec);
+    TSP_TRY(tsp_malloc(&c.d_val, vs * c.m->dnssize));
+    return tsp_memcpy_h2d(c.d_val, c.m->Blockdense_Val, vs * c.m->dnssize);
+}
+
 static int launch_class(tsp_plan *p, ClassDev &c)
 {
     if (!c.active() || c.ntasks == 0) return TSP_OK;
+    if (c.fmt == 2)
+        return tsp_spmm_launch_packed(c.bm, p->prec, c.ntasks, p->colB_p, c.d_pval, c.d_bmp, c.d_vptr,
+                                      c.d_rows, c.d_colstart, p->d_B, p->d_C, c.d_colidx, p->rowA,
+                                      c.stream, c.var_w, c.var_s, c.var_tpw, c.var_order);
     if (c.var_w || c.var_s || c.var_tpw || c.var_order)
         return tsp_spmm_launch_variant(c.bm, p->prec, c.ntasks, p->colB_p, c.d_val, c.d_rows,
                                        c.d_colstart, p->d_B, p->d_C, c.d_colidx, p->rowA, c.stream,
                                        c.var_w, c.var_s, c.var_tpw, c.var_order);
     return tsp_spmm_launch(c.bm, p->prec, c.ntasks, p->colB_p, c.d_val, c.d_rows, c.d_colstart,
                            p->d_B, p->d_C, c.d_colidx, p->rowA, c.stream);
+}
+
+extern "C" int tsp_plan_set_format(tsp_plan *p, int bm, int fmt)
+{
+    if (!p || fmt < 0 || fmt > 2) return TSP_EINVAL;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) {
+            if (!c.active()) return TSP_OK;
+            if (fmt == 0) fmt = c.fmt;
+            if (fmt == 2 && bm == 64) return TSP_EINVAL;
+            TSP_TRY(tsp_device_sync());
+            TSP_TRY(fmt == 2 ? upload_packed(p, c) : upload_dense(p, c));
+            c.fmt = fmt;
+            return TSP_OK;
+        }
+    return TSP_EINVAL;
+}
+
+extern "C" int tsp_plan_get_format(tsp_plan *p, int bm)
+{
+    if (!p) return -1;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) return c.active() ? c.fmt : 0;
+    return -1;
 }
 
 extern "C" int tsp_plan_set_variant(tsp_plan *p, int bm, int w, int stages, int tasks_per_wave,
@@ -135,6 +229,9 @@ extern "C" int tsp_plan_destroy(tsp_plan *p)
     tsp_device_sync();
     for (ClassDev &c : p->cls) {
         tsp_free(c.d_val);
+        tsp_free(c.d_pval);
+        tsp_free(c.d_bmp);
+        tsp_free(c.d_vptr);
         tsp_free(c.d_colidx);
         tsp_free(c.d_rows);
         tsp_free(c.d_colstart);
@@ -181,8 +278,11 @@ extern "C" int tsp_plan_create(tsp_plan **out, int device_id, Tile_matrix *m64, 
         if (!c.active()) continue;
         if (c.m->bm != bms[i] || c.m->prec != prec || c.m->bn != tsp_tile_bn(bms[i], prec)) return fail(TSP_EINVAL);
         const size_t nt = (size_t)c.m->tilenum;
-        if ((st = tsp_malloc(&c.d_val, vs * c.m->dnssize))) return fail(st);
-        if ((st = tsp_memcpy_h2d(c.d_val, c.m->Blockdense_Val, vs * c.m->dnssize))) return fail(st);
+        // A format: bitmap-packed when it moves at most 3/4 of the dense bytes
+        long long nvals = 0;
+        const size_t pbytes = c.bm != 64 ? packed_bytes(c.m, vs, &nvals) : 0;
+        c.fmt = (c.bm != 64 && pbytes * 4 <= vs * c.m->dnssize * 3) ? 2 : 1;
+        if ((st = c.fmt == 2 ? upload_packed(p.get(), c) : upload_dense(p.get(), c))) return fail(st);
         if ((st = tsp_malloc((void **)&c.d_colidx, sizeof(int) * nt * c.m->bn))) return fail(st);
         if ((st = tsp_memcpy_h2d(c.d_colidx, c.m->tile_colidx, sizeof(int) * nt * c.m->bn))) return fail(st);
         c.cap_tasks = (long long)c.m->tilem + c.m->tilenum;
