@@ -163,6 +163,7 @@ def main():
         k_rows = int(np.unique(t.arrays()["tile_colidx"]).size)
         b = alg_bytes(sb.rows, sb.nnz, s, k_rows, colB, s)
         cls[bm] = {"ms": cms, "rows": sb.rows, "nnz": int(sb.nnz), "tiles": t.tilenum,
+                   "format": {1: "dense", 2: "packed"}.get(plan.get_format(bm), "?"),
                    "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9}
     dom = max(cls, key=lambda k: cls[k]["ms"])
     k_all = int(np.unique(A.colidx).size)

@@ -33,6 +33,7 @@ struct ClassDev {
     int ntasks = 0;
     int var_w = 0, var_s = 0, var_tpw = 0, var_order = 0;   // kernel variant, 0 = library default
     int fmt = 1;                  // A format on the device: 1 dense tiles, 2 bitmap-packed
+    bool pack_ok = false;         // packed format is worth trying (fewer bytes)
     void *d_pval = nullptr;       // packed values (+4 elements of padding)
     uint64_t *d_bmp = nullptr;    // per-tile occupancy bitmaps
     int *d_vptr = nullptr;        // per-tile offset into d_pval
@@ -278,11 +279,13 @@ extern "C" int tsp_plan_create(tsp_plan **out, int device_id, Tile_matrix *m64, 
         if (!c.active()) continue;
         if (c.m->bm != bms[i] || c.m->prec != prec || c.m->bn != tsp_tile_bn(bms[i], prec)) return fail(TSP_EINVAL);
         const size_t nt = (size_t)c.m->tilenum;
-        // A format: bitmap-packed when it moves at most 3/4 of the dense bytes
+        // Dense tiles first; the bitmap-packed format is a tuning candidate
+        // when it moves at most 3/4 of the dense bytes (8/16-row classes).
         long long nvals = 0;
         const size_t pbytes = c.bm != 64 ? packed_bytes(c.m, vs, &nvals) : 0;
-        c.fmt = (c.bm != 64 && pbytes * 4 <= vs * c.m->dnssize * 3) ? 2 : 1;
-        if ((st = c.fmt == 2 ? upload_packed(p.get(), c) : upload_dense(p.get(), c))) return fail(st);
+        c.pack_ok = c.bm != 64 && pbytes * 4 <= vs * c.m->dnssize * 3;
+        c.fmt = 1;
+        if ((st = upload_dense(p.get(), c))) return fail(st);
         if ((st = tsp_malloc((void **)&c.d_colidx, sizeof(int) * nt * c.m->bn))) return fail(st);
         if ((st = tsp_memcpy_h2d(c.d_colidx, c.m->tile_colidx, sizeof(int) * nt * c.m->bn))) return fail(st);
         c.cap_tasks = (long long)c.m->tilem + c.m->tilenum;
@@ -419,23 +422,32 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
         t3 = now_ms();
     }
     if (tune) {
-        // Column-chunk order per class (MI355X addition): chunks of one task
-        // side by side share A tiles in L2, chunk-major shrinks the live B
-        // working set per phase; which wins depends on |B| against the
-        // MALL and on the tile class, so measure both.
-        for (ClassDev &c : p->cls) {
+        // MI355X additions, measured per class: the A format (dense tiles or
+        // bitmap-packed -- fewer bytes against a per-lane decode) and the
+        // column-chunk order (chunks of one task side by side share A tiles
+        // in L2; chunk-major shrinks the live B working set per phase).
+        // Which wins depends on the matrix, |B| against the MALL and the
+        // class, so both are timed.
+        for (int i = 0; i < 3; ++i) {
+            ClassDev &c = p->cls[i];
             if (!c.active() || c.ntasks == 0 || c.var_w || c.var_order) continue;
             tsp_kernel_info k;
             TSP_TRY(tsp_kernel_probe(c.bm, p->prec, p->colB_p, &k));
-            if (p->colB_p / k.cols_per_task < 2) continue;
-            double ms[2] = {0, 0};
-            for (int o = 1; o <= 2; ++o) {
-                c.var_order = o;
-                double warm = 0;
-                TSP_TRY(tsp_plan_time_class(p, c.bm, 3, &warm));
-                TSP_TRY(tsp_plan_time_class(p, c.bm, 10, &ms[o - 1]));
+            const bool chunks = p->colB_p / k.cols_per_task >= 2;
+            double best_ms = 1e30;
+            int best_fmt = 1, best_order = 0;
+            for (int fmt = 1; fmt <= (c.pack_ok ? 2 : 1); ++fmt) {
+                TSP_TRY(tsp_plan_set_format(p, c.bm, fmt));
+                for (int o = chunks ? 1 : 0; o <= (chunks ? 2 : 0); ++o) {
+                    c.var_order = o;
+                    double warm = 0, ms = 0;
+                    TSP_TRY(tsp_plan_time_class(p, c.bm, 3, &warm));
+                    TSP_TRY(tsp_plan_time_class(p, c.bm, 10, &ms));
+                    if (ms < best_ms) { best_ms = ms; best_fmt = fmt; best_order = o; }
+                }
             }
-            c.var_order = ms[1] < ms[0] ? 2 : 1;
+            TSP_TRY(tsp_plan_set_format(p, c.bm, best_fmt));
+            c.var_order = best_order;
         }
         t3 = now_ms();
     }

@@ -365,9 +365,124 @@ def cmd_check(args):
         print(f"mean slowdown vs exhaustive optimum: x{np.mean(tot):.3f}, worst x{np.max(tot):.3f}")
 
 
+# ---------------------------------------------------------------------------
+# threshold (TH) cost model calibration
+# ---------------------------------------------------------------------------
+def cmd_thsweep(args):
+    """Per matrix / colB / precision and per active class: the time of the
+    class kernel at every threshold TH = 8..128 (distinct task counts only),
+    plus the class's tile-length histogram and the probed resources, so the
+    cost model can be re-evaluated offline for any lambda."""
+    tsp.load()
+    if not tsp.device_available():
+        raise SystemExit("policy_tune thsweep needs a gfx950 device")
+    mats = [(f"config{cfg}", lambda cfg=cfg: tsp.gen_structure(cfg)) for cfg in args.configs]
+    if args.corpus:
+        mats += corpus(args.corpus)
+    if args.only:
+        mats = [m for m in mats if any(o in m[0] for o in args.only)]
+    with open(args.out, "a") as out:
+        for name, make in mats:
+            rows, cols, rp, ci = make()
+            for prec in args.precs:
+                A = with_values(rows, cols, rp, ci, prec, 11)
+                for colB in args.colBs:
+                    cbp = tsp.colB_padded(colB)
+                    b = np.zeros((A.cols, cbp), dtype=np.float32)
+                    b[:, :colB] = np.random.default_rng(7).uniform(-1, 1, (A.cols, colB))
+                    B = b.astype(np.float16).view(np.uint16) if prec == 0 else b
+                    g, d = tsp.predict(tsp.features(A, 9.5, colB), prec)
+                    subs = tsp.matrix_split(A, g, d)
+                    tiles = [tsp.tile_create(s, A.cols, bm, prec) for s, bm in zip(subs, (64, 16, 8))]
+                    plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
+                    try:
+                        for t, bm in zip(tiles, (64, 16, 8)):
+                            if t.tilenum == 0:
+                                continue
+                            lens = np.diff(t.arrays()["tile_ptr"])
+                            maxlen = int(lens.max())
+                            ths, times, seen = [], [], set()
+                            for th in range(8, min(128, (maxlen + 7) // 8 * 8) + 1, 8):
+                                nt = int(np.where(lens <= th, 1, -(-lens // th)).sum())
+                                if nt in seen:
+                                    continue
+                                seen.add(nt)
+                                plan.set_th(th if bm == 64 else 0, th if bm == 16 else 0, th if bm == 8 else 0)
+                                plan.time_class(bm, 3)
+                                ths.append(th)
+                                times.append(plan.time_class(bm, args.reps))
+                            u, c = np.unique(lens[lens > 0], return_counts=True)
+                            prm = tsp.ThParams()
+                            hip, host = tsp.load()
+                            host.tsp_th_params_probe(0, bm, prec, cbp, C_byref(prm))
+                            rec = {"matrix": name, "prec": prec, "colB": colB, "colB_p": cbp, "bm": bm,
+                                   "tilem": int(len(lens)), "hist_len": u.tolist(), "hist_cnt": c.tolist(),
+                                   "th": ths, "ms": times,
+                                   "params": {f: getattr(prm, f) for f, _ in tsp.ThParams._fields_}}
+                            out.write(json.dumps(rec) + "\n")
+                            out.flush()
+                            best = ths[int(np.argmin(times))]
+                            print(f"{name} prec={prec} colB={colB} bm={bm}: best TH {best}, "
+                                  f"{min(times):.4f} ms ({len(ths)} THs)", flush=True)
+                    finally:
+                        plan.close()
+
+
+def C_byref(x):
+    import ctypes
+    return ctypes.byref(x)
+
+
+def model_top1(rec, lam):
+    """The product cost model (tsp_optimal_th) on a recorded histogram with
+    lambda_atom = lam."""
+    prm = tsp.ThParams(**rec["params"])
+    prm.lambda_atom = lam
+    lens = np.repeat(np.array(rec["hist_len"], dtype=np.int64), rec["hist_cnt"])
+    tp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    _, top4 = tsp.optimal_th(rec["bm"], rec["colB_p"], tp, prm)
+    return int(top4[0])
+
+
+def cmd_thfit(args):
+    tsp.load()
+    recs = [json.loads(l) for l in open(args.inp) if l.strip()]
+    lams = [0.0005, 0.001, 0.002, 0.004, 0.006, 0.008, 0.01, 0.015, 0.02, 0.03, 0.05, 0.08]
+    groups = {}
+    for r in recs:
+        key = (r["bm"], r["prec"], 32 if r["colB_p"] == 32 else 64)
+        groups.setdefault(key, []).append(r)
+    for key, rs in sorted(groups.items()):
+        res = []
+        for lam in lams:
+            reg = []
+            for r in rs:
+                th = model_top1(r, lam)
+                t = dict(zip(r["th"], r["ms"]))
+                # a TH not timed has the task count of the next smaller timed TH
+                cand = max([x for x in r["th"] if x <= th] or [r["th"][0]])
+                reg.append(t[cand] / min(r["ms"]))
+            res.append((float(np.mean(reg)), float(np.max(reg)), lam))
+        best = min(res)
+        cur = [x for x in res if x[2] == rs[0]["params"]["lambda_atom"]]
+        print(f"class bm={key[0]} prec={key[1]} width={'32' if key[2] == 32 else '>=64'}: {len(rs)} cases; "
+              f"best lambda_atom {best[2]} (mean regret x{best[0]:.3f}, worst x{best[1]:.3f})"
+              + (f"; current {cur[0][2]} x{cur[0][0]:.3f}" if cur else ""))
+
+
 def main():
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
+    t = sub.add_parser("thsweep")
+    t.add_argument("--configs", type=int, nargs="*", default=[])
+    t.add_argument("--corpus", choices=["small", "full"], default=None)
+    t.add_argument("--precs", type=int, nargs="*", default=[0, 1])
+    t.add_argument("--colBs", type=int, nargs="*", default=[32, 128])
+    t.add_argument("--reps", type=int, default=20)
+    t.add_argument("--only", nargs="*", default=None)
+    t.add_argument("--out", required=True)
+    tf = sub.add_parser("thfit")
+    tf.add_argument("--inp", required=True)
     s = sub.add_parser("sweep")
     s.add_argument("--configs", type=int, nargs="*", default=[])
     s.add_argument("--corpus", choices=["small", "full"], default=None)
@@ -385,7 +500,8 @@ def main():
     c = sub.add_parser("check")
     c.add_argument("--inp", required=True)
     args = ap.parse_args()
-    {"sweep": cmd_sweep, "fit": cmd_fit, "check": cmd_check}[args.cmd](args)
+    {"sweep": cmd_sweep, "fit": cmd_fit, "check": cmd_check, "thsweep": cmd_thsweep,
+     "thfit": cmd_thfit}[args.cmd](args)
 
 
 if __name__ == "__main__":
