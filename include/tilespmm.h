@@ -124,8 +124,15 @@ typedef struct {
      * (src/csr2tile.h:588-601); the MI355X kernels report theirs through
      * tsp_kernel_probe. */
     int tasks_per_block, cols_per_task;
+    /* weight of the L2 re-read term: lambda_L2 = lambda_l2_scale *
+     * iteration_bytes * cap / l2_bytes.  1.0 is the reference's model;
+     * the probe fills the MI355X calibration. */
+    float lambda_l2_scale;
 } tsp_th_params;
 int tsp_th_params_probe(int device_id, int bm, int prec, int colB_p, tsp_th_params *out);
+/* The MI355X calibration the probe applies: lambda_atom and lambda_l2_scale
+ * for (class, precision, padded colB).  No device needed. */
+int tsp_th_weights(int bm, int prec, int colB_p, float *lambda_atom, float *lambda_l2_scale);
 /* Fills top4 (cheapest first); returns the number of distinct candidates
  * evaluated (>= 1), or a negative value when the resources do not fit. */
 int tsp_optimal_th(int BM, int colB, int tilem, const int *tile_ptr, const tsp_th_params *p,

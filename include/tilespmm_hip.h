@@ -168,6 +168,32 @@ int tsp_vendor_spmm(int prec, int m, int k, long long nnz, const int *rowptr, co
  * calibrate HBM byte counters and the achievable copy bandwidth. */
 int tsp_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
 
+/* ---- CSR -> tiles on the device ------------------------------------------
+ * Device counterpart of Tile_create (src/csr2tile.h:724-795, convert_step1-3
+ * at :15-379) producing the same arrays as the host tsp_tile_create, bit for
+ * bit: tile_ptr[tilem+1], tile_nnz[tilenum+1], tile_colidx[tilenum*BN]
+ * (sorted distinct columns, last tile padded with the last column), val
+ * (canonical row-major BM x BN tiles, duplicates summed in CSR order with the
+ * value type's rounding per add) and the occupancy bitmap.  The schedule and
+ * orig_tile_row_idx stay host work (tsp_tile_pretreatment). */
+typedef struct {
+    int tilem, tilenum, bm, bn, prec, bitmap_words;
+    int *d_tile_ptr;
+    int *d_tile_nnz;
+    int *d_tile_colidx;
+    void *d_val;                /* fp16 or fp32 (tf32 values) */
+    unsigned long long *d_bitmap;
+} tsp_dev_tiles;
+
+/* d_ptr[rows+1], d_idx[nnz], d_val[nnz] (prec-typed) are the class sub-CSR
+ * on the device.  Allocates the output arrays (free with tsp_dev_tiles_free)
+ * and its scratch; synchronises `stream` before returning.  On failure the
+ * outputs are already freed. */
+int tsp_tile_create_device(tsp_dev_tiles *out, int rows, int colA, long long nnz, const int *d_ptr,
+                           const int *d_idx, const void *d_val, int BM, int BN, int prec,
+                           void *stream);
+int tsp_dev_tiles_free(tsp_dev_tiles *t);
+
 #ifdef __cplusplus
 }
 #endif

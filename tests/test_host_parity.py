@@ -150,7 +150,7 @@ def ref_geometry_params(tsp, bm, colB, **kw):
     p = tsp.ThParams(sm_count=132, threads_per_sm=2048, registers_per_sm=65536, blocks_per_sm=32,
                      shared_bytes_per_sm=228 * 1024, l2_bytes=50 * 1024 * 1024, kernel_threads=64,
                      kernel_registers=40, kernel_shared_bytes=4608, iteration_bytes=2 * (bm * 16 + 16 * 64),
-                     lambda_atom=0.01)
+                     lambda_atom=0.01, lambda_l2_scale=1.0)
     p.tasks_per_block = 4 if (colB == 32 and bm in (8, 16)) else 1
     p.cols_per_task = 32 if colB == 32 else 64
     for k, v in kw.items():

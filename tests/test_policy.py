@@ -61,3 +61,35 @@ def test_policy_against_exhaustive_tuning(tsp):
     assert np.mean(slow) <= 1.03 and max(slow) <= 1.25, (np.mean(slow), max(slow))
     prov = [r["times_ms"][24] / r["best_ms"] for r in records()]
     assert np.mean(slow) < np.mean(prov)
+
+
+TH_DATA = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_thsweep.jsonl")
+
+
+def th_regret(tsp, r, lam, l2s):
+    """Measured time of the best of the cost model's top-4 thresholds (what
+    the runtime tuning times) over the best threshold of the sweep."""
+    p = tsp.ThParams(**{k: v for k, v in r["params"].items() if k in dict(tsp.ThParams._fields_)})
+    p.lambda_atom, p.lambda_l2_scale = lam, l2s
+    lens = np.repeat(np.array(r["hist_len"], dtype=np.int64), r["hist_cnt"])
+    tp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    _, top4 = tsp.optimal_th(r["bm"], r["colB_p"], tp, p)
+    t = dict(zip(r["th"], r["ms"]))
+    # a threshold that was not timed has the task count of the next smaller timed one
+    cands = [max([x for x in r["th"] if x <= th] or [r["th"][0]]) for th in top4]
+    return min(t[c] for c in cands) / min(r["ms"])
+
+
+def test_threshold_weights_against_exhaustive_sweep(tsp):
+    """The MI355X cost-model weights (tsp_th_weights) put a threshold within a
+    few percent of the best measured one into the top 4 on every class sweep;
+    the reference's weights (L2 scale 1, per-class lambda_atom table) do not."""
+    recs = [json.loads(l) for l in open(TH_DATA) if l.strip()]
+    assert len(recs) >= 60
+    new, ref = [], []
+    for r in recs:
+        lam, l2s = tsp.th_weights(r["bm"], r["prec"], r["colB_p"])
+        new.append(th_regret(tsp, r, lam, l2s))
+        ref.append(th_regret(tsp, r, r["params"]["lambda_atom"], 1.0))
+    assert np.mean(new) <= 1.01 and max(new) <= 1.10, (np.mean(new), max(new))
+    assert np.mean(ref) > 1.10 and np.mean(new) < np.mean(ref)

@@ -89,6 +89,7 @@ class ThParams(C.Structure):
         ("l2_bytes", C.c_longlong), ("kernel_threads", C.c_int), ("kernel_registers", C.c_int),
         ("kernel_shared_bytes", C.c_longlong), ("iteration_bytes", C.c_int),
         ("lambda_atom", C.c_float), ("tasks_per_block", C.c_int), ("cols_per_task", C.c_int),
+        ("lambda_l2_scale", C.c_float),
     ]
 
 
@@ -107,6 +108,14 @@ class KernelInfo(C.Structure):
         ("threads", C.c_int), ("tasks_per_block", C.c_int), ("registers_per_thread", C.c_int),
         ("shared_bytes", C.c_longlong), ("iteration_bytes", C.c_int), ("cols_per_task", C.c_int),
     ]
+
+
+class DevTiles(C.Structure):
+    """tsp_dev_tiles: device tile arrays made by tsp_tile_create_device."""
+    _fields_ = [("tilem", C.c_int), ("tilenum", C.c_int), ("bm", C.c_int), ("bn", C.c_int),
+                ("prec", C.c_int), ("bitmap_words", C.c_int), ("d_tile_ptr", C.c_void_p),
+                ("d_tile_nnz", C.c_void_p), ("d_tile_colidx", C.c_void_p), ("d_val", C.c_void_p),
+                ("d_bitmap", C.c_void_p)]
 
 
 class RunResult(C.Structure):
@@ -158,6 +167,9 @@ HIP_SYMBOLS = {
                                   C.c_int, _P, _P, C.c_int, C.c_int, C.POINTER(C.c_double),
                                   C.POINTER(C.c_double)]),
     "tsp_copy_kernel": (C.c_int, [_P, _P, C.c_size_t, _P]),
+    "tsp_tile_create_device": (C.c_int, [C.POINTER(DevTiles), C.c_int, C.c_int, C.c_longlong, _P, _P, _P,
+                                         C.c_int, C.c_int, C.c_int, _P]),
+    "tsp_dev_tiles_free": (C.c_int, [C.POINTER(DevTiles)]),
 }
 HOST_SYMBOLS = {
     "tsp_mm_read": (C.c_int, [C.c_char_p, _IP, _IP, C.POINTER(C.c_longlong), _IP,
@@ -175,6 +187,7 @@ HOST_SYMBOLS = {
     "tsp_tile_pretreatment": (C.c_int, [C.POINTER(Tile_matrix), C.c_int, _IP,
                                         C.POINTER(C.POINTER(C.c_uint)), C.POINTER(_IP)]),
     "tsp_th_params_probe": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(ThParams)]),
+    "tsp_th_weights": (C.c_int, [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
     "tsp_optimal_th": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, C.POINTER(ThParams), _P]),
     "tsp_features_from_csr": (C.c_int, [C.c_int, C.c_int, C.c_longlong, _P, C.c_double, C.c_int,
                                         _P]),
@@ -425,6 +438,58 @@ def tile_create(sub, colA: int, bm: int, prec: int, bn: Optional[int] = None) ->
     return t
 
 
+class _DevBuf:
+    """A device buffer holding a copy of a host numpy array."""
+
+    def __init__(self, a: np.ndarray):
+        hip, _ = load()
+        a = np.ascontiguousarray(a)
+        self.p = C.c_void_p()
+        _check("tsp_malloc", hip.tsp_malloc(C.byref(self.p), max(a.nbytes, 16)))
+        if a.nbytes:
+            _check("tsp_memcpy_h2d", hip.tsp_memcpy_h2d(self.p, _ptr(a), a.nbytes))
+
+    def free(self):
+        if self.p:
+            load()[0].tsp_free(self.p)
+            self.p = C.c_void_p()
+
+
+def _d2h(ptr, n, dtype) -> np.ndarray:
+    out = np.zeros(n, dtype=dtype)
+    if n:
+        _check("tsp_memcpy_d2h", load()[0].tsp_memcpy_d2h(_ptr(out), ptr, out.nbytes))
+    return out
+
+
+def tile_create_device(sub, colA: int, bm: int, prec: int, bn: Optional[int] = None) -> dict:
+    """Builds the tiles of one class sub-CSR on the GPU (tsp_tile_create_device)
+    and returns host copies of the arrays, keyed like TileMatrix.arrays()
+    (without orig_tile_row_idx)."""
+    hip, _ = load()
+    bn = tile_bn(bm, prec) if bn is None else bn
+    bufs = [_DevBuf(np.asarray(sub.rowptr, dtype=np.int32)), _DevBuf(np.asarray(sub.colidx, dtype=np.int32)),
+            _DevBuf(np.asarray(sub.val))]
+    t = DevTiles()
+    try:
+        _check("tsp_tile_create_device",
+               hip.tsp_tile_create_device(C.byref(t), sub.rows, colA, sub.nnz, bufs[0].p, bufs[1].p, bufs[2].p,
+                                          bm, bn, prec, None))
+        try:
+            return {
+                "tile_ptr": _d2h(t.d_tile_ptr, t.tilem + 1, np.int32),
+                "tile_nnz": _d2h(t.d_tile_nnz, t.tilenum + 1, np.int32),
+                "tile_colidx": _d2h(t.d_tile_colidx, t.tilenum * bn, np.int32),
+                "dense": _d2h(t.d_val, t.tilenum * bm * bn, _vdtype(prec)),
+                "bitmap": _d2h(t.d_bitmap, t.tilenum * t.bitmap_words, np.uint64),
+            }
+        finally:
+            hip.tsp_dev_tiles_free(C.byref(t))
+    finally:
+        for b in bufs:
+            b.free()
+
+
 def pretreatment(t: TileMatrix, th: int):
     _, host = load()
     n = C.c_int()
@@ -441,6 +506,14 @@ def optimal_th(bm: int, colB: int, tile_ptr: np.ndarray, params: ThParams):
     top4 = np.zeros(4, dtype=np.int32)
     n = host.tsp_optimal_th(bm, colB, len(tp) - 1, _ptr(tp), C.byref(params), _ptr(top4))
     return n, top4
+
+
+def th_weights(bm: int, prec: int, colB_p: int):
+    """(lambda_atom, lambda_l2_scale) of the MI355X threshold calibration."""
+    _, host = load()
+    lam, l2s = C.c_float(), C.c_float()
+    _check("tsp_th_weights", host.tsp_th_weights(bm, prec, colB_p, C.byref(lam), C.byref(l2s)))
+    return lam.value, l2s.value
 
 
 def features(A: Csr, capability: float, colB: int) -> np.ndarray:

@@ -8,7 +8,8 @@
 //               + sum_L cnt(L)(1 - 1/tasks(L)) * lambda_L2
 //               + atom_pen * extra tasks       (atomic traffic)
 //   cap         = resident blocks per CU * CUs
-//   lambda_L2   = iteration_bytes * cap / L2 bytes
+//   lambda_L2   = lambda_l2_scale * iteration_bytes * cap / L2 bytes
+//                 (scale 1 in the reference's model)
 //   atom_pen    = lambda_atom / 32 * colB, x0.04 when max length > 5 x mean
 // consecutive thresholds with the same task count are skipped; the four
 // cheapest survive (stable on ties).  The float arithmetic keeps this order.
@@ -23,18 +24,26 @@
 #include <vector>
 
 #include "common.hpp"
+#include "th_calibration.h"
 
 namespace {
 
-// Atomic-cost weights per (class, precision, width).  The analytic model only
-// uses them relative to the throughput and tail terms; these values are the
-// provisional MI355X calibration (one weight per class; fp32 global atomics
-// are native on gfx950 so split tasks are cheap relative to NVIDIA parts).
-float lambda_atom_mi355x(int bm, int prec, int colB_p)
+// Weights of the atomic and L2 terms for (class, precision, width): the
+// MI355X calibration in th_calibration.h (regret-minimising fit of the
+// model's top-4 against exhaustive per-threshold timings).  On gfx950 the
+// re-read penalty of split row-blocks is close to zero and fp32 global
+// atomics are cheap, so the fitted weights make small thresholds (16-32)
+// win where the reference's weights pick 96-128.
+void th_weights_mi355x(int bm, int prec, int colB_p, float *lambda_atom, float *l2_scale)
 {
-    (void)prec;
-    if (colB_p == 32) return bm == 64 ? 0.016f : bm == 16 ? 0.008f : 0.005f;
-    return bm == 64 ? 0.010f : bm == 16 ? 0.010f : 0.008f;
+    const int wide = colB_p == 32 ? 0 : 1;
+    *lambda_atom = 0.004f;
+    *l2_scale = 1.0f;
+    for (const tsp_th_weight &w : tsp_th_weight_table)
+        if (w.bm == bm && w.prec == prec && w.wide == wide) {
+            *lambda_atom = w.lambda_atom;
+            *l2_scale = w.lambda_l2_scale;
+        }
 }
 
 }  // namespace
@@ -57,7 +66,7 @@ extern "C" int tsp_optimal_th(int BM, int colB, int tilem, const int *tile_ptr,
     if (blk_sm > p->blocks_per_sm) blk_sm = p->blocks_per_sm;
     if (blk_sm <= 0) return -1;
     const float cap = (float)(blk_sm * p->sm_count);
-    const float lambda_L2 = (float)(p->iteration_bytes * cap) / (float)p->l2_bytes;
+    const float lambda_L2 = p->lambda_l2_scale * (float)(p->iteration_bytes * cap) / (float)p->l2_bytes;
     const float atom_per_col = p->lambda_atom * (1.0f / 32.0f);
 
     int max_len = 0;
@@ -122,6 +131,13 @@ extern "C" int tsp_optimal_th(int BM, int colB, int tilem, const int *tile_ptr,
     return (int)c.size();
 }
 
+extern "C" int tsp_th_weights(int bm, int prec, int colB_p, float *lambda_atom, float *lambda_l2_scale)
+{
+    if (!lambda_atom || !lambda_l2_scale || (bm != 64 && bm != 16 && bm != 8)) return TSP_EINVAL;
+    th_weights_mi355x(bm, prec, colB_p, lambda_atom, lambda_l2_scale);
+    return TSP_OK;
+}
+
 extern "C" int tsp_th_params_probe(int device_id, int bm, int prec, int colB_p, tsp_th_params *out)
 {
     if (!out) return TSP_EINVAL;
@@ -142,7 +158,7 @@ extern "C" int tsp_th_params_probe(int device_id, int bm, int prec, int colB_p, 
     out->kernel_registers = k.registers_per_thread > 0 ? k.registers_per_thread : 1;
     out->kernel_shared_bytes = k.shared_bytes;
     out->iteration_bytes = k.iteration_bytes;
-    out->lambda_atom = lambda_atom_mi355x(bm, prec, colB_p);
+    th_weights_mi355x(bm, prec, colB_p, &out->lambda_atom, &out->lambda_l2_scale);
     out->tasks_per_block = k.tasks_per_block;
     out->cols_per_task = k.cols_per_task;
     return TSP_OK;

@@ -433,41 +433,107 @@ def C_byref(x):
     return ctypes.byref(x)
 
 
-def model_top1(rec, lam):
+def model_top4(rec, lam, l2s=None):
     """The product cost model (tsp_optimal_th) on a recorded histogram with
-    lambda_atom = lam."""
-    prm = tsp.ThParams(**rec["params"])
+    lambda_atom = lam (and lambda_l2_scale = l2s when given): its four best
+    thresholds, best first."""
+    prm = tsp.ThParams(**{k: v for k, v in rec["params"].items() if k in dict(tsp.ThParams._fields_)})
     prm.lambda_atom = lam
+    prm.lambda_l2_scale = rec["params"].get("lambda_l2_scale", 1.0) if l2s is None else l2s
     lens = np.repeat(np.array(rec["hist_len"], dtype=np.int64), rec["hist_cnt"])
     tp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     _, top4 = tsp.optimal_th(rec["bm"], rec["colB_p"], tp, prm)
-    return int(top4[0])
+    return [int(x) for x in top4 if int(x) > 0]
+
+
+def th_regret(r, lam, l2s, top):
+    """Measured time of the best of the model's top-`top` thresholds over the
+    best measured time of any threshold."""
+    t = dict(zip(r["th"], r["ms"]))
+    # a TH not timed has the task count of the next smaller timed TH
+    ths = model_top4(r, lam, l2s)[:top]
+    cands = [max([x for x in r["th"] if x <= th] or [r["th"][0]]) for th in ths]
+    return min(t[c] for c in cands) / min(r["ms"])
+
+
+TH_LAMS = [0.0005, 0.001, 0.002, 0.004, 0.008, 0.015, 0.03, 0.08]
+TH_L2S = [0.0, 0.0001, 0.0003, 0.001, 0.003, 0.01, 0.03, 0.1, 0.3, 1.0]
+
+
+def export_th_header(path, table, note):
+    lines = [
+        "// th_calibration.h -- MI355X weights of the split-threshold cost model:",
+        "// lambda_atom and lambda_l2_scale per (row class, precision, width class",
+        "// colB_p == 32 or >= 64), chosen to minimise the measured regret of the",
+        "// model's top-4 thresholds over an exhaustive per-threshold sweep.",
+        "//",
+        f"// GENERATED by tilespmm_amd/policy_tune.py thfit ({note}).",
+        "#pragma once",
+        "",
+        "struct tsp_th_weight {",
+        "    int bm, prec, wide;",
+        "    float lambda_atom, lambda_l2_scale;",
+        "};",
+        "",
+        "static const tsp_th_weight tsp_th_weight_table[] = {",
+    ]
+    for (bm, prec, wide), (lam, l2s) in sorted(table.items()):
+        lines.append(f"    {{{bm}, {prec}, {wide}, {float(lam)!r}f, {float(l2s)!r}f}},")
+    lines += ["};", ""]
+    open(path, "w").write("\n".join(lines))
+
+
+def fit_th_pair(recs, top):
+    """(lambda_atom, lambda_l2_scale) minimising the mean top-k regret over
+    recs; ties -> the larger weights (closer to the reference's model)."""
+    res = []
+    for l2s in TH_L2S:
+        for lam in TH_LAMS:
+            reg = [th_regret(r, lam, l2s, top) for r in recs]
+            res.append((round(float(np.mean(reg)), 4), -l2s, -lam))
+    best = min(res)
+    return -best[2], -best[1]
 
 
 def cmd_thfit(args):
+    """Fits the cost model's (lambda_atom, lambda_l2_scale) on a thsweep file:
+    one pair for all classes by default (per-class fits overfit the small
+    64-row groups), per (class, precision, width) group with --per-group.
+    Reports the top-4 regret in-sample and leave-one-matrix-out; with
+    --header writes the generated calibration table."""
     tsp.load()
     recs = [json.loads(l) for l in open(args.inp) if l.strip()]
-    lams = [0.0005, 0.001, 0.002, 0.004, 0.006, 0.008, 0.01, 0.015, 0.02, 0.03, 0.05, 0.08]
+    keyf = lambda r: (r["bm"], r["prec"], 0 if r["colB_p"] == 32 else 1)
     groups = {}
     for r in recs:
-        key = (r["bm"], r["prec"], 32 if r["colB_p"] == 32 else 64)
-        groups.setdefault(key, []).append(r)
+        groups.setdefault(keyf(r), []).append(r)
+
+    def fit(rs):
+        if not args.per_group:
+            pair = fit_th_pair(rs, args.top)
+            return {k: pair for k in groups}
+        return {k: fit_th_pair([r for r in rs if keyf(r) == k] or rs, args.top) for k in groups}
+
+    table = fit(recs)
+    new = [th_regret(r, *table[keyf(r)], args.top) for r in recs]
+    cur = [th_regret(r, r["params"]["lambda_atom"], None, args.top) for r in recs]
+    lomo = []
+    for m in sorted(set(r["matrix"] for r in recs)):
+        t = fit([r for r in recs if r["matrix"] != m])
+        lomo += [th_regret(r, *t[keyf(r)], args.top) for r in recs if r["matrix"] == m]
     for key, rs in sorted(groups.items()):
-        res = []
-        for lam in lams:
-            reg = []
-            for r in rs:
-                th = model_top1(r, lam)
-                t = dict(zip(r["th"], r["ms"]))
-                # a TH not timed has the task count of the next smaller timed TH
-                cand = max([x for x in r["th"] if x <= th] or [r["th"][0]])
-                reg.append(t[cand] / min(r["ms"]))
-            res.append((float(np.mean(reg)), float(np.max(reg)), lam))
-        best = min(res)
-        cur = [x for x in res if x[2] == rs[0]["params"]["lambda_atom"]]
-        print(f"class bm={key[0]} prec={key[1]} width={'32' if key[2] == 32 else '>=64'}: {len(rs)} cases; "
-              f"best lambda_atom {best[2]} (mean regret x{best[0]:.3f}, worst x{best[1]:.3f})"
-              + (f"; current {cur[0][2]} x{cur[0][0]:.3f}" if cur else ""))
+        g = [th_regret(r, *table[key], args.top) for r in rs]
+        print(f"class bm={key[0]} prec={key[1]} width={'32' if key[2] == 0 else '>=64'}: {len(rs)} cases; "
+              f"lambda_atom {table[key][0]} l2_scale {table[key][1]}: mean x{np.mean(g):.3f} "
+              f"worst x{np.max(g):.3f}")
+    note = (f"{len(recs)} class sweeps, {'per-group' if args.per_group else 'pooled'} fit, top-{args.top} "
+            f"regret mean x{np.mean(new):.3f} worst x{np.max(new):.3f}, leave-one-matrix-out mean "
+            f"x{np.mean(lomo):.3f} worst x{np.max(lomo):.3f}; as recorded mean x{np.mean(cur):.3f} "
+            f"worst x{np.max(cur):.3f}")
+    print(note)
+    if args.header:
+        export_th_header(args.header, table, note)
+        print("wrote", args.header)
 
 
 def main():
@@ -482,7 +548,11 @@ def main():
     t.add_argument("--only", nargs="*", default=None)
     t.add_argument("--out", required=True)
     tf = sub.add_parser("thfit")
+    tf.add_argument("--top", type=int, default=4,
+                    help="regret of the best measured among the model's top-k (the plan tunes k=4)")
     tf.add_argument("--inp", required=True)
+    tf.add_argument("--header", default=None, help="write the calibration table (host/th_calibration.h)")
+    tf.add_argument("--per-group", action="store_true", help="one weight pair per (class, prec, width)")
     s = sub.add_parser("sweep")
     s.add_argument("--configs", type=int, nargs="*", default=[])
     s.add_argument("--corpus", choices=["small", "full"], default=None)
