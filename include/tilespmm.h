@@ -171,6 +171,15 @@ int tsp_colB_padded(int colB);
 typedef struct tsp_plan tsp_plan;
 int tsp_plan_create(tsp_plan **plan, int device_id, Tile_matrix *m64, Tile_matrix *m16,
                     Tile_matrix *m8, int rowA, int colA, int colB_p, int prec, const void *h_B);
+/* The same plan from the three class sub-CSRs (matrix_split outputs, NULL
+ * or rows == 0 for an empty class): Tile_create runs on the device
+ * (tsp_tile_create_device, bit-identical to tsp_tile_create) instead of the
+ * host, and only tile_ptr / orig_tile_row_idx / the schedule stay on the
+ * host.  *tile_ms (optional) = wall time of the sub-CSR upload + device
+ * conversion. */
+int tsp_plan_create_csr(tsp_plan **plan, int device_id, const tsp_sub_csr *s64,
+                        const tsp_sub_csr *s16, const tsp_sub_csr *s8, int rowA, int colA,
+                        int colB_p, int prec, const void *h_B, double *tile_ms);
 /* Build + upload schedules for the three classes (a TH <= 0 keeps the
  * current one). */
 int tsp_plan_set_th(tsp_plan *plan, int th64, int th16, int th8);
@@ -216,6 +225,14 @@ int tsp_call_tilespmm(int device_id, Tile_matrix *m64, Tile_matrix *m16, Tile_ma
                       int colA, int colB_p, long long total_nnz, int prec, const void *h_B,
                       float *h_C, double cpu_pre_time_ms, int logical_colB, int repeat, int tune,
                       FILE *csv, tsp_run_result *out);
+/* The steps of tsp_call_tilespmm after the plan exists (tune, warmup,
+ * result run, download, timed loop, CSV fields 11-16), for a plan from
+ * tsp_plan_create or tsp_plan_create_csr.  cpu_pre_time_ms is the caller's
+ * preprocessing time, to which the plan adds its model and tuning time. */
+int tsp_plan_execute(tsp_plan *plan, long long total_nnz, float *h_C, double cpu_pre_time_ms,
+                     int logical_colB, int repeat, int tune, FILE *csv, tsp_run_result *out);
+/* Tile count of one class of the plan (-1 on a bad argument). */
+int tsp_plan_tilenum(tsp_plan *plan, int bm);
 
 #ifdef __cplusplus
 }

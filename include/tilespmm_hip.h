@@ -194,6 +194,16 @@ int tsp_tile_create_device(tsp_dev_tiles *out, int rows, int colA, long long nnz
                            void *stream);
 int tsp_dev_tiles_free(tsp_dev_tiles *t);
 
+/* Bitmap-packed A on the device (the format tsp_spmm_launch_packed reads):
+ * *nvals = set bits over all tiles; when d_pval/d_vptr are non-NULL also
+ * allocates and fills d_vptr[tilenum+1] (per-tile offsets) and d_pval
+ * (values at the set bits in row-major bit order, + 4 zero elements).
+ * d_val/d_bitmap as in tsp_dev_tiles.  No reference counterpart (the
+ * reference has no packed format). */
+int tsp_tiles_pack_device(int tilenum, int bm, int bn, int prec, const void *d_val,
+                          const unsigned long long *d_bitmap, long long *nvals, void **d_pval,
+                          int **d_vptr, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -167,16 +167,19 @@ def test_cli_integer_stream_dc2_exact(gpu, orc, dc2_path, prec, colB):
         assert np.array_equal(Cg[:, :colB].astype(np.float64), Cref)
 
 
-@pytest.mark.parametrize("exe", ["tilespmm_fp16", "tilespmm_tf32"])
-@pytest.mark.parametrize("colB", [32, 128])
-def test_cli_end_to_end(gpu, dc2_path, tmp_path, exe, colB):
-    """The reference's test.sh run: CLI on dc2, check passes, 19-field CSV row."""
+@pytest.mark.parametrize("exe,colB,tiling", [("tilespmm_fp16", 32, "device"), ("tilespmm_fp16", 128, "device"),
+                                             ("tilespmm_tf32", 32, "device"), ("tilespmm_tf32", 128, "device"),
+                                             ("tilespmm_fp16", 128, "host"), ("tilespmm_tf32", 32, "host")])
+def test_cli_end_to_end(gpu, dc2_path, tmp_path, exe, colB, tiling):
+    """The reference's test.sh run: CLI on dc2, check passes, 19-field CSV row;
+    tiles built on the device (default) or by the host library."""
     import subprocess
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     binary = os.path.join(root, "tilespmm_amd", "bin", exe)
-    say(f"cli {exe} colB={colB}")
+    say(f"cli {exe} colB={colB} tiling={tiling}")
+    env = dict(os.environ, TSP_TILING=tiling)
     r = subprocess.run([binary, "-d", "0", dc2_path, str(colB)], cwd=tmp_path, capture_output=True, text=True,
-                       timeout=240)
+                       timeout=240, env=env)
     assert r.returncode == 0, r.stderr
     assert "Check... PASS!" in r.stdout, r.stdout[-2000:]
     csv = tmp_path / ("TileSpMM-FP16.csv" if exe.endswith("fp16") else "TileSpMM-TF32.csv")

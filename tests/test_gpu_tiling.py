@@ -29,7 +29,11 @@ def assert_same(d, ref, prec, what):
     assert np.array_equal(d["tile_colidx"], ref["tile_colidx"]), f"{what}: tile_colidx"
     assert np.array_equal(d["tile_nnz"], ref["tile_nnz"]), f"{what}: tile_nnz"
     vt = np.uint16 if prec == 0 else np.uint32
-    dv, rv = d["dense"].view(vt), np.asarray(ref["dense"]).astype(vt)
+    rv = np.asarray(ref["dense"])
+    # host tile arrays hold float32 values for tf32 (compare their bits); the
+    # oracle returns the bit patterns already
+    rv = rv.view(vt) if rv.dtype.itemsize == np.dtype(vt).itemsize else rv.astype(vt)
+    dv = d["dense"].view(vt)
     if not np.array_equal(dv, rv):
         i = int(np.argwhere(dv != rv)[0][0])
         pytest.fail(f"{what}: value bits differ at {i}: {dv[i]:#x} vs {rv[i]:#x}")
@@ -121,3 +125,56 @@ def test_device_tiles_config_classes(gpu, config, prec):
         h = tsp.tile_create(s, A.cols, bm, prec).arrays()
         d = tsp.tile_create_device(s, A.cols, bm, prec)
         assert_same(d, h, prec, f"config {config} class {bm}")
+
+
+def test_device_tiles_rejects_out_of_range_column(gpu):
+    # the fill kernel finds no slot for a column outside [0, colA): the call
+    # reports TSP_EINVAL and frees its outputs
+    rows, cols = 20, 64
+    rp = np.arange(0, 41, 2, dtype=np.int32)
+    ci = np.tile(np.array([3, 9], np.int32), 20)
+    ci[17] = cols
+    sub = gpu.Csr(rows, cols, rp, ci, np.ones(40, np.float32), 1)
+    with pytest.raises(gpu.TspError) as e:
+        gpu.tile_create_device(sub, cols, 16, 1)
+    assert e.value.status == 1001
+
+
+def plan_c(plan, th, fmt16=1, fmt8=1):
+    plan.set_th(*th)
+    plan.set_format(16, fmt16)
+    plan.set_format(8, fmt8)
+    plan.run(zero_c=True)
+    return plan.download_c()
+
+
+@pytest.mark.parametrize("config,prec", [(2, 0), (3, 1)])
+def test_plan_from_csr_matches_host_tiles(gpu, config, prec):
+    """A plan whose tiles were built on the device computes the same C, bit
+    for bit, as a plan over the host library's tiles (same thresholds and A
+    format, no split tasks so no atomics), in the dense and the device-packed
+    format."""
+    tsp = gpu
+    A, B, colB, cbp = tsp.gen_config(config, prec=prec)
+    g, dl = tsp.predict(tsp.features(A, 9.5, colB), prec)
+    subs = tsp.matrix_split(A, g, dl)
+    tiles = [tsp.tile_create(s, A.cols, bm, prec) for s, bm in zip(subs, (64, 16, 8))]
+    th = []
+    for t in tiles:
+        lens = np.diff(t.arrays()["tile_ptr"]) if t.tilenum else np.zeros(1, np.int64)
+        th.append(int(max(8, -(-int(lens.max()) // 8) * 8)))     # >= every row-block: no split tasks
+    say(f"config {config} prec {prec}: thresholds {th}")
+    host_plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
+    dev_plan = tsp.Plan.from_csr(subs, A.rows, A.cols, cbp, prec, B)
+    try:
+        say(f"device tiling {dev_plan.tile_ms:.2f} ms")
+        hip, host = tsp.load()
+        for bm, t in zip((64, 16, 8), tiles):
+            assert host.tsp_plan_tilenum(dev_plan.p, bm) == t.tilenum
+        for fmt in (1, 2):
+            Ch = plan_c(host_plan, th, fmt, fmt)
+            Cd = plan_c(dev_plan, th, fmt, fmt)
+            assert np.array_equal(Ch.view(np.uint32), Cd.view(np.uint32)), f"format {fmt}"
+    finally:
+        host_plan.close()
+        dev_plan.close()

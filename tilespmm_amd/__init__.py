@@ -170,6 +170,8 @@ HIP_SYMBOLS = {
     "tsp_tile_create_device": (C.c_int, [C.POINTER(DevTiles), C.c_int, C.c_int, C.c_longlong, _P, _P, _P,
                                          C.c_int, C.c_int, C.c_int, _P]),
     "tsp_dev_tiles_free": (C.c_int, [C.POINTER(DevTiles)]),
+    "tsp_tiles_pack_device": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, C.POINTER(C.c_longlong),
+                                        C.POINTER(C.c_void_p), C.POINTER(C.c_void_p), _P]),
 }
 HOST_SYMBOLS = {
     "tsp_mm_read": (C.c_int, [C.c_char_p, _IP, _IP, C.POINTER(C.c_longlong), _IP,
@@ -203,6 +205,9 @@ HOST_SYMBOLS = {
     "tsp_plan_create": (C.c_int, [C.POINTER(C.c_void_p), C.c_int, C.POINTER(Tile_matrix),
                                   C.POINTER(Tile_matrix), C.POINTER(Tile_matrix), C.c_int, C.c_int,
                                   C.c_int, C.c_int, _P]),
+    "tsp_plan_create_csr": (C.c_int, [C.POINTER(C.c_void_p), C.c_int, C.POINTER(tsp_sub_csr),
+                                      C.POINTER(tsp_sub_csr), C.POINTER(tsp_sub_csr), C.c_int, C.c_int,
+                                      C.c_int, C.c_int, _P, C.POINTER(C.c_double)]),
     "tsp_plan_set_th": (C.c_int, [_P, C.c_int, C.c_int, C.c_int]),
     "tsp_plan_tune": (C.c_int, [_P, C.c_int, _P, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "tsp_plan_set_variant": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
@@ -219,6 +224,9 @@ HOST_SYMBOLS = {
                                     C.POINTER(Tile_matrix), C.c_int, C.c_int, C.c_int,
                                     C.c_longlong, C.c_int, _P, _P, C.c_double, C.c_int, C.c_int,
                                     C.c_int, _P, C.POINTER(RunResult)]),
+    "tsp_plan_execute": (C.c_int, [_P, C.c_longlong, _P, C.c_double, C.c_int, C.c_int, C.c_int, _P,
+                                   C.POINTER(RunResult)]),
+    "tsp_plan_tilenum": (C.c_int, [_P, C.c_int]),
     "tsp_policy_candidates": (C.c_int, [_P, _P]),
 }
 
@@ -554,6 +562,29 @@ class Plan:
         B = np.ascontiguousarray(B)
         _check("tsp_plan_create", host.tsp_plan_create(C.byref(self.p), device, C.byref(t64.m), C.byref(t16.m),
                                                        C.byref(t8.m), rowA, colA, colB_p, prec, _ptr(B)))
+
+    @classmethod
+    def from_csr(cls, subs, rowA: int, colA: int, colB_p: int, prec: int, B: np.ndarray, device: int = 0):
+        """Plan whose tiles are built on the device from the class sub-CSRs
+        (tsp_plan_create_csr); .tile_ms = upload + device conversion time."""
+        _, host = load()
+        self = cls.__new__(cls)
+        self.rowA, self.colB_p = rowA, colB_p
+        self.p = C.c_void_p()
+        B = np.ascontiguousarray(B)
+        keep, structs = [], []
+        for s in subs:
+            rp, ci, v, orow = (np.ascontiguousarray(a) for a in (s.rowptr, s.colidx, s.val, s.orig_row))
+            keep.append((rp, ci, v, orow))
+            structs.append(tsp_sub_csr(s.rows, s.nnz, rp.ctypes.data_as(_IP), ci.ctypes.data_as(_IP),
+                                       v.ctypes.data_as(C.c_void_p), orow.ctypes.data_as(_IP)))
+        self._keep = (keep, structs)
+        ms = C.c_double()
+        _check("tsp_plan_create_csr",
+               host.tsp_plan_create_csr(C.byref(self.p), device, C.byref(structs[0]), C.byref(structs[1]),
+                                        C.byref(structs[2]), rowA, colA, colB_p, prec, _ptr(B), C.byref(ms)))
+        self.tile_ms = ms.value
+        return self
 
     def close(self):
         if self.p and _host is not None:

@@ -104,13 +104,15 @@ __device__ __forceinline__ V add_round(V a, V b)
     else return a + b;
 }
 
-// one thread per row of the sub-CSR
+// one thread per row of the sub-CSR; a column index that is not in its
+// row-block's distinct list (out of [0, colA), so the key sort could not
+// place it) is counted in cnt[tilenum] and written nowhere
 template <typename V>
 __global__ void fill_kernel(const int *__restrict__ ptr, const int *__restrict__ idx, const V *__restrict__ val,
                             int rows, int bm, int bn, int words, const int *__restrict__ tile_ptr,
                             const int *__restrict__ dstart, const int *__restrict__ dcount,
-                            const int *__restrict__ dcols, int *__restrict__ cnt, V *__restrict__ dense,
-                            unsigned long long *__restrict__ bitmap)
+                            const int *__restrict__ dcols, int *__restrict__ cnt, int *__restrict__ bad,
+                            V *__restrict__ dense, unsigned long long *__restrict__ bitmap)
 {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
     if (r >= rows) return;
@@ -126,12 +128,47 @@ __global__ void fill_kernel(const int *__restrict__ ptr, const int *__restrict__
             if (dl[mid] < c) lo = mid + 1;
             else hi = mid;
         }
+        if (lo >= d || dl[lo] != c) {
+            atomicAdd(bad, 1);
+            continue;
+        }
         const int tile = t0 + lo / bn;
         const int slot = lr * bn + lo % bn;
         atomicAdd(&cnt[tile], 1);
         atomicOr(&bitmap[(size_t)tile * words + slot / 64], 1ull << (slot % 64));
         V *dst = dense + (size_t)tile * bm * bn + slot;
         *dst = add_round(*dst, val[j]);
+    }
+}
+
+// ---- bitmap-packed A -------------------------------------------------------
+__global__ void popcount_kernel(const unsigned long long *__restrict__ bmp, int tilenum, int words,
+                                int *__restrict__ cnt)
+{
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= tilenum) return;
+    int k = 0;
+    for (int w = 0; w < words; ++w) k += __popcll(bmp[(size_t)t * words + w]);
+    cnt[t] = k;
+}
+
+// one thread per tile: the values at the set bits, in bit (row-major) order
+template <typename V>
+__global__ void pack_kernel(const V *__restrict__ dense, const unsigned long long *__restrict__ bmp,
+                            const int *__restrict__ vptr, int tilenum, int words, int slots,
+                            V *__restrict__ pval)
+{
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= tilenum) return;
+    int o = vptr[t];
+    const V *src = dense + (size_t)t * slots;
+    for (int w = 0; w < words; ++w) {
+        unsigned long long m = bmp[(size_t)t * words + w];
+        while (m) {
+            const int b = __ffsll((long long)m) - 1;
+            pval[o++] = src[w * 64 + b];
+            m &= m - 1;
+        }
     }
 }
 
@@ -271,12 +308,13 @@ int tile_create_device(tsp_dev_tiles *out, int rows, int colA, long long nnz, co
     TCHK(hipMalloc(&out->d_val, vs * tn * BM * BN));
     TCHK(hipMalloc((void **)&out->d_bitmap, sizeof(uint64_t) * tn * out->bitmap_words));
     int *cnt = nullptr;
-    TCHK(hipMalloc(&cnt, sizeof(int) * (tn + 1)));
+    TCHK(hipMalloc(&cnt, sizeof(int) * (tn + 2)));    // + the invalid-column counter
     struct FreeCnt {
         int *p;
         ~FreeCnt() { (void)hipFree(p); }
     } fc{cnt};
-    TCHK(hipMemsetAsync(cnt, 0, sizeof(int) * (tn + 1), s));
+    TCHK(hipMemsetAsync(cnt, 0, sizeof(int) * (tn + 2), s));
+    int *bad = cnt + tn + 1;
     TCHK(hipMemsetAsync(out->d_val, 0, vs * tn * BM * BN, s));
     TCHK(hipMemsetAsync(out->d_bitmap, 0, sizeof(uint64_t) * tn * out->bitmap_words, s));
     if (tilenum > 0) {
@@ -284,11 +322,11 @@ int tile_create_device(tsp_dev_tiles *out, int rows, int colA, long long nnz, co
         if (prec == TSP_PREC_FP16)
             fill_kernel<_Float16><<<nblocks(rows), kThreads, 0, s>>>(
                 d_ptr, d_idx, (const _Float16 *)d_val, rows, BM, BN, out->bitmap_words, out->d_tile_ptr, dstart,
-                dcount, w.dcols, cnt, (_Float16 *)out->d_val, (unsigned long long *)out->d_bitmap);
+                dcount, w.dcols, cnt, bad, (_Float16 *)out->d_val, (unsigned long long *)out->d_bitmap);
         else
             fill_kernel<float><<<nblocks(rows), kThreads, 0, s>>>(
                 d_ptr, d_idx, (const float *)d_val, rows, BM, BN, out->bitmap_words, out->d_tile_ptr, dstart,
-                dcount, w.dcols, cnt, (float *)out->d_val, (unsigned long long *)out->d_bitmap);
+                dcount, w.dcols, cnt, bad, (float *)out->d_val, (unsigned long long *)out->d_bitmap);
         TCHK(hipGetLastError());
         need = 0;
         TCHK(rocprim::exclusive_scan(nullptr, need, cnt, out->d_tile_nnz, 0, (size_t)tilenum + 1,
@@ -299,7 +337,10 @@ int tile_create_device(tsp_dev_tiles *out, int rows, int colA, long long nnz, co
     } else {
         TCHK(hipMemsetAsync(out->d_tile_nnz, 0, sizeof(int), s));
     }
-    return (int)hipStreamSynchronize(s);
+    int nbad = 0;
+    TCHK(hipMemcpyAsync(&nbad, bad, sizeof(int), hipMemcpyDeviceToHost, s));
+    TCHK(hipStreamSynchronize(s));
+    return nbad ? TSP_EINVAL : TSP_OK;
 }
 
 }  // namespace
@@ -309,9 +350,75 @@ extern "C" {
 int tsp_tile_create_device(tsp_dev_tiles *out, int rows, int colA, long long nnz, const int *d_ptr,
                            const int *d_idx, const void *d_val, int BM, int BN, int prec, void *stream)
 {
+    if (!out) return TSP_EINVAL;
+    memset(out, 0, sizeof *out);
     const int st = tile_create_device(out, rows, colA, nnz, d_ptr, d_idx, d_val, BM, BN, prec, stream);
-    if (st != TSP_OK && st != TSP_EINVAL) tsp_dev_tiles_free(out);
+    if (st != TSP_OK) tsp_dev_tiles_free(out);
     return st;
+}
+
+int tsp_tiles_pack_device(int tilenum, int bm, int bn, int prec, const void *d_val,
+                          const unsigned long long *d_bitmap, long long *nvals, void **d_pval, int **d_vptr,
+                          void *stream)
+{
+    if (tilenum < 0 || !nvals || (bm != 64 && bm != 16 && bm != 8) || bn <= 0 || bn > 32) return TSP_EINVAL;
+    if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
+    if ((d_pval == nullptr) != (d_vptr == nullptr)) return TSP_EINVAL;
+    if (tilenum > 0 && (!d_bitmap || (d_pval && !d_val))) return TSP_EINVAL;
+    hipStream_t s = (hipStream_t)stream;
+    const int words = (bm * bn + 63) / 64;
+    int *vptr = nullptr, *cnt = nullptr;
+    Scratch tmp;
+    TCHK(hipMalloc(&cnt, sizeof(int) * ((size_t)tilenum + 1)));
+    struct FreeCnt {
+        int *p;
+        ~FreeCnt() { (void)hipFree(p); }
+    } fc{cnt};
+    hipError_t e = hipMalloc(&vptr, sizeof(int) * ((size_t)tilenum + 1));
+    if (e != hipSuccess) return (int)e;
+    auto fail = [&](int st) {
+        (void)hipFree(vptr);
+        return st;
+    };
+    if ((e = hipMemsetAsync(cnt + tilenum, 0, sizeof(int), s)) != hipSuccess) return fail((int)e);
+    if (tilenum > 0) popcount_kernel<<<nblocks(tilenum), kThreads, 0, s>>>(d_bitmap, tilenum, words, cnt);
+    size_t need = 0;
+    if ((e = rocprim::exclusive_scan(nullptr, need, cnt, vptr, 0, (size_t)tilenum + 1, rocprim::plus<int>(), s)) !=
+        hipSuccess)
+        return fail((int)e);
+    if ((e = tmp.grow(need)) != hipSuccess) return fail((int)e);
+    if ((e = rocprim::exclusive_scan(tmp.p, need, cnt, vptr, 0, (size_t)tilenum + 1, rocprim::plus<int>(), s)) !=
+        hipSuccess)
+        return fail((int)e);
+    int total = 0;   // <= slots of all tiles; a class's nnz bounds it below 2^31
+    if ((e = hipMemcpyAsync(&total, vptr + tilenum, sizeof(int), hipMemcpyDeviceToHost, s)) != hipSuccess)
+        return fail((int)e);
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return fail((int)e);
+    *nvals = total;
+    if (!d_pval) return fail(TSP_OK);
+    // 4 elements of zero padding: the kernels' packed loads may read past the last value
+    const size_t vs = prec == TSP_PREC_FP16 ? 2 : 4;
+    void *pv = nullptr;
+    if ((e = hipMalloc(&pv, vs * ((size_t)total + 4))) != hipSuccess) return fail((int)e);
+    if ((e = hipMemsetAsync((char *)pv + vs * (size_t)total, 0, vs * 4, s)) != hipSuccess) {
+        (void)hipFree(pv);
+        return fail((int)e);
+    }
+    if (tilenum > 0) {
+        if (prec == TSP_PREC_FP16)
+            pack_kernel<uint16_t><<<nblocks(tilenum), kThreads, 0, s>>>(
+                (const uint16_t *)d_val, d_bitmap, vptr, tilenum, words, bm * bn, (uint16_t *)pv);
+        else
+            pack_kernel<uint32_t><<<nblocks(tilenum), kThreads, 0, s>>>(
+                (const uint32_t *)d_val, d_bitmap, vptr, tilenum, words, bm * bn, (uint32_t *)pv);
+    }
+    if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(s)) != hipSuccess) {
+        (void)hipFree(pv);
+        return fail((int)e);
+    }
+    *d_pval = pv;
+    *d_vptr = vptr;
+    return TSP_OK;
 }
 
 int tsp_dev_tiles_free(tsp_dev_tiles *t)

@@ -10,7 +10,10 @@
 //     every C entry is an exact integer in fp32;
 //   * colB_padded = colB <= 32 ? 32 : roundup(colB, 64) (src/main.cu:173);
 //   * features -> policy (gamma, delta) -> matrix_split -> tiles, timed as
-//     the CPU preprocessing time;
+//     the preprocessing time.  The tiles are built on the GPU from the class
+//     sub-CSRs (upload + device conversion, included in that time); with
+//     TSP_TILING=host in the environment they are built by the host library
+//     instead, as the reference does;
 //   * one 19-field row is appended to ./TileSpMM-FP16.csv or
 //     ./TileSpMM-TF32.csv (README.md:89-97): matrix, rows, cols, nnz, colB,
 //     tilenum64/16/8, gamma, delta, TH64/16/8, pre-time, runtime, TFLOPS,
@@ -139,15 +142,31 @@ int main(int argc, char **argv)
     tsp_sub_csr *subs[3] = {&s64, &s16, &s8};
     Tile_matrix *ms[3] = {&m64, &m16, &m8};
     const int bms[3] = {64, 16, 8};
-    for (int i = 0; i < 3; ++i) {
-        if (subs[i]->rows <= 0) continue;
-        if ((st = tsp_tile_create(ms[i], subs[i]->rows, colA, subs[i]->nnz, subs[i]->ptr, subs[i]->idx,
-                                  subs[i]->val, subs[i]->orig_row, bms[i], tsp_tile_bn(bms[i], prec), prec)))
-            return die("Tile_create", st);
+    const char *tiling = getenv("TSP_TILING");
+    const bool host_tiles = tiling && strcmp(tiling, "host") == 0;
+    tsp_plan *plan = nullptr;
+    if (host_tiles) {
+        for (int i = 0; i < 3; ++i) {
+            if (subs[i]->rows <= 0) continue;
+            if ((st = tsp_tile_create(ms[i], subs[i]->rows, colA, subs[i]->nnz, subs[i]->ptr, subs[i]->idx,
+                                      subs[i]->val, subs[i]->orig_row, bms[i], tsp_tile_bn(bms[i], prec), prec)))
+                return die("Tile_create", st);
+        }
+        t2 = wall_ms();
+        if ((st = tsp_plan_create(&plan, device_id, &m64, &m16, &m8, rowA, colA, colB_p, prec, B.data())))
+            return die("plan", st);
+    } else {
+        // B's upload is not preprocessing: the host path uploads it outside the timed span too
+        const double t_split = wall_ms();
+        double tile_ms = 0;
+        if ((st = tsp_plan_create_csr(&plan, device_id, &s64, &s16, &s8, rowA, colA, colB_p, prec, B.data(),
+                                      &tile_ms)))
+            return die("Tile_create (device)", st);
+        t2 = t_split + tile_ms;
+        for (int i = 0; i < 3; ++i) ms[i]->tilenum = tsp_plan_tilenum(plan, bms[i]);
     }
-    t2 = wall_ms();
     const double pre_ms = t2 - t1;
-    printf("  CPU preprocessing time = %4.5f s\n", pre_ms / 1000.0);
+    printf("  %s preprocessing time = %4.5f s\n", host_tiles ? "CPU" : "CPU+GPU", pre_ms / 1000.0);
 
     const char *csv_path = prec == TSP_PREC_FP16 ? "TileSpMM-FP16.csv" : "TileSpMM-TF32.csv";
     FILE *fout = fopen(csv_path, "a");
@@ -161,9 +180,9 @@ int main(int argc, char **argv)
 
     std::vector<float> C((size_t)rowA * colB_p);
     tsp_run_result res;
-    if ((st = tsp_call_tilespmm(device_id, &m64, &m16, &m8, rowA, colA, colB_p, nnzA, prec, B.data(),
-                                C.data(), pre_ms, colB, 1000, 1, fout, &res)))
-        return die("TileSpMM", st);
+    st = tsp_plan_execute(plan, nnzA, C.data(), pre_ms, colB, 1000, 1, fout, &res);
+    tsp_plan_destroy(plan);
+    if (st) return die("TileSpMM", st);
     printf("  TileSpMM runtime %4.3f ms, %4.3f TFlops\n", res.time_ms, res.tflops);
 
     std::vector<float> Cv((size_t)rowA * colB);

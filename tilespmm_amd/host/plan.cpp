@@ -38,6 +38,8 @@ struct ClassDev {
     uint64_t *d_bmp = nullptr;    // per-tile occupancy bitmaps
     int *d_vptr = nullptr;        // per-tile offset into d_pval
     void *stream = nullptr;
+    bool dev_built = false;       // tiles made on the device: `own` holds the host-side view
+    Tile_matrix own{};            // tile_ptr, orig_tile_row_idx, schedule; no value arrays
     std::map<int, std::pair<std::vector<unsigned>, std::vector<int>>> cache;
     bool active() const { return m && m->tilenum > 0; }
 };
@@ -110,19 +112,23 @@ static int upload_schedule(tsp_plan *p, ClassDev &c, int th)
 // Bitmap-packed A: per tile the canonical tile's occupancy bitmap plus the
 // values at its set bits in bit (row-major) order.  Chosen for 8- and 16-row
 // classes when it moves fewer bytes than the dense zero-padded tiles.
-static size_t packed_bytes(const Tile_matrix *m, size_t vs, long long *nvals)
+static long long packed_values(const Tile_matrix *m)
 {
     const size_t words = (size_t)m->tilenum * m->bitmap_words;
     long long n = 0;
 #pragma omp parallel for reduction(+ : n)
     for (long long i = 0; i < (long long)words; ++i) n += __builtin_popcountll(m->tile_bitmap[i]);
-    *nvals = n;
-    return (size_t)n * vs + words * 8 + (size_t)m->tilenum * 4;
+    return n;
 }
 
 static int upload_packed(tsp_plan *p, ClassDev &c)
 {
     if (c.d_pval) return TSP_OK;
+    if (c.dev_built) {
+        long long n = 0;
+        return tsp_tiles_pack_device(c.m->tilenum, c.m->bm, c.m->bn, p->prec, c.d_val,
+                                     (const unsigned long long *)c.d_bmp, &n, &c.d_pval, &c.d_vptr, nullptr);
+    }
     const Tile_matrix *m = c.m;
     const size_t vs = tsph::val_size(p->prec);
     const int nt = m->tilenum, wd = m->bitmap_words, slots = m->bm * m->bn;
@@ -237,6 +243,7 @@ extern "C" int tsp_plan_destroy(tsp_plan *p)
         tsp_free(c.d_rows);
         tsp_free(c.d_colstart);
         tsp_stream_destroy(c.stream);
+        if (c.dev_built) tsp_tile_destroy(&c.own);
     }
     tsp_free(p->d_B);
     tsp_free(p->d_C);
@@ -248,30 +255,67 @@ extern "C" int tsp_plan_destroy(tsp_plan *p)
     return TSP_OK;
 }
 
-extern "C" int tsp_plan_create(tsp_plan **out, int device_id, Tile_matrix *m64, Tile_matrix *m16,
-                               Tile_matrix *m8, int rowA, int colA, int colB_p, int prec,
-                               const void *h_B)
+// Plan shell: B, C.  Classes are filled by the caller.
+static int plan_begin(std::unique_ptr<tsp_plan> &p, int device_id, int rowA, int colA, int colB_p, int prec,
+                      const void *h_B)
 {
-    if (!out || rowA < 0 || colA < 0 || (prec != 0 && prec != 1)) return TSP_EINVAL;
+    if (rowA < 0 || colA < 0 || (prec != 0 && prec != 1)) return TSP_EINVAL;
     if (colB_p != 32 && (colB_p <= 0 || colB_p % 64)) return TSP_EINVAL;
-    *out = nullptr;
     TSP_TRY(tsp_device_init(device_id));
-    std::unique_ptr<tsp_plan> p(new tsp_plan);
+    p.reset(new tsp_plan);
     p->dev = device_id;
     p->prec = prec;
     p->rowA = rowA;
     p->colA = colA;
     p->colB_p = colB_p;
     const size_t vs = tsph::val_size(prec);
+    const size_t bbytes = vs * (size_t)colA * colB_p, cbytes = sizeof(float) * (size_t)rowA * colB_p;
+    TSP_TRY(tsp_malloc(&p->d_B, bbytes));
+    TSP_TRY(tsp_malloc((void **)&p->d_C, cbytes));
+    if (h_B) TSP_TRY(tsp_memcpy_h2d(p->d_B, h_B, bbytes));
+    return tsp_memset(p->d_C, 0, cbytes);
+}
+
+// Per active class: schedule buffers (a row-block splits into at most its
+// tile count of tasks) and the class stream.
+static int class_finish(ClassDev &c)
+{
+    c.cap_tasks = (long long)c.m->tilem + c.m->tilenum;
+    TSP_TRY(tsp_malloc((void **)&c.d_rows, sizeof(unsigned) * (size_t)c.cap_tasks));
+    TSP_TRY(tsp_malloc((void **)&c.d_colstart, sizeof(int) * ((size_t)c.cap_tasks + 1)));
+    return tsp_stream_create_nonblocking(&c.stream);
+}
+
+static int plan_end(tsp_plan *p)
+{
+    TSP_TRY(tsp_stream_create_nonblocking(&p->main));
+    TSP_TRY(tsp_event_create(&p->ev0));
+    TSP_TRY(tsp_event_create(&p->ev1));
+    for (void *&e : p->done) TSP_TRY(tsp_event_create(&e));
+    return TSP_OK;
+}
+
+// The bitmap-packed format is a tuning candidate for the 8/16-row classes
+// when it moves at most 3/4 of the dense bytes.
+static bool packed_pays(const Tile_matrix *m, size_t vs, long long nvals)
+{
+    const size_t pbytes = (size_t)nvals * vs + (size_t)m->tilenum * m->bitmap_words * 8 + (size_t)m->tilenum * 4;
+    return m->bm != 64 && pbytes * 4 <= vs * m->dnssize * 3;
+}
+
+extern "C" int tsp_plan_create(tsp_plan **out, int device_id, Tile_matrix *m64, Tile_matrix *m16,
+                               Tile_matrix *m8, int rowA, int colA, int colB_p, int prec,
+                               const void *h_B)
+{
+    if (!out) return TSP_EINVAL;
+    *out = nullptr;
+    std::unique_ptr<tsp_plan> p;
+    int st = plan_begin(p, device_id, rowA, colA, colB_p, prec, h_B);
+    auto fail = [&](int s) { tsp_plan_destroy(p.release()); return s; };
+    if (st) return fail(st);
+    const size_t vs = tsph::val_size(prec);
     Tile_matrix *ms[3] = {m64, m16, m8};
     const int bms[3] = {64, 16, 8};
-    int st = TSP_OK;
-    auto fail = [&](int s) { tsp_plan_destroy(p.release()); return s; };
-    const size_t bbytes = vs * (size_t)colA * colB_p, cbytes = sizeof(float) * (size_t)rowA * colB_p;
-    if ((st = tsp_malloc(&p->d_B, bbytes))) return fail(st);
-    if ((st = tsp_malloc((void **)&p->d_C, cbytes))) return fail(st);
-    if (h_B && (st = tsp_memcpy_h2d(p->d_B, h_B, bbytes))) return fail(st);
-    if ((st = tsp_memset(p->d_C, 0, cbytes))) return fail(st);
     for (int i = 0; i < 3; ++i) {
         ClassDev &c = p->cls[i];
         c.m = ms[i];
@@ -279,25 +323,104 @@ extern "C" int tsp_plan_create(tsp_plan **out, int device_id, Tile_matrix *m64, 
         if (!c.active()) continue;
         if (c.m->bm != bms[i] || c.m->prec != prec || c.m->bn != tsp_tile_bn(bms[i], prec)) return fail(TSP_EINVAL);
         const size_t nt = (size_t)c.m->tilenum;
-        // Dense tiles first; the bitmap-packed format is a tuning candidate
-        // when it moves at most 3/4 of the dense bytes (8/16-row classes).
-        long long nvals = 0;
-        const size_t pbytes = c.bm != 64 ? packed_bytes(c.m, vs, &nvals) : 0;
-        c.pack_ok = c.bm != 64 && pbytes * 4 <= vs * c.m->dnssize * 3;
+        c.pack_ok = c.bm != 64 && packed_pays(c.m, vs, packed_values(c.m));
         c.fmt = 1;
         if ((st = upload_dense(p.get(), c))) return fail(st);
         if ((st = tsp_malloc((void **)&c.d_colidx, sizeof(int) * nt * c.m->bn))) return fail(st);
         if ((st = tsp_memcpy_h2d(c.d_colidx, c.m->tile_colidx, sizeof(int) * nt * c.m->bn))) return fail(st);
-        c.cap_tasks = (long long)c.m->tilem + c.m->tilenum;
-        if ((st = tsp_malloc((void **)&c.d_rows, sizeof(unsigned) * (size_t)c.cap_tasks))) return fail(st);
-        if ((st = tsp_malloc((void **)&c.d_colstart, sizeof(int) * ((size_t)c.cap_tasks + 1)))) return fail(st);
-        if ((st = tsp_stream_create_nonblocking(&c.stream))) return fail(st);
+        if ((st = class_finish(c))) return fail(st);
     }
-    if ((st = tsp_stream_create_nonblocking(&p->main))) return fail(st);
-    if ((st = tsp_event_create(&p->ev0))) return fail(st);
-    if ((st = tsp_event_create(&p->ev1))) return fail(st);
-    for (void *&e : p->done)
-        if ((st = tsp_event_create(&e))) return fail(st);
+    if ((st = plan_end(p.get()))) return fail(st);
+    *out = p.release();
+    return TSP_OK;
+}
+
+// Device-built class: upload the sub-CSR, convert on the device, keep the
+// device arrays the kernels read and only tile_ptr / orig_tile_row_idx on
+// the host.
+static int class_from_csr(tsp_plan *p, ClassDev &c, const tsp_sub_csr *s)
+{
+    const int BM = c.bm, BN = tsp_tile_bn(BM, p->prec);
+    Tile_matrix &m = c.own;
+    memset(&m, 0, sizeof m);
+    c.dev_built = true;
+    c.m = &m;
+    m.bm = BM;
+    m.bn = BN;
+    m.prec = p->prec;
+    m.bitmap_words = (BM * BN + 63) / 64;
+    const int rows = s ? s->rows : 0;
+    m.tilem = (rows + BM - 1) / BM;
+    m.tilen = (p->colA + BN - 1) / BN;
+    m.tile_ptr = tsph::alloc_n<int>((size_t)m.tilem + 1);
+    m.orig_tile_row_idx = tsph::alloc_n<int>((size_t)(m.tilem > 0 ? m.tilem : 1));
+    if (!m.tile_ptr || !m.orig_tile_row_idx) return TSP_ENOMEM;
+    m.tile_ptr[0] = 0;
+    if (rows == 0) return TSP_OK;
+    if (!s->ptr || !s->orig_row || (s->nnz > 0 && (!s->idx || !s->val))) return TSP_EINVAL;
+    if ((long long)s->ptr[rows] != s->nnz) return TSP_EINVAL;
+    for (int b = 0; b < m.tilem; ++b) m.orig_tile_row_idx[b] = s->orig_row[(size_t)b * BM];
+    const size_t vs = tsph::val_size(p->prec), nnz = (size_t)s->nnz;
+    void *d_ptr = nullptr, *d_idx = nullptr, *d_v = nullptr;
+    struct FreeIn {
+        void **a[3];
+        ~FreeIn()
+        {
+            for (void **x : a) tsp_free(*x);
+        }
+    } fin{{&d_ptr, &d_idx, &d_v}};
+    TSP_TRY(tsp_malloc(&d_ptr, sizeof(int) * ((size_t)rows + 1)));
+    TSP_TRY(tsp_malloc(&d_idx, sizeof(int) * (nnz ? nnz : 1)));
+    TSP_TRY(tsp_malloc(&d_v, vs * (nnz ? nnz : 1)));
+    TSP_TRY(tsp_memcpy_h2d(d_ptr, s->ptr, sizeof(int) * ((size_t)rows + 1)));
+    if (nnz) {
+        TSP_TRY(tsp_memcpy_h2d(d_idx, s->idx, sizeof(int) * nnz));
+        TSP_TRY(tsp_memcpy_h2d(d_v, s->val, vs * nnz));
+    }
+    tsp_dev_tiles dt;
+    TSP_TRY(tsp_tile_create_device(&dt, rows, p->colA, s->nnz, (const int *)d_ptr, (const int *)d_idx, d_v, BM, BN,
+                                   p->prec, nullptr));
+    // adopt the arrays the kernels read; the plan frees them
+    c.d_val = dt.d_val;
+    c.d_colidx = dt.d_tile_colidx;
+    c.d_bmp = (uint64_t *)dt.d_bitmap;
+    m.tilenum = dt.tilenum;
+    m.dnssize = (size_t)dt.tilenum * BM * BN;
+    int st = tsp_memcpy_d2h(m.tile_ptr, dt.d_tile_ptr, sizeof(int) * ((size_t)m.tilem + 1));
+    tsp_free(dt.d_tile_ptr);
+    tsp_free(dt.d_tile_nnz);
+    if (st) return st;
+    if (c.bm != 64 && m.tilenum > 0) {
+        long long nvals = 0;
+        TSP_TRY(tsp_tiles_pack_device(m.tilenum, BM, BN, p->prec, nullptr, dt.d_bitmap, &nvals, nullptr, nullptr,
+                                      nullptr));
+        c.pack_ok = packed_pays(&m, vs, nvals);
+    }
+    c.fmt = 1;
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_create_csr(tsp_plan **out, int device_id, const tsp_sub_csr *s64, const tsp_sub_csr *s16,
+                                   const tsp_sub_csr *s8, int rowA, int colA, int colB_p, int prec,
+                                   const void *h_B, double *tile_ms)
+{
+    if (!out) return TSP_EINVAL;
+    *out = nullptr;
+    std::unique_ptr<tsp_plan> p;
+    int st = plan_begin(p, device_id, rowA, colA, colB_p, prec, h_B);
+    auto fail = [&](int s) { tsp_plan_destroy(p.release()); return s; };
+    if (st) return fail(st);
+    const tsp_sub_csr *ss[3] = {s64, s16, s8};
+    const int bms[3] = {64, 16, 8};
+    const double t0 = now_ms();
+    for (int i = 0; i < 3; ++i) {
+        ClassDev &c = p->cls[i];
+        c.bm = bms[i];
+        if ((st = class_from_csr(p.get(), c, ss[i]))) return fail(st);
+        if (c.active() && (st = class_finish(c))) return fail(st);
+    }
+    if (tile_ms) *tile_ms = now_ms() - t0;
+    if ((st = plan_end(p.get()))) return fail(st);
     *out = p.release();
     return TSP_OK;
 }
@@ -470,14 +593,19 @@ extern "C" int tsp_plan_device_c(tsp_plan *p, float **d_C)
     return TSP_OK;
 }
 
-extern "C" int tsp_call_tilespmm(int device_id, Tile_matrix *m64, Tile_matrix *m16, Tile_matrix *m8,
-                                 int rowA, int colA, int colB_p, long long total_nnz, int prec,
-                                 const void *h_B, float *h_C, double cpu_pre_ms, int logical_colB,
-                                 int repeat, int tune, FILE *csv, tsp_run_result *out)
+extern "C" int tsp_plan_tilenum(tsp_plan *p, int bm)
 {
-    tsp_plan *p = nullptr;
-    TSP_TRY(tsp_plan_create(&p, device_id, m64, m16, m8, rowA, colA, colB_p, prec, h_B));
-    std::unique_ptr<tsp_plan, int (*)(tsp_plan *)> guard(p, tsp_plan_destroy);
+    if (!p) return -1;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) return c.m ? c.m->tilenum : 0;
+    return -1;
+}
+
+// tune + warmup + result run + download + timed loop + CSV fields 11-16
+extern "C" int tsp_plan_execute(tsp_plan *p, long long total_nnz, float *h_C, double cpu_pre_ms,
+                                int logical_colB, int repeat, int tune, FILE *csv, tsp_run_result *out)
+{
+    if (!p) return TSP_EINVAL;
     int th[3];
     double model_ms = 0, tune_ms = 0;
     TSP_TRY(tsp_plan_tune(p, tune, th, &model_ms, &tune_ms));
@@ -503,4 +631,15 @@ extern "C" int tsp_call_tilespmm(int device_id, Tile_matrix *m64, Tile_matrix *m
         out->tune_ms = tune_ms;
     }
     return TSP_OK;
+}
+
+extern "C" int tsp_call_tilespmm(int device_id, Tile_matrix *m64, Tile_matrix *m16, Tile_matrix *m8,
+                                 int rowA, int colA, int colB_p, long long total_nnz, int prec,
+                                 const void *h_B, float *h_C, double cpu_pre_ms, int logical_colB,
+                                 int repeat, int tune, FILE *csv, tsp_run_result *out)
+{
+    tsp_plan *p = nullptr;
+    TSP_TRY(tsp_plan_create(&p, device_id, m64, m16, m8, rowA, colA, colB_p, prec, h_B));
+    std::unique_ptr<tsp_plan, int (*)(tsp_plan *)> guard(p, tsp_plan_destroy);
+    return tsp_plan_execute(p, total_nnz, h_C, cpu_pre_ms, logical_colB, repeat, tune, csv, out);
 }
