@@ -133,9 +133,12 @@ def main():
     if args.delta is not None:
         d = args.delta
     subs = tsp.matrix_split(A, g, d)
+    split_ms = (time.time() - t0) * 1e3
+    t0 = time.time()
     tiles = [tsp.tile_create(sb, A.cols, bm, prec) for sb, bm in zip(subs, (64, 16, 8))]
-    pre_ms = (time.time() - t0) * 1e3
-    log(f"split+tiles gamma={g} delta={d}: tilenum {[t.tilenum for t in tiles]} ({pre_ms:.0f} ms)")
+    host_tiles_ms = (time.time() - t0) * 1e3
+    log(f"split gamma={g} delta={d} ({split_ms:.0f} ms); host tiles: tilenum {[t.tilenum for t in tiles]} "
+        f"({host_tiles_ms:.0f} ms)")
 
     plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
     th, model_ms, tune_ms = plan.tune(not args.no_tune)
@@ -183,6 +186,12 @@ def main():
             "alg_bytes_per_launch": cls[dom]["alg_bytes"],
             "step_achieved": round(step_gbs, 2), "step_frac": round(step_gbs / HBM_PEAK_GBS, 4),
             "step_alg_bytes": step_bytes}
+
+    # the same tiles built on the GPU (upload of the class sub-CSRs + device
+    # conversion), the alternative to the host conversion timed above
+    dplan = tsp.Plan.from_csr(subs, A.rows, A.cols, cbp, prec, B)
+    dev_tiles_ms = dplan.tile_ms
+    dplan.close()
 
     vendor = None
     if not args.no_vendor:
@@ -237,7 +246,8 @@ def main():
                     for k, v in cls.items()},
         "vendor": vendor,
         "cpu_baseline": cpu,
-        "pre_ms": {"split_tiles": round(pre_ms, 1), "model": round(model_ms, 2), "tune": round(tune_ms, 1)},
+        "pre_ms": {"split": round(split_ms, 1), "tiles_host": round(host_tiles_ms, 1),
+                   "tiles_device": round(dev_tiles_ms, 1), "model": round(model_ms, 2), "tune": round(tune_ms, 1)},
     }
     plan.close()
     print(json.dumps(line), flush=True)

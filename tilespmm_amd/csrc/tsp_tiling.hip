@@ -1,19 +1,26 @@
 // tsp_tiling.hip -- CSR -> tiles on the GPU (the csr2tile conversion of
 // src/csr2tile.h:15-379,724-795 moved onto MI355X), bit-exact with the host
-// conversion (tilespmm_amd/host/tiles.cpp):
-//   1. segmented radix sort (rocPRIM) of every row-block's column indices;
-//   2. first-of-run flags + exclusive scan -> the block's sorted distinct
-//      columns and their count d;
+// conversion (tilespmm_amd/host/tiles.cpp).
+//
+//   1. key[e] = (row-block of entry e, column), value = e; one stable LSD
+//      radix sort (rocPRIM) of all pairs.  Entries of one (block, column)
+//      pair become a contiguous run that keeps the CSR order.
+//   2. run heads -> exclusive scan -> run ids.  A block's runs are its sorted
+//      distinct columns; the rank of a run inside its block is its run id
+//      minus the run id at the block's first entry, and the block's distinct
+//      count d is the difference at its ends (the sort keeps blocks in place,
+//      so block b's entries still start at ptr[b*BM]).
 //   3. ceil(d/BN) tiles per block, exclusive scan -> tile_ptr; tile_colidx is
-//      the distinct list cut into BN-wide tiles, padded with the last column;
-//   4. one thread per CSR row places its entries in CSR order: rank by binary
-//      search in the block's distinct list, atomic per-tile entry count,
-//      atomic bitmap OR, and a sequential add into the canonical row-major
-//      tile slot with the value type's rounding after every add (fp16: exact
-//      fp32 add then round to half) -- only that thread ever touches a slot of
-//      its row, so duplicate entries accumulate in CSR order exactly as on the
-//      host;
+//      the distinct list cut into BN-wide tiles, padded with the last column.
+//   4. one thread per run walks its entries in CSR order: slot
+//      (local row, rank % BN) of tile rank / BN, per-tile entry count, bitmap
+//      bit, and a sequential add into the canonical row-major slot with the
+//      value type's rounding after every add (fp16: fp32 add then round to
+//      half).  A slot belongs to exactly one run, so duplicates accumulate in
+//      CSR order exactly as on the host.
 //   5. exclusive scan of the per-tile counts -> tile_nnz.
+// Work is O(nnz) with no per-row serial loop, so hub rows of power-law
+// matrices cost no more than their entries.
 #include <cstring>
 #include <hip/hip_runtime.h>
 #include <rocprim/rocprim.hpp>
@@ -27,72 +34,83 @@ constexpr int kThreads = 256;
 
 inline unsigned nblocks(long long n) { return (unsigned)((n + kThreads - 1) / kThreads); }
 
-// off[b] = ptr[min(rows, b*stride + shift)] for b <= nseg (segment b covers
-// rows [b*stride+shift, min(rows, b*stride+shift+len))); end[b] likewise.
-__global__ void seg_bounds_kernel(const int *__restrict__ ptr, int rows, int nseg, int stride,
-                                  int shift, int len, int *__restrict__ beg, int *__restrict__ end)
+int bits_for(long long v)     // bits to hold values 0 .. v-1
 {
-    const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nseg) return;
-    const long long r0 = (long long)b * stride + shift;
-    const long long r1 = r0 + len;
-    beg[b] = ptr[r0 < rows ? r0 : rows];
-    end[b] = ptr[r1 < rows ? r1 : rows];
+    int b = 1;
+    while (b < 62 && (1ll << b) < v) ++b;
+    return b;
 }
 
-// head[i] = 1 at the first entry of every non-empty segment
-__global__ void head_kernel(const int *__restrict__ beg, const int *__restrict__ end, int nseg,
-                            uint8_t *__restrict__ head)
+// bptr[b] = ptr[min(rows, b*BM)], b = 0..tilem
+__global__ void block_ptr_kernel(const int *__restrict__ ptr, int rows, int tilem, int bm, int *__restrict__ bptr)
 {
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nseg) return;
-    if (end[b] > beg[b]) head[beg[b]] = 1;
+    if (b > tilem) return;
+    const long long r = (long long)b * bm;
+    bptr[b] = ptr[r < rows ? r : rows];
 }
 
-// flag[i] = 1 where a new distinct column starts within its segment
-__global__ void flag_kernel(const int *__restrict__ sorted, const uint8_t *__restrict__ head, long long n,
-                            int *__restrict__ flag)
+// one thread per entry: key = (block << cbits) | col, value = entry index,
+// lrow = row inside the block.  The row comes from a binary search of ptr.
+__global__ void key_kernel(const int *__restrict__ ptr, const int *__restrict__ idx, int rows, long long nnz,
+                           int bm, int cbits, int colA, unsigned long long *__restrict__ key,
+                           int *__restrict__ ent, uint8_t *__restrict__ lrow, int *__restrict__ bad)
+{
+    const long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nnz) return;
+    int lo = 0, hi = rows - 1;                 // last row r with ptr[r] <= e
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (ptr[mid] <= e) lo = mid;
+        else hi = mid - 1;
+    }
+    const int c = idx[e];
+    if (c < 0 || c >= colA) atomicAdd(bad, 1);
+    const unsigned cc = (unsigned)c & ((1u << cbits) - 1u);
+    key[e] = ((unsigned long long)(lo / bm) << cbits) | cc;
+    ent[e] = (int)e;
+    lrow[e] = (uint8_t)(lo % bm);
+}
+
+__global__ void head_kernel(const unsigned long long *__restrict__ key, long long n, int *__restrict__ flag)
 {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    flag[i] = (head[i] || sorted[i] != sorted[i - 1]) ? 1 : 0;
+    flag[i] = (i == 0 || key[i] != key[i - 1]) ? 1 : 0;
 }
 
-__global__ void distinct_scatter_kernel(const int *__restrict__ sorted, const int *__restrict__ flag,
-                                        const int *__restrict__ pos, long long n, int *__restrict__ dcols)
+// run r starts at sorted position i; its column goes to dcols[r]
+__global__ void run_scatter_kernel(const unsigned long long *__restrict__ key, const int *__restrict__ flag,
+                                   const int *__restrict__ run, long long n, unsigned cmask,
+                                   int *__restrict__ run_start, int *__restrict__ dcols)
 {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    if (flag[i]) dcols[pos[i]] = sorted[i];
+    if (flag[i]) {
+        run_start[run[i]] = (int)i;
+        dcols[run[i]] = (int)(key[i] & cmask);
+    }
 }
 
-// per segment: distinct count d = pos[end] - pos[beg] (pos has n+1 entries)
-__global__ void seg_distinct_kernel(const int *__restrict__ beg, const int *__restrict__ end,
-                                    const int *__restrict__ pos, int nseg, int *__restrict__ dstart,
-                                    int *__restrict__ dcount)
+// per block: first run id and distinct count; tiles ceil(d/BN)
+__global__ void block_runs_kernel(const int *__restrict__ bptr, const int *__restrict__ run, int tilem, int bn,
+                                  int *__restrict__ dstart, int *__restrict__ nt)
 {
     const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nseg) return;
-    const int s = pos[beg[b]], e = pos[end[b]];
-    if (dstart) dstart[b] = s;
-    dcount[b] = e - s;
-}
-
-__global__ void ntiles_kernel(const int *__restrict__ dcount, int nseg, int bn, int *__restrict__ nt)
-{
-    const int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nseg) return;
-    nt[b] = (dcount[b] + bn - 1) / bn;
+    if (b >= tilem) return;
+    const int s = run[bptr[b]], e = run[bptr[b + 1]];
+    dstart[b] = s;
+    nt[b] = (e - s + bn - 1) / bn;
 }
 
 // one work-group per row-block writes its padded column indices
 __global__ void colidx_kernel(const int *__restrict__ tile_ptr, const int *__restrict__ dstart,
-                              const int *__restrict__ dcount, const int *__restrict__ dcols, int bn,
-                              int *__restrict__ colidx)
+                              const int *__restrict__ dcols, int bn, int *__restrict__ colidx)
 {
     const int b = blockIdx.x;
     const int t0 = tile_ptr[b], nt = tile_ptr[b + 1] - t0;
-    const int d = dcount[b], s = dstart[b];
+    if (nt == 0) return;
+    const int s = dstart[b], d = dstart[b + 1] - s;
     for (int k = threadIdx.x; k < nt * bn; k += blockDim.x)
         colidx[(size_t)t0 * bn + k] = dcols[s + (k < d ? k : d - 1)];
 }
@@ -104,41 +122,30 @@ __device__ __forceinline__ V add_round(V a, V b)
     else return a + b;
 }
 
-// one thread per row of the sub-CSR; a column index that is not in its
-// row-block's distinct list (out of [0, colA), so the key sort could not
-// place it) is counted in cnt[tilenum] and written nowhere
+// one thread per run (distinct column of a block)
 template <typename V>
-__global__ void fill_kernel(const int *__restrict__ ptr, const int *__restrict__ idx, const V *__restrict__ val,
-                            int rows, int bm, int bn, int words, const int *__restrict__ tile_ptr,
-                            const int *__restrict__ dstart, const int *__restrict__ dcount,
-                            const int *__restrict__ dcols, int *__restrict__ cnt, int *__restrict__ bad,
-                            V *__restrict__ dense, unsigned long long *__restrict__ bitmap)
+__global__ void fill_kernel(const unsigned long long *__restrict__ key, const int *__restrict__ ent,
+                            const uint8_t *__restrict__ lrow, const V *__restrict__ val,
+                            const int *__restrict__ run_start, int nruns, long long n, int cbits, int bm, int bn,
+                            int words, const int *__restrict__ tile_ptr, const int *__restrict__ dstart,
+                            int *__restrict__ cnt, V *__restrict__ dense, unsigned long long *__restrict__ bitmap)
 {
     const int r = blockIdx.x * blockDim.x + threadIdx.x;
-    if (r >= rows) return;
-    const int b = r / bm, lr = r - b * bm;
-    const int *dl = dcols + dstart[b];
-    const int d = dcount[b];
-    const int t0 = tile_ptr[b];
-    for (int j = ptr[r]; j < ptr[r + 1]; ++j) {
-        const int c = idx[j];
-        int lo = 0, hi = d;                       // lower_bound in the sorted distinct list
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (dl[mid] < c) lo = mid + 1;
-            else hi = mid;
-        }
-        if (lo >= d || dl[lo] != c) {
-            atomicAdd(bad, 1);
-            continue;
-        }
-        const int tile = t0 + lo / bn;
-        const int slot = lr * bn + lo % bn;
-        atomicAdd(&cnt[tile], 1);
-        atomicOr(&bitmap[(size_t)tile * words + slot / 64], 1ull << (slot % 64));
-        V *dst = dense + (size_t)tile * bm * bn + slot;
-        *dst = add_round(*dst, val[j]);
+    if (r >= nruns) return;
+    const long long i0 = run_start[r];
+    const long long i1 = r + 1 < nruns ? run_start[r + 1] : n;
+    const int b = (int)(key[i0] >> cbits);
+    const int rank = r - dstart[b];
+    const int tile = tile_ptr[b] + rank / bn, col = rank % bn;
+    V *tv = dense + (size_t)tile * bm * bn;
+    unsigned long long *tb = bitmap + (size_t)tile * words;
+    for (long long i = i0; i < i1; ++i) {
+        const int e = ent[i];
+        const int slot = lrow[e] * bn + col;
+        atomicOr(&tb[slot / 64], 1ull << (slot % 64));
+        tv[slot] = add_round(tv[slot], val[e]);
     }
+    atomicAdd(&cnt[tile], (int)(i1 - i0));
 }
 
 // ---- bitmap-packed A -------------------------------------------------------
@@ -190,12 +197,24 @@ struct Scratch {
     }
 };
 
-int bits_for(int colA)
-{
-    int b = 1;
-    while (b < 31 && (1ll << b) < (long long)colA) ++b;
-    return b;
-}
+// device buffers freed at scope exit
+struct DevBufs {
+    void *p[16] = {};
+    int n = 0;
+    template <typename T>
+    hipError_t get(T **out, size_t bytes)
+    {
+        void *q = nullptr;
+        hipError_t e = hipMalloc(&q, bytes ? bytes : 16);
+        if (e == hipSuccess) p[n++] = q;
+        *out = (T *)q;
+        return e;
+    }
+    ~DevBufs()
+    {
+        for (int i = 0; i < n; ++i) (void)hipFree(p[i]);
+    }
+};
 
 #define TCHK(x)                                     \
     do {                                            \
@@ -203,144 +222,116 @@ int bits_for(int colA)
         if (e_ != hipSuccess) return (int)e_;       \
     } while (0)
 
-// Distinct columns of every segment [beg, end): sorted keys + flags + scan.
-// Outputs (device): pos (n+1 ints, exclusive scan of flags), dcols (<= n).
-struct DistinctWork {
-    int *sorted = nullptr, *flag = nullptr, *pos = nullptr, *dcols = nullptr;
-    uint8_t *head = nullptr;
-    ~DistinctWork()
-    {
-        (void)hipFree(sorted);
-        (void)hipFree(flag);
-        (void)hipFree(pos);
-        (void)hipFree(dcols);
-        (void)hipFree(head);
-    }
-};
-
-int distinct_segments(const int *d_idx, long long n, int colA, int nseg, const int *beg, const int *end,
-                      DistinctWork &w, Scratch &tmp, hipStream_t s)
+template <typename T>
+int scan_excl(Scratch &tmp, const T *in, T *out, size_t n, hipStream_t s)
 {
-    const size_t nn = (size_t)(n > 0 ? n : 1);
-    if (!w.sorted) {
-        TCHK(hipMalloc(&w.sorted, nn * sizeof(int)));
-        TCHK(hipMalloc(&w.flag, (nn + 1) * sizeof(int)));
-        TCHK(hipMalloc(&w.pos, (nn + 1) * sizeof(int)));
-        TCHK(hipMalloc(&w.dcols, nn * sizeof(int)));
-        TCHK(hipMalloc(&w.head, nn));
-    }
-    if (n == 0) return (int)hipMemsetAsync(w.pos, 0, sizeof(int), s);
     size_t need = 0;
-    TCHK(rocprim::segmented_radix_sort_keys(nullptr, need, d_idx, w.sorted, (unsigned)n, (unsigned)nseg, beg,
-                                            end, 0, (unsigned)bits_for(colA), s));
+    TCHK(rocprim::exclusive_scan(nullptr, need, in, out, T(0), n, rocprim::plus<T>(), s));
     TCHK(tmp.grow(need));
-    TCHK(rocprim::segmented_radix_sort_keys(tmp.p, need, d_idx, w.sorted, (unsigned)n, (unsigned)nseg, beg,
-                                            end, 0, (unsigned)bits_for(colA), s));
-    TCHK(hipMemsetAsync(w.head, 0, nn, s));
-    TCHK(hipMemsetAsync(w.flag + n, 0, sizeof(int), s));
-    head_kernel<<<nblocks(nseg), kThreads, 0, s>>>(beg, end, nseg, w.head);
-    flag_kernel<<<nblocks(n), kThreads, 0, s>>>(w.sorted, w.head, n, w.flag);
-    // exclusive scan over n+1 flags (the last is 0): pos[n] = distinct total
-    need = 0;
-    TCHK(rocprim::exclusive_scan(nullptr, need, w.flag, w.pos, 0, (size_t)n + 1, rocprim::plus<int>(), s));
-    TCHK(tmp.grow(need));
-    TCHK(rocprim::exclusive_scan(tmp.p, need, w.flag, w.pos, 0, (size_t)n + 1, rocprim::plus<int>(), s));
-    distinct_scatter_kernel<<<nblocks(n), kThreads, 0, s>>>(w.sorted, w.flag, w.pos, n, w.dcols);
-    return (int)hipGetLastError();
+    TCHK(rocprim::exclusive_scan(tmp.p, need, in, out, T(0), n, rocprim::plus<T>(), s));
+    return 0;
 }
 
-int tile_create_device(tsp_dev_tiles *out, int rows, int colA, long long nnz, const int *d_ptr,
-                           const int *d_idx, const void *d_val, int BM, int BN, int prec, void *stream)
+int tile_create_device(tsp_dev_tiles *out, int rows, int colA, long long nnz, const int *d_ptr, const int *d_idx,
+                       const void *d_val, int BM, int BN, int prec, void *stream)
 {
     if (!out || rows < 0 || colA <= 0 || nnz < 0 || nnz > 0x7ffffff0LL) return TSP_EINVAL;
     if ((BM != 64 && BM != 16 && BM != 8) || BN <= 0 || BN > 32) return TSP_EINVAL;
     if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
     if (rows > 0 && (!d_ptr || (nnz > 0 && (!d_idx || !d_val)))) return TSP_EINVAL;
     hipStream_t s = (hipStream_t)stream;
-    memset(out, 0, sizeof *out);
     out->bm = BM;
     out->bn = BN;
     out->prec = prec;
     out->bitmap_words = (BM * BN + 63) / 64;
     const int tilem = (rows + BM - 1) / BM;
     out->tilem = tilem;
+    const size_t vs = prec == TSP_PREC_FP16 ? 2 : 4;
     TCHK(hipMalloc(&out->d_tile_ptr, sizeof(int) * ((size_t)tilem + 1)));
-    if (tilem == 0) {
-        TCHK(hipMemsetAsync(out->d_tile_ptr, 0, sizeof(int), s));
+    if (tilem == 0 || nnz == 0) {
+        // no entries: every row-block has zero tiles
+        TCHK(hipMemsetAsync(out->d_tile_ptr, 0, sizeof(int) * ((size_t)tilem + 1), s));
+        TCHK(hipMalloc(&out->d_tile_colidx, 16));
+        TCHK(hipMalloc(&out->d_val, 16));
+        TCHK(hipMalloc((void **)&out->d_bitmap, 16));
+        TCHK(hipMalloc(&out->d_tile_nnz, sizeof(int)));
+        TCHK(hipMemsetAsync(out->d_tile_nnz, 0, sizeof(int), s));
         return (int)hipStreamSynchronize(s);
     }
-    int *beg = nullptr, *end = nullptr, *dstart = nullptr, *dcount = nullptr, *nt = nullptr;
+    const int cbits = bits_for(colA);
+    const int bbits = bits_for(tilem);
+    const size_t n = (size_t)nnz;
+    DevBufs db;
     Scratch tmp;
-    DistinctWork w;
-    struct Free {
-        int **a[5];
-        ~Free()
-        {
-            for (int **p : a) (void)hipFree(*p);
-        }
-    } fr{{&beg, &end, &dstart, &dcount, &nt}};
-    TCHK(hipMalloc(&beg, sizeof(int) * (size_t)tilem));
-    TCHK(hipMalloc(&end, sizeof(int) * (size_t)tilem));
-    TCHK(hipMalloc(&dstart, sizeof(int) * (size_t)tilem));
-    TCHK(hipMalloc(&dcount, sizeof(int) * (size_t)tilem));
-    TCHK(hipMalloc(&nt, sizeof(int) * ((size_t)tilem + 1)));
-    seg_bounds_kernel<<<nblocks(tilem), kThreads, 0, s>>>(d_ptr, rows, tilem, BM, 0, BM, beg, end);
-    int st = distinct_segments(d_idx, nnz, colA, tilem, beg, end, w, tmp, s);
-    if (st) return st;
-    seg_distinct_kernel<<<nblocks(tilem), kThreads, 0, s>>>(beg, end, w.pos, tilem, dstart, dcount);
-    TCHK(hipMemsetAsync(nt + tilem, 0, sizeof(int), s));
-    ntiles_kernel<<<nblocks(tilem), kThreads, 0, s>>>(dcount, tilem, BN, nt);
+    unsigned long long *key = nullptr, *key2 = nullptr;
+    int *ent = nullptr, *ent2 = nullptr, *flag = nullptr, *run = nullptr, *run_start = nullptr, *dcols = nullptr;
+    int *bptr = nullptr, *dstart = nullptr, *nt = nullptr, *bad = nullptr;
+    uint8_t *lrow = nullptr;
+    TCHK(db.get(&key, n * 8));
+    TCHK(db.get(&key2, n * 8));
+    TCHK(db.get(&ent, n * 4));
+    TCHK(db.get(&ent2, n * 4));
+    TCHK(db.get(&lrow, n));
+    TCHK(db.get(&flag, (n + 1) * 4));
+    TCHK(db.get(&run, (n + 1) * 4));
+    TCHK(db.get(&run_start, n * 4));
+    TCHK(db.get(&dcols, n * 4));
+    TCHK(db.get(&bptr, ((size_t)tilem + 1) * 4));
+    TCHK(db.get(&dstart, ((size_t)tilem + 1) * 4));
+    TCHK(db.get(&nt, ((size_t)tilem + 1) * 4));
+    TCHK(db.get(&bad, 4));
+    TCHK(hipMemsetAsync(bad, 0, 4, s));
+    block_ptr_kernel<<<nblocks(tilem + 1), kThreads, 0, s>>>(d_ptr, rows, tilem, BM, bptr);
+    key_kernel<<<nblocks(nnz), kThreads, 0, s>>>(d_ptr, d_idx, rows, nnz, BM, cbits, colA, key, ent, lrow, bad);
+    // 1. stable sort by (block, column)
     size_t need = 0;
-    TCHK(rocprim::exclusive_scan(nullptr, need, nt, out->d_tile_ptr, 0, (size_t)tilem + 1,
-                                 rocprim::plus<int>(), s));
+    TCHK(rocprim::radix_sort_pairs(nullptr, need, key, key2, ent, ent2, n, 0, cbits + bbits, s));
     TCHK(tmp.grow(need));
-    TCHK(rocprim::exclusive_scan(tmp.p, need, nt, out->d_tile_ptr, 0, (size_t)tilem + 1,
-                                 rocprim::plus<int>(), s));
-    // every tile holds at least one CSR entry, so tilenum <= nnz < 2^31
-    int tilenum = 0;
-    TCHK(hipMemcpyAsync(&tilenum, out->d_tile_ptr + tilem, sizeof(int), hipMemcpyDeviceToHost, s));
+    TCHK(rocprim::radix_sort_pairs(tmp.p, need, key, key2, ent, ent2, n, 0, cbits + bbits, s));
+    // 2. runs
+    TCHK(hipMemsetAsync(flag + n, 0, 4, s));
+    head_kernel<<<nblocks(nnz), kThreads, 0, s>>>(key2, nnz, flag);
+    if (int st = scan_excl(tmp, flag, run, n + 1, s)) return st;
+    run_scatter_kernel<<<nblocks(nnz), kThreads, 0, s>>>(key2, flag, run, nnz, (1u << cbits) - 1u, run_start,
+                                                        dcols);
+    // 3. tiles per block, tile_ptr
+    TCHK(hipMemsetAsync(nt + tilem, 0, 4, s));
+    block_runs_kernel<<<nblocks(tilem), kThreads, 0, s>>>(bptr, run, tilem, BN, dstart, nt);
+    int nruns = 0;
+    TCHK(hipMemcpyAsync(&nruns, run + n, 4, hipMemcpyDeviceToHost, s));
+    TCHK(hipMemcpyAsync(dstart + tilem, run + n, 4, hipMemcpyDeviceToDevice, s));
+    if (int st = scan_excl(tmp, nt, out->d_tile_ptr, (size_t)tilem + 1, s)) return st;
+    int tilenum = 0, nbad = 0;
+    TCHK(hipMemcpyAsync(&tilenum, out->d_tile_ptr + tilem, 4, hipMemcpyDeviceToHost, s));
+    TCHK(hipMemcpyAsync(&nbad, bad, 4, hipMemcpyDeviceToHost, s));
     TCHK(hipStreamSynchronize(s));
+    if (nbad) return TSP_EINVAL;        // a column outside [0, colA)
+    // every tile holds at least one entry, so tilenum <= nnz < 2^31
     out->tilenum = tilenum;
-    const size_t vs = prec == TSP_PREC_FP16 ? 2 : 4;
-    const size_t tn = (size_t)(tilenum > 0 ? tilenum : 1);
-    TCHK(hipMalloc(&out->d_tile_colidx, sizeof(int) * tn * BN));
-    TCHK(hipMalloc(&out->d_tile_nnz, sizeof(int) * (tn + 1)));
+    const size_t tn = (size_t)tilenum;
+    TCHK(hipMalloc(&out->d_tile_colidx, 4 * tn * BN));
+    TCHK(hipMalloc(&out->d_tile_nnz, 4 * (tn + 1)));
     TCHK(hipMalloc(&out->d_val, vs * tn * BM * BN));
-    TCHK(hipMalloc((void **)&out->d_bitmap, sizeof(uint64_t) * tn * out->bitmap_words));
+    TCHK(hipMalloc((void **)&out->d_bitmap, 8 * tn * out->bitmap_words));
     int *cnt = nullptr;
-    TCHK(hipMalloc(&cnt, sizeof(int) * (tn + 2)));    // + the invalid-column counter
-    struct FreeCnt {
-        int *p;
-        ~FreeCnt() { (void)hipFree(p); }
-    } fc{cnt};
-    TCHK(hipMemsetAsync(cnt, 0, sizeof(int) * (tn + 2), s));
-    int *bad = cnt + tn + 1;
+    TCHK(db.get(&cnt, 4 * (tn + 1)));
+    TCHK(hipMemsetAsync(cnt, 0, 4 * (tn + 1), s));
     TCHK(hipMemsetAsync(out->d_val, 0, vs * tn * BM * BN, s));
-    TCHK(hipMemsetAsync(out->d_bitmap, 0, sizeof(uint64_t) * tn * out->bitmap_words, s));
-    if (tilenum > 0) {
-        colidx_kernel<<<tilem, kThreads, 0, s>>>(out->d_tile_ptr, dstart, dcount, w.dcols, BN, out->d_tile_colidx);
-        if (prec == TSP_PREC_FP16)
-            fill_kernel<_Float16><<<nblocks(rows), kThreads, 0, s>>>(
-                d_ptr, d_idx, (const _Float16 *)d_val, rows, BM, BN, out->bitmap_words, out->d_tile_ptr, dstart,
-                dcount, w.dcols, cnt, bad, (_Float16 *)out->d_val, (unsigned long long *)out->d_bitmap);
-        else
-            fill_kernel<float><<<nblocks(rows), kThreads, 0, s>>>(
-                d_ptr, d_idx, (const float *)d_val, rows, BM, BN, out->bitmap_words, out->d_tile_ptr, dstart,
-                dcount, w.dcols, cnt, bad, (float *)out->d_val, (unsigned long long *)out->d_bitmap);
-        TCHK(hipGetLastError());
-        need = 0;
-        TCHK(rocprim::exclusive_scan(nullptr, need, cnt, out->d_tile_nnz, 0, (size_t)tilenum + 1,
-                                     rocprim::plus<int>(), s));
-        TCHK(tmp.grow(need));
-        TCHK(rocprim::exclusive_scan(tmp.p, need, cnt, out->d_tile_nnz, 0, (size_t)tilenum + 1,
-                                     rocprim::plus<int>(), s));
-    } else {
-        TCHK(hipMemsetAsync(out->d_tile_nnz, 0, sizeof(int), s));
-    }
-    int nbad = 0;
-    TCHK(hipMemcpyAsync(&nbad, bad, sizeof(int), hipMemcpyDeviceToHost, s));
-    TCHK(hipStreamSynchronize(s));
-    return nbad ? TSP_EINVAL : TSP_OK;
+    TCHK(hipMemsetAsync(out->d_bitmap, 0, 8 * tn * out->bitmap_words, s));
+    colidx_kernel<<<tilem, kThreads, 0, s>>>(out->d_tile_ptr, dstart, dcols, BN, out->d_tile_colidx);
+    // 4. values, counts, bitmaps
+    if (prec == TSP_PREC_FP16)
+        fill_kernel<_Float16><<<nblocks(nruns), kThreads, 0, s>>>(
+            key2, ent2, lrow, (const _Float16 *)d_val, run_start, nruns, nnz, cbits, BM, BN, out->bitmap_words,
+            out->d_tile_ptr, dstart, cnt, (_Float16 *)out->d_val, (unsigned long long *)out->d_bitmap);
+    else
+        fill_kernel<float><<<nblocks(nruns), kThreads, 0, s>>>(
+            key2, ent2, lrow, (const float *)d_val, run_start, nruns, nnz, cbits, BM, BN, out->bitmap_words,
+            out->d_tile_ptr, dstart, cnt, (float *)out->d_val, (unsigned long long *)out->d_bitmap);
+    TCHK(hipGetLastError());
+    // 5. tile_nnz
+    if (int st = scan_excl(tmp, cnt, out->d_tile_nnz, tn + 1, s)) return st;
+    return (int)hipStreamSynchronize(s);
 }
 
 }  // namespace
