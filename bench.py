@@ -35,6 +35,38 @@ def alg_bytes(rows, nnz, s_a, k_rows, n, s_b):
     return 4 * (rows + 1) + nnz * (4 + s_a) + k_rows * n * s_b + rows * n * 4
 
 
+def gather_calibration(hip, reps):
+    """Random 128/256-byte row gathers from tables of 2 MB .. 2 GB
+    (tsp_gather_kernel): the bandwidth ceiling of B-row gathers."""
+    import ctypes as C
+    maxb = 2 << 30
+    tab, sink = C.c_void_p(), C.c_void_p()
+    assert hip.tsp_malloc(C.byref(tab), maxb) == 0 and hip.tsp_malloc(C.byref(sink), 8192 * 256 * 4) == 0
+    hip.tsp_memset(tab, 1, maxb)
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    hip.tsp_event_create(C.byref(e0))
+    hip.tsp_event_create(C.byref(e1))
+    iters = 64
+    for rowb in (128, 256):
+        for mb in (2, 8, 32, 128, 256, 512, 1024, 2048):
+            nb = mb << 20
+            for w in range(3):
+                assert hip.tsp_gather_kernel(tab, nb, rowb, iters, w, sink, None) == 0
+            hip.tsp_event_record(e0, None)
+            for r in range(reps):
+                hip.tsp_gather_kernel(tab, nb, rowb, iters, 100 + r, sink, None)
+            hip.tsp_event_record(e1, None)
+            hip.tsp_event_sync(e1)
+            ms = C.c_float()
+            hip.tsp_event_elapsed_ms(C.byref(ms), e0, e1)
+            t = ms.value / reps
+            nbytes = 8192 * 256 * 16 * iters
+            print(json.dumps({"gather_row_bytes": rowb, "table_mb": mb, "ms": round(t, 5),
+                              "gbs": round(nbytes / (t * 1e-3) / 1e9, 1)}), flush=True)
+    hip.tsp_free(tab)
+    hip.tsp_free(sink)
+
+
 def copy_calibration(hip, nbytes, reps):
     """Plain 16-byte-vector copy of nbytes (dst = src): its FETCH_SIZE /
     WRITE_SIZE per dispatch calibrate the HBM byte counters, its time gives the
@@ -98,10 +130,18 @@ def main():
     ap.add_argument("--gamma", type=float, default=None)
     ap.add_argument("--delta", type=float, default=None)
     ap.add_argument("--no-tune", action="store_true")
+    ints3 = lambda s: [int(x) for x in s.split(",")]
+    ap.add_argument("--th", type=ints3, default=None, help="pin thresholds TH64,TH16,TH8 (after tuning, if any)")
+    ap.add_argument("--format", type=ints3, default=None,
+                    help="pin the A format per class 64,16,8 (1 dense, 2 packed, 0 keep)")
+    ap.add_argument("--order", type=ints3, default=None,
+                    help="pin the chunk order per class 64,16,8 (1 side by side, 2 chunk-major, 0 keep)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-vendor", action="store_true")
     ap.add_argument("--class-reps", type=int, default=200)
     ap.add_argument("--sweep", action="store_true", help="time every kernel variant per class instead")
+    ap.add_argument("--gather", action="store_true",
+                    help="only run the random row-gather probe (gather bandwidth ceiling)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run the plain copy kernel on this many bytes (counter calibration)")
     args = ap.parse_args()
@@ -114,6 +154,9 @@ def main():
     hip, host = tsp.load()
     if not tsp.device_available():
         raise SystemExit("bench.py: no gfx950 device")
+    if args.gather:
+        gather_calibration(hip, min(args.steps, 20))
+        return
     if args.copy_bytes:
         copy_calibration(hip, args.copy_bytes, args.steps)
         return
@@ -142,6 +185,16 @@ def main():
 
     plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
     th, model_ms, tune_ms = plan.tune(not args.no_tune)
+    if args.th:
+        plan.set_th(*args.th)
+        th = tuple(args.th)
+    for bm, f in zip((64, 16, 8), args.format or ()):
+        if f:
+            plan.set_format(bm, f)
+    for bm, o in zip((64, 16, 8), args.order or ()):
+        if o:
+            w, st, tpw, _ = plan.get_variant(bm)
+            plan.set_variant(bm, w, st, tpw, o)
     log(f"thresholds {th} (model {model_ms:.1f} ms, tuning {tune_ms:.1f} ms)")
 
     if args.sweep:
@@ -167,6 +220,7 @@ def main():
         b = alg_bytes(sb.rows, sb.nnz, s, k_rows, colB, s)
         cls[bm] = {"ms": cms, "rows": sb.rows, "nnz": int(sb.nnz), "tiles": t.tilenum,
                    "format": {1: "dense", 2: "packed"}.get(plan.get_format(bm), "?"),
+                   "order": {0: "side-by-side", 1: "side-by-side", 2: "chunk-major"}[plan.get_variant(bm)[3]],
                    "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9}
     dom = max(cls, key=lambda k: cls[k]["ms"])
     k_all = int(np.unique(A.colidx).size)

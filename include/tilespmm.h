@@ -197,6 +197,9 @@ int tsp_plan_set_variant(tsp_plan *plan, int bm, int w, int stages, int tasks_pe
  * current format (0 for an empty class, -1 on a bad argument). */
 int tsp_plan_set_format(tsp_plan *plan, int bm, int fmt);
 int tsp_plan_get_format(tsp_plan *plan, int bm);
+/* The variant a class is pinned to (0 = library default), e.g. after
+ * tsp_plan_tune picked the chunk order. */
+int tsp_plan_get_variant(tsp_plan *plan, int bm, int *w, int *stages, int *tasks_per_wave, int *order);
 /* Launch the three classes once (each on its own stream, joined on the null
  * stream).  zero_c != 0 clears C first. */
 int tsp_plan_run(tsp_plan *plan, int zero_c);

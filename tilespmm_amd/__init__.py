@@ -167,6 +167,7 @@ HIP_SYMBOLS = {
                                   C.c_int, _P, _P, C.c_int, C.c_int, C.POINTER(C.c_double),
                                   C.POINTER(C.c_double)]),
     "tsp_copy_kernel": (C.c_int, [_P, _P, C.c_size_t, _P]),
+    "tsp_gather_kernel": (C.c_int, [_P, C.c_size_t, C.c_int, C.c_int, C.c_uint, _P, _P]),
     "tsp_tile_create_device": (C.c_int, [C.POINTER(DevTiles), C.c_int, C.c_int, C.c_longlong, _P, _P, _P,
                                          C.c_int, C.c_int, C.c_int, _P]),
     "tsp_dev_tiles_free": (C.c_int, [C.POINTER(DevTiles)]),
@@ -213,6 +214,7 @@ HOST_SYMBOLS = {
     "tsp_plan_set_variant": (C.c_int, [_P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "tsp_plan_set_format": (C.c_int, [_P, C.c_int, C.c_int]),
     "tsp_plan_get_format": (C.c_int, [_P, C.c_int]),
+    "tsp_plan_get_variant": (C.c_int, [_P, C.c_int, _IP, _IP, _IP, _IP]),
     "tsp_plan_run": (C.c_int, [_P, C.c_int]),
     "tsp_plan_warmup": (C.c_int, [_P, C.c_int]),
     "tsp_plan_time": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double)]),
@@ -613,6 +615,12 @@ class Plan:
 
     def get_format(self, bm: int) -> int:
         return load()[1].tsp_plan_get_format(self.p, bm)
+
+    def get_variant(self, bm: int):
+        """(w, stages, tasks_per_wave, order) the class is pinned to (0 = default)."""
+        v = [C.c_int() for _ in range(4)]
+        _check("tsp_plan_get_variant", load()[1].tsp_plan_get_variant(self.p, bm, *[C.byref(x) for x in v]))
+        return tuple(x.value for x in v)
 
     def run(self, zero_c: bool = True):
         _check("tsp_plan_run", load()[1].tsp_plan_run(self.p, int(zero_c)))

@@ -237,4 +237,13 @@ int tsp_copy_kernel(void *dst, const void *src, size_t bytes, void *stream)
     return tsp::launch_copy(dst, src, bytes, (hipStream_t)stream);
 }
 
+int tsp_gather_kernel(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed,
+                      void *sink, void *stream)
+{
+    if (!table || !sink || (row_bytes != 128 && row_bytes != 256) || iters <= 0) return TSP_EINVAL;
+    if (table_bytes < (size_t)row_bytes || table_bytes / (size_t)row_bytes > 0xffffffffull) return TSP_EINVAL;
+    if ((uintptr_t)table & 15) return TSP_EINVAL;
+    return tsp::launch_gather(table, table_bytes, row_bytes, iters, seed, sink, (hipStream_t)stream);
+}
+
 }  // extern "C"

@@ -30,5 +30,8 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
            const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
            const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order);
 int launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
+constexpr int kGatherBlocks = 8192;      // gather probe grid: 8192 x 256 threads
+int launch_gather(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed, void *sink,
+                  hipStream_t s);
 
 }  // namespace tsp

@@ -523,6 +523,48 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
     return TSP_EINVAL;
 }
 
+// Random row gathers from a table: each group of ROWB/16 lanes reads one
+// ROWB-byte row (16 bytes per lane) per iteration, rows drawn uniformly by an
+// integer hash.  The XOR of everything read is stored only when an
+// improbable bit pattern appears, which keeps the loads live without output
+// traffic.  Measures the gather bandwidth ceiling of row-wise SpMM.
+__device__ __forceinline__ uint32_t hash32(uint32_t x)
+{
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    x ^= x >> 16;
+    return x;
+}
+
+template <int ROWB>
+__global__ __launch_bounds__(256) void gather_kernel(const u4 *__restrict__ tab, uint32_t nrows, int iters,
+                                                     uint32_t seed, uint32_t *__restrict__ sink)
+{
+    constexpr int RL = ROWB / 16;
+    const uint32_t tid = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t grp = tid / RL, sub = tid % RL;
+    u4 acc = {0u, 0u, 0u, 0u};
+#pragma unroll 8
+    for (int i = 0; i < iters; ++i) {
+        const uint32_t r = hash32(grp * 2654435761u + (uint32_t)i * 40503u + seed) % nrows;
+        acc ^= tab[(size_t)r * RL + sub];
+    }
+    if ((acc.x & 0xfffffu) == 0x12345u) sink[tid] = acc.x ^ acc.y ^ acc.z ^ acc.w;
+}
+
+int launch_gather(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed, void *sink,
+                  hipStream_t s)
+{
+    const uint32_t nrows = (uint32_t)(table_bytes / (size_t)row_bytes);
+    if (row_bytes == 128)
+        gather_kernel<128><<<kGatherBlocks, 256, 0, s>>>((const u4 *)table, nrows, iters, seed, (uint32_t *)sink);
+    else
+        gather_kernel<256><<<kGatherBlocks, 256, 0, s>>>((const u4 *)table, nrows, iters, seed, (uint32_t *)sink);
+    return (int)hipGetLastError();
+}
+
 int launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s)
 {
     const size_t n = bytes / 16;

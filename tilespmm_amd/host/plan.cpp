@@ -230,6 +230,20 @@ extern "C" int tsp_plan_set_variant(tsp_plan *p, int bm, int w, int stages, int 
     return TSP_EINVAL;
 }
 
+extern "C" int tsp_plan_get_variant(tsp_plan *p, int bm, int *w, int *stages, int *tasks_per_wave, int *order)
+{
+    if (!p || !w || !stages || !tasks_per_wave || !order) return TSP_EINVAL;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) {
+            *w = c.var_w;
+            *stages = c.var_s;
+            *tasks_per_wave = c.var_tpw;
+            *order = c.var_order;
+            return TSP_OK;
+        }
+    return TSP_EINVAL;
+}
+
 extern "C" int tsp_plan_destroy(tsp_plan *p)
 {
     if (!p) return TSP_OK;

@@ -17,10 +17,20 @@ tool rebuilds the policy for gfx950:
             left_feature = right_feature = -1).
   check  -- report, per swept matrix, the policy's pick vs the exhaustive
             optimum (the "checked against exhaustive tuning" figure).
+  thsweep -- per matrix / precision / colB and active row class, the class
+            kernel's time at every split threshold TH = 8..128 (distinct task
+            counts only) plus the class's tile-length histogram and probed
+            resources.
+  thfit  -- fit the threshold cost model's weights (lambda_atom, and the
+            weight of the L2 re-read term) so that the model's top-4
+            thresholds, which the runtime tuning times, contain a near-best
+            one; writes tilespmm_amd/host/th_calibration.h.
 
   python -m tilespmm_amd.policy_tune sweep --corpus small --out gpurun_out/policy.jsonl
   python -m tilespmm_amd.policy_tune fit --inp gpurun_out/policy.jsonl
   python -m tilespmm_amd.policy_tune check --inp gpurun_out/policy.jsonl
+  python -m tilespmm_amd.policy_tune thsweep --configs 1 2 3 4 --corpus small --out gpurun_out/th.jsonl
+  python -m tilespmm_amd.policy_tune thfit --inp gpurun_out/th.jsonl --header tilespmm_amd/host/th_calibration.h
 """
 from __future__ import annotations
 
