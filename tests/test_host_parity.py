@@ -220,6 +220,56 @@ def test_mm_read_matches_oracle(tsp, orc, dc2_path, tmp_path):
         assert np.array_equal(np.asarray(x), np.asarray(y))
 
 
+def test_mm_read_values_correctly_rounded(tsp, tmp_path):
+    """Every decimal spelling of a value parses to the correctly rounded
+    double (Python's float() is correctly rounded): short decimals, 17
+    significant digits, exponents at and beyond the fast-path range, signs,
+    leading zeros, integers, and more than 19 digits."""
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal(4000) * 10.0 ** rng.integers(-30, 30, 4000)
+    toks = []
+    for i, v in enumerate(x):
+        f = ["%.17g", "%.6e", "%.3f", "%+.9E", "%.0f", "%.25f", "%.20e"][i % 7]
+        toks.append(f % v)
+    toks += ["0", "-0", "+0.0", "000123", "-000.000450", "1e22", "1e23", "9007199254740993", "1.5e-22",
+             "4.9e-324", "1.7976931348623157e308", "12345678901234567890123", "0.1", ".5", "5.", "-.25e+2"]
+    n = len(toks)
+    body = "".join(f"{i + 1} 1 {t}\n" for i, t in enumerate(toks))
+    p = tmp_path / "v.mtx"
+    p.write_text(f"%%MatrixMarket matrix coordinate real general\n{n} 1 {n}\n" + body)
+    m, _, rp, ci, v, _ = tsp.mm_read(str(p))
+    want = np.array([float(t) for t in toks])
+    assert m == n and np.array_equal(rp, np.arange(n + 1))
+    assert np.array_equal(v.view(np.uint64), want.view(np.uint64))
+
+
+def test_mm_read_parallel_and_fallback(tsp, orc, tmp_path):
+    """A multi-chunk file (parsed in parallel) and the same entries spread
+    over several lines per entry (parsed by the sequential fallback) give the
+    oracle's CSR, for general, symmetric, pattern and integer files."""
+    rng = np.random.default_rng(12)
+    n, nz = 3000, 120000
+    r = rng.integers(1, n + 1, nz)
+    c = rng.integers(1, n + 1, nz)
+    vals = rng.integers(-50, 50, nz)
+    for kind in ("real general", "real symmetric", "pattern general", "integer general"):
+        if "pattern" in kind:
+            lines = [f"{a} {b}" for a, b in zip(r, c)]
+        else:
+            lines = [f"{a} {b} {v}" for a, b, v in zip(r, c, vals)]
+        if "symmetric" in kind:
+            keep = r >= c
+            lines = [l for l, k in zip(lines, keep) if k]
+        for split in (False, True):
+            body = "\n".join(l.replace(" ", "\n") if split else l for l in lines) + "\n"
+            p = tmp_path / "p.mtx"
+            p.write_text(f"%%MatrixMarket matrix coordinate {kind}\n% comment\n{n} {n} {len(lines)}\n" + body)
+            a, b = tsp.mm_read(str(p)), orc.mm_read(str(p))
+            for x, y in zip(a[:5], b[:5]):
+                assert np.array_equal(np.asarray(x), np.asarray(y)), (kind, split)
+            assert a[5] == b[5]
+
+
 def test_mm_read_errors(tsp, tmp_path):
     with pytest.raises(tsp.TspError):
         tsp.mm_read(str(tmp_path / "missing.mtx"))
