@@ -191,15 +191,15 @@ def time_candidate(A, B, colB, cbp, g, d, reps, tune):
     """Split + tiles + thresholds (cost-model top-1, or runtime-tuned) and the
     mean time of `reps` full SpMM steps."""
     subs = tsp.matrix_split(A, g, d)
-    tiles = [tsp.tile_create(s, A.cols, bm, A.prec) for s, bm in zip(subs, (64, 16, 8))]
-    plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, A.prec, B)
+    plan = tsp.Plan.from_csr(subs, A.rows, A.cols, cbp, A.prec, B)     # tiles built on the GPU
     try:
         th, _, _ = plan.tune(tune)
         plan.warmup(5)
         ms = plan.time(reps)
+        tilenum = [tsp.load()[1].tsp_plan_tilenum(plan.p, bm) for bm in (64, 16, 8)]
     finally:
         plan.close()
-    return ms, th, [t.tilenum for t in tiles]
+    return ms, th, tilenum
 
 
 def sweep_matrix(name, A, colB, reps, out, tune=False):
@@ -355,6 +355,26 @@ def cmd_fit(args):
                              "right": shift(n["right"])})
         roots.append(shift(root))
     note = f"{len(recs)} swept (matrix, colB, precision) cases, depth <= {args.depth}"
+    if args.lomo:
+        # leave one matrix out: refit without it, score its cases
+        def walk(root, nodes, f):
+            x = root
+            while x >= 0:
+                n = nodes[x]
+                x = n["left"] if np.float32(f[n["feature"] + 2]) < np.float32(n["cut"]) else n["right"]
+            return -1 - x
+        reg, insample = [], []
+        for prec in (0, 1):
+            rs = [r for r in recs if r["prec"] == prec]
+            root, nodes = fit_tree(rs, args.depth, args.min_leaf)
+            insample += [r["times_ms"][walk(root, nodes, r["features"])] / r["best_ms"] for r in rs]
+            for m in sorted(set(r["matrix"] for r in rs)):
+                root, nodes = fit_tree([r for r in rs if r["matrix"] != m], args.depth, args.min_leaf)
+                reg += [r["times_ms"][walk(root, nodes, r["features"])] / r["best_ms"]
+                        for r in rs if r["matrix"] == m]
+        note += (f"; in-sample mean x{np.mean(insample):.3f} worst x{np.max(insample):.3f}, "
+                 f"leave-one-matrix-out mean x{np.mean(reg):.3f} worst x{np.max(reg):.3f}")
+        print(note)
     export_header(args.header, roots, allnodes, note)
     print(f"wrote {args.header}: {len(allnodes)} nodes, roots {roots}")
 
@@ -577,6 +597,7 @@ def main():
     f.add_argument("--header", default=os.path.join(HERE, "host", "policy_model.h"))
     f.add_argument("--depth", type=int, default=4)
     f.add_argument("--min-leaf", type=int, default=3)
+    f.add_argument("--lomo", action="store_true", help="also report leave-one-matrix-out regret")
     c = sub.add_parser("check")
     c.add_argument("--inp", required=True)
     args = ap.parse_args()
