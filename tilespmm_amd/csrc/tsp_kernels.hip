@@ -11,15 +11,20 @@
 //     columns.  The tiles of consecutive tasks are contiguous in memory, so
 //     the wave streams them through one software pipeline that never drains
 //     at task boundaries; at a boundary it only flushes its accumulators to C
-//     (plain stores, or fp32 atomics for split tasks) and clears them.  A
-//     256-thread block runs four independent waves: there is no block barrier;
+//     and clears them.  Consecutive tasks of one split row-block keep
+//     accumulating; a flush is a plain vector store unless other waves also
+//     write the row-block, then fp32 atomics whose lanes cover whole rows
+//     (the slab is transposed through LDS first).  A 256-thread block runs
+//     four independent waves: there is no block barrier;
 //   * S tiles are in flight per wave: the B row panel (BN rows x W columns,
 //     16-byte vector loads) and the A fragment of tile t+S are loaded while
-//     tile t is computed, and the column indices of tile t+S+1 one step
-//     earlier still (they feed the B addresses);
+//     tile t is computed, and the column indices of tile t+2S (they feed the
+//     B addresses) S steps earlier still;
 //   * the B panel is staged in a wave-private LDS slice (one wave's LDS
-//     operations execute in issue order, so one buffer is safe) and read back
-//     in MFMA operand order;
+//     operations execute in issue order, so one buffer is safe).  MFMA
+//     column n of 16-column block c is chunk column n*CB + c (CB = W/16
+//     blocks), so a lane reads CB adjacent values of a B row with one LDS
+//     read and owns CB adjacent output columns (one vector store per row);
 //   * A tiles are canonical row-major BM x BN blocks read straight into MFMA
 //     operand registers (8 or 16 bytes per lane);
 //   * fp16: v_mfma_f32_16x16x16_f16 (BN = 16) and v_mfma_f32_16x16x32_f16
@@ -99,14 +104,18 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     constexpr int VPR = W / VV;              // vectors per panel row
     constexpr int NV = BN * VPR / 64;        // vectors per lane per tile
     static_assert(NV >= 1 && (BN * VPR) % 64 == 0, "panel does not tile the wave");
-    constexpr int LDSW = F16 ? W + 4 : W + (BN == 8 ? 8 : 4);
+    // LDS row stride: a multiple of the CB-value vectors the MFMA operand
+    // reads use (up to 32 bytes), padded so consecutive rows shift banks
+    constexpr int LDSW = W + 8;
     constexpr int RG = BM >= 16 ? BM / 16 : 1;   // 16-row MFMA row groups
     constexpr int CB = W / 16;                   // 16-column MFMA blocks
     constexpr int KS = F16 ? 1 : BN / 4;         // tf32 MFMA steps per tile
     constexpr int AW = F16 ? (BN == 32 ? 4 : 2) : KS;   // A words per row group
     using VT = typename std::conditional<F16, _Float16, float>::type;
+    using RV = VT __attribute__((ext_vector_type(CB)));     // CB values of one B row
+    using FV = float __attribute__((ext_vector_type(CB)));  // CB output columns
 
-    __shared__ __attribute__((aligned(16))) VT lds_all[kWavesPerBlock][BN * LDSW];
+    __shared__ __attribute__((aligned(32))) VT lds_all[kWavesPerBlock][BN * LDSW];
 
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform per wave
@@ -126,6 +135,7 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     int k = k0;
     int kend = uload(colstart, k0 + 1);
     while (kend <= tb) kend = uload(colstart, ++k + 1);  // skip leading empty tasks
+    int gfirst = k;                  // first task of the accumulation group
     const int col0 = chunk * W;
 
     VT *lds = lds_all[wid];
@@ -254,23 +264,61 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
         for (int i = 0; i < NV; ++i)
             dst[i] = *(const u4 *)(Bb + ((size_t)cid[i] * ld + col0 + pcol[i]) * sizeof(VT));
     };
-    auto flush = [&](int task) {
-        const unsigned rw = uload(rows, task);
-        const bool split = (rw & 0x80000000u) != 0;
+    // Flush the accumulators of tasks first..last, which this wave ran back
+    // to back and which share one row-block.  A split row-block (bit 31)
+    // needs atomics unless this wave ran every task of it.
+    auto flush = [&](int first, int last) {
+        const unsigned rw = uload(rows, last);
         const int row0 = (int)(rw & 0x7fffffffu);
+        bool split = (rw & 0x80000000u) != 0;
+        if (split) {
+            const bool from_start = first == 0 || (int)(uload(rows, first - 1) & 0x7fffffffu) != row0;
+            const bool to_end = last + 1 >= ntasks || (int)(uload(rows, last + 1) & 0x7fffffffu) != row0;
+            split = !(from_start && to_end);
+        }
+        if (!split) {
+            // MFMA column n of block c is output column n*CB + c: the lane
+            // owns CB adjacent columns of each of its rows (one vector store)
 #pragma unroll
-        for (int g = 0; g < RG; ++g) {
-            if (BM == 8 && lq >= 2) break;
+            for (int g = 0; g < RG; ++g) {
+                if (BM == 8 && lq >= 2) break;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int r = row0 + 16 * g + 4 * lq + j;
-                if (r >= c_rows) continue;
-                float *crow = C + (size_t)r * ld + col0 + ln;
+                for (int j = 0; j < 4; ++j) {
+                    const int r = row0 + 16 * g + 4 * lq + j;
+                    if (r >= c_rows) continue;
+                    FV v;
 #pragma unroll
-                for (int c = 0; c < CB; ++c) {
-                    if (split) unsafeAtomicAdd(crow + 16 * c, acc[g][c][j]);
-                    else __builtin_nontemporal_store(acc[g][c][j], crow + 16 * c);
+                    for (int c = 0; c < CB; ++c) v[c] = acc[g][c][j];
+                    __builtin_nontemporal_store(v, (FV *)(C + (size_t)r * ld + col0 + ln * CB));
                 }
+            }
+        } else {
+            // fp32 atomics are issued per lane: transpose each 8-row slab
+            // through the wave's (now idle) B panel in LDS so that every
+            // atomic instruction covers whole rows of consecutive columns
+            static_assert(BN * LDSW * sizeof(VT) >= 8 * W * sizeof(float), "panel too small for a slab");
+            float *tr = (float *)lds;
+#pragma unroll
+            for (int h = 0; h < BM / 8; ++h) {
+                if ((lq >> 1) == (h & 1)) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        FV v;
+#pragma unroll
+                        for (int c = 0; c < CB; ++c) v[c] = acc[h >> 1][c][j];
+                        *(FV *)(tr + (4 * (lq & 1) + j) * W + ln * CB) = v;
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int i = 0; i < 8 * W / 64; ++i) {
+                    const int idx = lane + 64 * i;
+                    const int rr = idx / W, col = idx % W;
+                    const int r = row0 + 8 * h + rr;
+                    const float x = tr[rr * W + col];
+                    if (r < c_rows) unsafeAtomicAdd(C + (size_t)r * ld + col0 + col, x);
+                }
+                __builtin_amdgcn_wave_barrier();
             }
         }
 #pragma unroll
@@ -278,41 +326,48 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
 #pragma unroll
             for (int c = 0; c < CB; ++c) acc[g][c] = f4{0.f, 0.f, 0.f, 0.f};
     };
+    // B operand of MFMA block c at lane (n = ln, group lq): column n*CB + c
+    // of the chunk, so one LDS read of CB adjacent values per B row serves
+    // all CB blocks.
     auto compute = [&](const uint32_t (&a)[RG][AW]) {
+        const VT *lb = lds + ln * CB;
+        if constexpr (F16) {
+            constexpr int KR = BN == 16 ? 4 : 8;     // B rows of one lane
+            RV rv[KR];
 #pragma unroll
-        for (int c = 0; c < CB; ++c) {
-            const int col = 16 * c + ln;
-            if constexpr (F16) {
+            for (int j = 0; j < 4; ++j) rv[j] = *(const RV *)(lb + (4 * lq + j) * LDSW);
+            if constexpr (BN == 32) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) rv[4 + j] = *(const RV *)(lb + (16 + 4 * lq + j) * LDSW);
+            }
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
                 if constexpr (BN == 16) {
-                    h4 b;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) b[j] = lds[(4 * lq + j) * LDSW + col];
+                    const h4 b = h4{rv[0][c], rv[1][c], rv[2][c], rv[3][c]};
 #pragma unroll
                     for (int g = 0; g < RG; ++g) {
                         const h4 av = __builtin_bit_cast(h4, u2{a[g][0], a[g][1]});
                         acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, b, acc[g][c], 0, 0, 0);
                     }
                 } else {
-                    h8 b;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) b[j] = lds[(4 * lq + j) * LDSW + col];
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) b[4 + j] = lds[(16 + 4 * lq + j) * LDSW + col];
+                    const h8 b = h8{rv[0][c], rv[1][c], rv[2][c], rv[3][c], rv[4][c], rv[5][c], rv[6][c], rv[7][c]};
 #pragma unroll
                     for (int g = 0; g < RG; ++g) {
                         const h8 av = __builtin_bit_cast(h8, u4{a[g][0], a[g][1], a[g][2], a[g][3]});
                         acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[g][c], 0, 0, 0);
                     }
                 }
-            } else {
+            }
+        } else {
 #pragma unroll
-                for (int s = 0; s < KS; ++s) {
-                    const float b = lds[(KS * lq + s) * LDSW + col];
+            for (int s = 0; s < KS; ++s) {
+                const RV rv = *(const RV *)(lb + (KS * lq + s) * LDSW);
+#pragma unroll
+                for (int c = 0; c < CB; ++c)
 #pragma unroll
                     for (int g = 0; g < RG; ++g)
-                        acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[g][s]), b,
+                        acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[g][s]), rv[c],
                                                                           acc[g][c], 0, 0, 0);
-                }
             }
         }
     };
@@ -334,21 +389,28 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
         }
     };
 
-    // Prologue: B panels and A fragments of the first S tiles in flight, the
-    // column indices of tile tb+S in SGPRs.
+    // Prologue: B panels and A fragments of the first S tiles in flight, and
+    // a ring of S column-index sets in SGPRs: slot s holds the indices of
+    // tile t+S when tile t = s (mod S) is computed, so each scalar load has S
+    // tile periods to arrive before its B addresses are formed (the indices
+    // stream from HBM; one period is not enough to hide that latency).
     u4 bv[S][NV];
     uint32_t ar[S][RG][AW];
-    CSV cs;
+    CSV cs[S];
     int cid[NV];
 #pragma unroll
     for (int s = 0; s < S; ++s)
+        if (tb + s < te) load_cs(tb + s, cs[s]);
+#pragma unroll
+    for (int s = 0; s < S; ++s)
         if (tb + s < te) {
-            load_cs(tb + s, cs);
-            select_cid(cs, cid);
+            select_cid(cs[s], cid);
             load_b(cid, bv[s]);
             load_a(tb + s, ar[s]);
         }
-    if (tb + S < te) load_cs(tb + S, cs);
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+        if (tb + S + s < te) load_cs(tb + S + s, cs[s]);
 
     for (int t0 = tb; t0 < te; t0 += S) {
 #pragma unroll
@@ -356,9 +418,17 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
             const int t = t0 + s;
             if (t < te) {
                 if (t >= kend) {                 // task k is complete
-                    flush(k);
-                    do kend = uload(colstart, ++k + 1);
+                    int kn = k;
+                    do kend = uload(colstart, ++kn + 1);
                     while (kend <= t);           // skip empty tasks
+                    // the next task continues the same row-block: keep
+                    // accumulating instead of flushing partial sums
+                    const bool same = (uload(rows, kn) & 0x7fffffffu) == (uload(rows, k) & 0x7fffffffu);
+                    if (!same) {
+                        flush(gfirst, k);
+                        gfirst = kn;
+                    }
+                    k = kn;
                 }
                 stage_b(bv[s]);
                 uint32_t acur[RG][AW];
@@ -367,16 +437,16 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
 #pragma unroll
                     for (int w = 0; w < AW; ++w) acur[g][w] = ar[s][g][w];
                 if (t + S < te) {
-                    select_cid(cs, cid);
+                    select_cid(cs[s], cid);
                     load_b(cid, bv[s]);
                     load_a(t + S, ar[s]);
-                    if (t + S + 1 < te) load_cs(t + S + 1, cs);
+                    if (t + 2 * S < te) load_cs(t + 2 * S, cs[s]);
                 }
                 compute(acur);
             }
         }
     }
-    flush(k);
+    flush(gfirst, k);
 }
 
 __global__ __launch_bounds__(256) void copy_kernel(u4 *__restrict__ dst, const u4 *__restrict__ src, size_t n)
@@ -390,11 +460,11 @@ __global__ __launch_bounds__(256) void copy_kernel(u4 *__restrict__ dst, const u
 // Dispatch.
 // ---------------------------------------------------------------------------
 // Defaults from the MI355X variant sweep (bench.py --sweep over configs 1-5):
-// one task per wave always won (the hardware dispatcher then balances tasks
-// and the resident waves cover a narrow window of rows, which keeps C writes
-// and shared B rows local); 8-row tiles prefer 64-column chunks with a single
-// prefetch stage (higher occupancy), 16-row tiles 128-column chunks with
-// three stages.
+// one task per wave (the plan's runtime tuning tries four where row-blocks
+// are split), 64-column chunks for 8- and 64-row tiles, 128-column chunks for
+// 16-row tiles at widths that are multiples of 128, and one prefetch stage:
+// with the column indices prefetched S tiles ahead, more stages cost
+// occupancy for no gain.
 int default_chunk_width(int bm, int colB_p)
 {
     if (colB_p == 32) return 32;
@@ -404,9 +474,10 @@ int default_chunk_width(int bm, int colB_p)
 
 int default_stages(int bm, int prec, int w)
 {
+    (void)bm;
     (void)prec;
     (void)w;
-    return bm == 16 ? 3 : 1;
+    return 1;
 }
 
 bool valid_variant(int bm, int w, int s)

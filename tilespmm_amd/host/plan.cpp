@@ -7,10 +7,11 @@
 // the current schedule in device memory, a host-side cache of schedules by
 // threshold (the reference caches four, src/csr2tile.h:657-711), and one
 // stream.  The three classes write disjoint rows of C and run concurrently;
-// every join point is an event on the null stream, which orders after all
-// three (blocking) class streams, as the reference's legacy-stream events do.
+// a run forks from and joins on the plan's main stream through events (the
+// reference orders its class streams with legacy null-stream events).
 #include <string.h>
 
+#include <algorithm>
 #include <chrono>
 #include <map>
 #include <memory>
@@ -567,24 +568,41 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
         // class, so both are timed.
         for (int i = 0; i < 3; ++i) {
             ClassDev &c = p->cls[i];
-            if (!c.active() || c.ntasks == 0 || c.var_w || c.var_order) continue;
+            if (!c.active() || c.ntasks == 0 || c.var_w || c.var_order || c.var_tpw) continue;
             tsp_kernel_info k;
             TSP_TRY(tsp_kernel_probe(c.bm, p->prec, p->colB_p, &k));
             const bool chunks = p->colB_p / k.cols_per_task >= 2;
-            double best_ms = 1e30;
-            int best_fmt = 1, best_order = 0;
-            for (int fmt = 1; fmt <= (c.pack_ok ? 2 : 1); ++fmt) {
-                TSP_TRY(tsp_plan_set_format(p, c.bm, fmt));
-                for (int o = chunks ? 1 : 0; o <= (chunks ? 2 : 0); ++o) {
-                    c.var_order = o;
+            // Tasks per wave: one, or four consecutive tasks streamed by one
+            // wave (consecutive tasks of a split row-block then merge into
+            // one flush instead of several atomic ones); worth timing only
+            // when the schedule has split tasks.
+            bool any_split = false;
+            for (int i2 = 0; i2 < c.ntasks && !any_split; ++i2)
+                any_split = (c.m->blkcoostylerowidx[i2] & 0x80000000u) != 0;
+            struct Opt { int fmt, order, tpw; };
+            std::vector<Opt> cand;
+            for (int fmt = 1; fmt <= (c.pack_ok ? 2 : 1); ++fmt)
+                for (int o = chunks ? 1 : 0; o <= (chunks ? 2 : 0); ++o)
+                    for (int tpw = 1; tpw <= (any_split ? 4 : 1); tpw += 3) cand.push_back({fmt, o, tpw});
+            // two interleaved rounds, best of each option: a drift of the
+            // clock between options cannot decide the pick
+            std::vector<double> best_of(cand.size(), 1e30);
+            for (int round = 0; round < (cand.size() > 1 ? 2 : 0); ++round)
+                for (size_t j = 0; j < cand.size(); ++j) {
+                    TSP_TRY(tsp_plan_set_format(p, c.bm, cand[j].fmt));
+                    c.var_order = cand[j].order;
+                    c.var_tpw = cand[j].tpw;
                     double warm = 0, ms = 0;
                     TSP_TRY(tsp_plan_time_class(p, c.bm, 3, &warm));
                     TSP_TRY(tsp_plan_time_class(p, c.bm, 10, &ms));
-                    if (ms < best_ms) { best_ms = ms; best_fmt = fmt; best_order = o; }
+                    best_of[j] = std::min(best_of[j], ms);
                 }
-            }
-            TSP_TRY(tsp_plan_set_format(p, c.bm, best_fmt));
-            c.var_order = best_order;
+            size_t pick = 0;
+            for (size_t j = 1; j < cand.size(); ++j)
+                if (best_of[j] < best_of[pick]) pick = j;
+            TSP_TRY(tsp_plan_set_format(p, c.bm, cand[pick].fmt));
+            c.var_order = cand[pick].order;
+            c.var_tpw = cand[pick].tpw == 1 ? 0 : cand[pick].tpw;
         }
         t3 = now_ms();
     }
