@@ -136,6 +136,8 @@ def main():
                     help="pin the A format per class 64,16,8 (1 dense, 2 packed, 0 keep)")
     ap.add_argument("--order", type=ints3, default=None,
                     help="pin the chunk order per class 64,16,8 (1 side by side, 2 chunk-major, 0 keep)")
+    ap.add_argument("--tpw", type=ints3, default=None,
+                    help="pin the tasks per wave per class 64,16,8 (0 keep)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-vendor", action="store_true")
     ap.add_argument("--class-reps", type=int, default=200)
@@ -195,6 +197,10 @@ def main():
         if o:
             w, st, tpw, _ = plan.get_variant(bm)
             plan.set_variant(bm, w, st, tpw, o)
+    for bm, n in zip((64, 16, 8), args.tpw or ()):
+        if n:
+            w, st, _, o = plan.get_variant(bm)
+            plan.set_variant(bm, w, st, n, o)
     log(f"thresholds {th} (model {model_ms:.1f} ms, tuning {tune_ms:.1f} ms)")
 
     if args.sweep:
@@ -221,6 +227,7 @@ def main():
         cls[bm] = {"ms": cms, "rows": sb.rows, "nnz": int(sb.nnz), "tiles": t.tilenum,
                    "format": {1: "dense", 2: "packed"}.get(plan.get_format(bm), "?"),
                    "order": {0: "side-by-side", 1: "side-by-side", 2: "chunk-major"}[plan.get_variant(bm)[3]],
+                   "tasks_per_wave": max(1, plan.get_variant(bm)[2]),
                    "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9}
     dom = max(cls, key=lambda k: cls[k]["ms"])
     k_all = int(np.unique(A.colidx).size)

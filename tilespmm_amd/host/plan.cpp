@@ -600,6 +600,10 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
             size_t pick = 0;
             for (size_t j = 1; j < cand.size(); ++j)
                 if (best_of[j] < best_of[pick]) pick = j;
+            if (getenv("TSP_TUNE_LOG"))
+                for (size_t j = 0; j < cand.size(); ++j)
+                    fprintf(stderr, "tune bm=%d th=%d format=%d order=%d tasks/wave=%d: %.5f ms%s\n", c.bm, c.th,
+                            cand[j].fmt, cand[j].order, cand[j].tpw, best_of[j], j == pick ? "  <- kept" : "");
             TSP_TRY(tsp_plan_set_format(p, c.bm, cand[pick].fmt));
             c.var_order = cand[pick].order;
             c.var_tpw = cand[pick].tpw == 1 ? 0 : cand[pick].tpw;
