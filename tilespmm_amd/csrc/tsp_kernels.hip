@@ -113,6 +113,11 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     constexpr int AW = F16 ? (BN == 32 ? 4 : 2) : KS;   // A words per row group
     using VT = typename std::conditional<F16, _Float16, float>::type;
     using RV = VT __attribute__((ext_vector_type(CB)));     // CB values of one B row
+    constexpr int PWD = PK ? BM * BN / 64 : 1;               // packed: bitmap words per tile
+    struct PMeta {
+        uint64_t bw[PWD];
+        int vbase;
+    };
     using FV = float __attribute__((ext_vector_type(CB)));  // CB output columns
 
     __shared__ __attribute__((aligned(32))) VT lds_all[kWavesPerBlock][BN * LDSW];
@@ -158,14 +163,22 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
 #pragma unroll
         for (int c = 0; c < CB; ++c) acc[g][c] = f4{0.f, 0.f, 0.f, 0.f};
 
-    auto load_a_packed = [&](int t, uint32_t (&dst)[RG][AW]) {
-        static_assert(!PK || BM <= 16, "packed tiles are 8- or 16-row");
-        constexpr int WD = BM * BN / 64;         // bitmap words per tile
-        constexpr int NVAL = F16 ? 4 : KS;       // operand values per lane
-        uint64_t bw[WD];
+    // Packed-format metadata of one tile (bitmap words, value offset): wave-
+    // uniform scalar loads, prefetched S tiles ahead like the column indices
+    // because the value addresses depend on them.
+    auto load_meta = [&](int t, PMeta &m) {
+        if constexpr (PK) {
 #pragma unroll
-        for (int w = 0; w < WD; ++w) bw[w] = uload(bmp, (size_t)t * WD + w);
-        const int vbase = uload(vptr, t);
+            for (int w = 0; w < PWD; ++w) m.bw[w] = uload(bmp, (size_t)t * PWD + w);
+            m.vbase = uload(vptr, t);
+        }
+    };
+    auto load_a_packed = [&](const PMeta &m, uint32_t (&dst)[RG][AW]) {
+        static_assert(!PK || BM <= 16, "packed tiles are 8- or 16-row");
+        constexpr int WD = PWD;                  // bitmap words per tile
+        constexpr int NVAL = F16 ? 4 : KS;       // operand values per lane
+        const uint64_t *bw = m.bw;
+        const int vbase = m.vbase;
         if (BM == 8 && ln >= 8) {
 #pragma unroll
             for (int w = 0; w < AW; ++w) dst[0][w] = 0u;
@@ -209,9 +222,9 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
             for (int j = 0; j < NVAL; ++j) dst[0][j] = round_tf32_bits(__float_as_uint(o[j]));
         }
     };
-    auto load_a = [&](int t, uint32_t (&dst)[RG][AW]) {
+    auto load_a = [&](int t, const PMeta &m, uint32_t (&dst)[RG][AW]) {
         if constexpr (PK) {
-            load_a_packed(t, dst);
+            load_a_packed(m, dst);
             return;
         }
         const VT *tile = val + (size_t)t * (BM * BN);
@@ -397,20 +410,27 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     u4 bv[S][NV];
     uint32_t ar[S][RG][AW];
     CSV cs[S];
+    PMeta pm[S];
     int cid[NV];
 #pragma unroll
     for (int s = 0; s < S; ++s)
-        if (tb + s < te) load_cs(tb + s, cs[s]);
+        if (tb + s < te) {
+            load_cs(tb + s, cs[s]);
+            load_meta(tb + s, pm[s]);
+        }
 #pragma unroll
     for (int s = 0; s < S; ++s)
         if (tb + s < te) {
             select_cid(cs[s], cid);
             load_b(cid, bv[s]);
-            load_a(tb + s, ar[s]);
+            load_a(tb + s, pm[s], ar[s]);
         }
 #pragma unroll
     for (int s = 0; s < S; ++s)
-        if (tb + S + s < te) load_cs(tb + S + s, cs[s]);
+        if (tb + S + s < te) {
+            load_cs(tb + S + s, cs[s]);
+            load_meta(tb + S + s, pm[s]);
+        }
 
     for (int t0 = tb; t0 < te; t0 += S) {
 #pragma unroll
@@ -439,8 +459,11 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
                 if (t + S < te) {
                     select_cid(cs[s], cid);
                     load_b(cid, bv[s]);
-                    load_a(t + S, ar[s]);
-                    if (t + 2 * S < te) load_cs(t + 2 * S, cs[s]);
+                    load_a(t + S, pm[s], ar[s]);
+                    if (t + 2 * S < te) {
+                        load_cs(t + 2 * S, cs[s]);
+                        load_meta(t + 2 * S, pm[s]);
+                    }
                 }
                 compute(acur);
             }
