@@ -138,6 +138,8 @@ def main():
                     help="pin the chunk order per class 64,16,8 (1 side by side, 2 chunk-major, 0 keep)")
     ap.add_argument("--tpw", type=ints3, default=None,
                     help="pin the tasks per wave per class 64,16,8 (0 keep)")
+    ap.add_argument("--place", type=ints3, default=None,
+                    help="pin the XCD placement per class 64,16,8 (1 contiguous, 2 interleaved, 0 keep)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-vendor", action="store_true")
     ap.add_argument("--class-reps", type=int, default=200)
@@ -201,6 +203,9 @@ def main():
         if n:
             w, st, _, o = plan.get_variant(bm)
             plan.set_variant(bm, w, st, n, o)
+    for bm, pl in zip((64, 16, 8), args.place or ()):
+        if pl:
+            plan.set_placement(bm, pl - 1)
     log(f"thresholds {th} (model {model_ms:.1f} ms, tuning {tune_ms:.1f} ms)")
 
     if args.sweep:
@@ -228,6 +233,7 @@ def main():
                    "format": {1: "dense", 2: "packed"}.get(plan.get_format(bm), "?"),
                    "order": {0: "side-by-side", 1: "side-by-side", 2: "chunk-major"}[plan.get_variant(bm)[3]],
                    "tasks_per_wave": max(1, plan.get_variant(bm)[2]),
+                   "placement": {0: "contiguous", 1: "interleaved"}.get(plan.get_placement(bm), "?"),
                    "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9}
     dom = max(cls, key=lambda k: cls[k]["ms"])
     k_all = int(np.unique(A.colidx).size)

@@ -200,6 +200,11 @@ int tsp_plan_get_format(tsp_plan *plan, int bm);
 /* The variant a class is pinned to (0 = library default), e.g. after
  * tsp_plan_tune picked the chunk order. */
 int tsp_plan_get_variant(tsp_plan *plan, int bm, int *w, int *stages, int *tasks_per_wave, int *order);
+/* Workgroup placement of one class on the XCDs (TSP_PLACE_CONTIGUOUS or
+ * TSP_PLACE_INTERLEAVED, see tsp_spmm_launch_placed); tsp_plan_tune times
+ * both.  get returns -1 on a bad argument. */
+int tsp_plan_set_placement(tsp_plan *plan, int bm, int placement);
+int tsp_plan_get_placement(tsp_plan *plan, int bm);
 /* Launch the three classes once (each on its own stream, joined on the null
  * stream).  zero_c != 0 clears C first. */
 int tsp_plan_run(tsp_plan *plan, int zero_c);

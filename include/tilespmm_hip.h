@@ -143,6 +143,25 @@ int tsp_spmm_launch_packed(int bm, int prec, int rowblkblock, int colB_p, const 
                            const int *d_colidx, int c_rows, void *stream, int w, int stages,
                            int tasks_per_wave, int order);
 
+/* Workgroup placement on the XCDs.  Each of the 8 XCDs of an MI355X has its
+ * own L2 and receives every 8th workgroup of a launch.  The launches above
+ * use TSP_PLACE_CONTIGUOUS: each XCD runs one contiguous eighth of the task
+ * ranges, so neighbouring row-blocks, which share B rows, share an L2.
+ * TSP_PLACE_INTERLEAVED deals runs of 4 workgroups to the XCDs in turn,
+ * which keeps matrices whose heavy rows sit together (graphs with hub
+ * vertices at one end) balanced across the XCDs.  tsp_spmm_launch_placed
+ * takes the placement with the variant arguments of tsp_spmm_launch_variant
+ * (d_bitmap NULL: dense A tiles in d_val; else the packed format of
+ * tsp_spmm_launch_packed, with d_val the packed values).  No counterpart in
+ * the reference (NVIDIA GPUs have one L2). */
+#define TSP_PLACE_CONTIGUOUS 0
+#define TSP_PLACE_INTERLEAVED 1
+int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
+                           const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,
+                           const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,
+                           int c_rows, void *stream, int w, int stages, int tasks_per_wave, int order,
+                           int placement);
+
 /* Per-class entry points with the reference dispatcher names
  * (src/tilespmm_cuda.h:1634, :1672, :1710) and argument order. */
 int tsp_switch_v64(int prec, int rowblkblock, int colB_p, const void *d_val,

@@ -66,6 +66,15 @@ def test_error_strings_and_arg_checks(tsp):
     assert hip.tsp_spmm_launch(16, 2, 1, 128, None, None, None, None, None, None, 0, None) == 1001
     assert hip.tsp_spmm_launch(16, 0, 1, 128, None, None, None, None, None, None, 0, None) == 1001
     assert hip.tsp_spmm_launch(16, 0, 0, 128, None, None, None, None, None, None, 0, None) == 0
+    # XCD placement: only contiguous (0) and interleaved (1); packed needs
+    # the value offsets and is 8-/16-row only
+    placed = lambda bm, bmp, vptr, place: hip.tsp_spmm_launch_placed(
+        bm, 0, 1, 128, None, bmp, vptr, None, None, None, None, None, 0, None, 0, 0, 0, 0, place)
+    for place in (-1, 2, 7):
+        assert placed(16, None, None, place) == 1001
+    assert placed(16, None, None, 0) == 1001 and placed(16, None, None, 1) == 1001   # null buffers
+    dummy = C.c_void_p(1)
+    assert placed(64, dummy, dummy, 0) == 1001 and placed(8, dummy, None, 0) == 1001
 
 
 def test_cli_usage_and_errors(tmp_path):

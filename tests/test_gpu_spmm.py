@@ -115,7 +115,8 @@ def test_random_all_classes(gpu, orc, prec, colB):
 @pytest.mark.parametrize("prec", [0, 1])
 def test_every_kernel_variant(gpu, orc, prec):
     """Every (chunk width, pipeline depth, tasks per wave) variant of every
-    class gives the oracle's result, split tasks included."""
+    class, with both XCD placements, gives the oracle's result, split tasks
+    included."""
     tsp = gpu
     rng = np.random.default_rng(50 + prec)
     A = random_matrix(tsp, rng, 611, 509, 45, prec, heavy_rows=4)
@@ -134,12 +135,16 @@ def test_every_kernel_variant(gpu, orc, prec):
                 for w in ((32, 64) if bm == 64 else (32, 64, 128)):
                     for s in (1, 2, 3, 4):
                         for tpw, order in ((1, 1), (3, 2), (0, 0)):
-                            tag = f"prec={prec} bm={bm} fmt={fmt} w={w} s={s} tpw={tpw} order={order}"
-                            say("variant " + tag)
-                            plan.set_variant(bm, w, s, tpw, order)
-                            plan.run(zero_c=True)
-                            Cg = plan.download_c()
-                            assert_close(Cg[:, :colB], Cref, Cabs, prec, tag)
+                            for place in (0, 1):
+                                tag = (f"prec={prec} bm={bm} fmt={fmt} w={w} s={s} tpw={tpw} order={order} "
+                                       f"place={place}")
+                                say("variant " + tag)
+                                plan.set_variant(bm, w, s, tpw, order)
+                                plan.set_placement(bm, place)
+                                assert plan.get_placement(bm) == place
+                                plan.run(zero_c=True)
+                                Cg = plan.download_c()
+                                assert_close(Cg[:, :colB], Cref, Cabs, prec, tag)
         finally:
             plan.close()
 
@@ -190,7 +195,8 @@ def test_cli_end_to_end(gpu, dc2_path, tmp_path, exe, colB, tiling):
 
 
 def test_direct_kernel_boundary(gpu, orc):
-    """tsp_switch_v16 called directly on device buffers (the kernel ABI)."""
+    """tsp_switch_v16 called directly on device buffers (the kernel ABI), and
+    tsp_spmm_launch_placed with both XCD placements on the same buffers."""
     tsp = gpu
     hip, _ = tsp.load()
     rng = np.random.default_rng(2)
@@ -216,17 +222,30 @@ def test_direct_kernel_boundary(gpu, orc):
         up("val", arr["dense"]); up("col", arr["tile_colidx"]); up("rows", rows); up("cs", cs); up("B", B)
         Cz = np.zeros((A.rows, cbp), dtype=np.float32)
         up("C", Cz)
-        st = hip.tsp_switch_v16(0, len(rows), cbp, bufs["val"], bufs["rows"], bufs["cs"], bufs["B"], bufs["C"],
-                                bufs["col"], A.rows, None)
-        assert st == 0
-        assert hip.tsp_device_sync() == 0
-        out = np.zeros_like(Cz)
-        assert hip.tsp_memcpy_d2h(out.ctypes.data_as(C.c_void_p), bufs["C"], out.nbytes) == 0
+        outs = []
+        for place in (None, 0, 1):
+            assert hip.tsp_memcpy_h2d(bufs["C"], Cz.ctypes.data_as(C.c_void_p), Cz.nbytes) == 0
+            if place is None:
+                st = hip.tsp_switch_v16(0, len(rows), cbp, bufs["val"], bufs["rows"], bufs["cs"], bufs["B"],
+                                        bufs["C"], bufs["col"], A.rows, None)
+            else:
+                st = hip.tsp_spmm_launch_placed(16, 0, len(rows), cbp, bufs["val"], None, None, bufs["rows"],
+                                                bufs["cs"], bufs["B"], bufs["C"], bufs["col"], A.rows, None,
+                                                0, 0, 0, 0, place)
+            assert st == 0
+            assert hip.tsp_device_sync() == 0
+            out = np.zeros_like(Cz)
+            assert hip.tsp_memcpy_d2h(out.ctypes.data_as(C.c_void_p), bufs["C"], out.nbytes) == 0
+            outs.append(out)
+        # an unknown placement is rejected before any launch
+        assert hip.tsp_spmm_launch_placed(16, 0, len(rows), cbp, bufs["val"], None, None, bufs["rows"], bufs["cs"],
+                                          bufs["B"], bufs["C"], bufs["col"], A.rows, None, 0, 0, 0, 0, 2) != 0
     finally:
         for p in bufs.values():
             hip.tsp_free(p)
     Cref, Cabs = reference(orc, A, B, colB)
-    assert_close(out[:, :colB], Cref, Cabs, 0, "direct v16")
+    for place, out in zip(("switch", "contiguous", "interleaved"), outs):
+        assert_close(out[:, :colB], Cref, Cabs, 0, f"direct v16 {place}")
 
 
 def test_edge_shapes(gpu, orc):

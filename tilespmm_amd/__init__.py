@@ -160,6 +160,8 @@ HIP_SYMBOLS = {
                                           C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int]),
     "tsp_spmm_launch_packed": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P,
                                          C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "tsp_spmm_launch_placed": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P,
+                                         C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "tsp_switch_v64": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v16": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v8": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
@@ -215,6 +217,8 @@ HOST_SYMBOLS = {
     "tsp_plan_set_format": (C.c_int, [_P, C.c_int, C.c_int]),
     "tsp_plan_get_format": (C.c_int, [_P, C.c_int]),
     "tsp_plan_get_variant": (C.c_int, [_P, C.c_int, _IP, _IP, _IP, _IP]),
+    "tsp_plan_set_placement": (C.c_int, [_P, C.c_int, C.c_int]),
+    "tsp_plan_get_placement": (C.c_int, [_P, C.c_int]),
     "tsp_plan_run": (C.c_int, [_P, C.c_int]),
     "tsp_plan_warmup": (C.c_int, [_P, C.c_int]),
     "tsp_plan_time": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double)]),
@@ -621,6 +625,13 @@ class Plan:
         v = [C.c_int() for _ in range(4)]
         _check("tsp_plan_get_variant", load()[1].tsp_plan_get_variant(self.p, bm, *[C.byref(x) for x in v]))
         return tuple(x.value for x in v)
+
+    def set_placement(self, bm: int, placement: int):
+        """XCD placement: 0 = contiguous eighths, 1 = runs dealt round-robin."""
+        _check("tsp_plan_set_placement", load()[1].tsp_plan_set_placement(self.p, bm, placement))
+
+    def get_placement(self, bm: int) -> int:
+        return load()[1].tsp_plan_get_placement(self.p, bm)
 
     def run(self, zero_c: bool = True):
         _check("tsp_plan_run", load()[1].tsp_plan_run(self.p, int(zero_c)))

@@ -16,6 +16,18 @@ constexpr __host__ __device__ int tile_bn(int bm, int prec)
     return prec == 0 ? (bm == 64 ? 32 : 16) : (bm == 64 ? 16 : 8);
 }
 
+// Placement of a launch's workgroups on the XCDs.  The hardware deals
+// workgroups to the XCDs round-robin (workgroup b -> XCD b % kXcds), and each
+// XCD has its own L2.  kPlaceContiguous gives each XCD one contiguous eighth
+// of the logical blocks (neighbouring task ranges, which share B rows, share
+// an L2); kPlaceInterleaved deals runs of kXcdRun consecutive logical blocks
+// to the XCDs in turn, which keeps skewed matrices (hub rows at one end)
+// balanced across the XCDs.
+constexpr int kXcds = 8;
+constexpr int kXcdRun = 4;
+constexpr int kPlaceContiguous = 0;
+constexpr int kPlaceInterleaved = 1;
+
 // Kernel variant = (chunk width W, pipeline stages S, tasks per wave).
 int default_chunk_width(int bm, int colB_p);
 int default_stages(int bm, int prec, int w);
@@ -28,7 +40,8 @@ int default_chunk_major(int bm, int prec, int colB_p, int w);
 // bitmap-packed A format (val = packed values, vptr = per-tile offsets).
 int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint64_t *bmp,
            const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
-           const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order);
+           const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order,
+           int placement = kPlaceContiguous);
 int launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
 constexpr int kGatherBlocks = 8192;      // gather probe grid: 8192 x 256 threads
 int launch_gather(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed, void *sink,

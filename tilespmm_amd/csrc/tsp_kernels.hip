@@ -34,8 +34,10 @@
 //     registers and multiplied with v_mfma_f32_16x16x4_f32 -- a tf32 product
 //     is exact in fp32, so this is tf32 arithmetic with fp32 accumulate
 //     (CDNA4 has no xf32 MFMA);
-//   * block ids are remapped so that consecutive task ranges (which tend to
-//     share B rows) run on the same XCD and share its L2.
+//   * workgroups are placed on the 8 XCDs (each with its own L2) either as
+//     8 contiguous ranges of task ranges (neighbouring row-blocks share B
+//     rows) or as runs of 4 workgroups dealt to the XCDs in turn (skewed
+//     matrices stay balanced); the plan's runtime tuning picks per class.
 //
 // The MFMA K index of (lane group q = lane/16, operand element j) is a free
 // permutation as long as A and B use the same one; this file uses
@@ -76,12 +78,14 @@ __device__ __forceinline__ T uload(const T *p, size_t i)
     return ((cptr<T>)p)[i];
 }
 
-// Block id -> logical block id such that each XCD (blocks are dealt to the 8
-// XCDs round-robin) receives one contiguous range of logical blocks.
-__device__ __forceinline__ int xcd_remap(int b, int nb)
+// Workgroup b of nb -> logical block.  Contiguous: each XCD receives one
+// contiguous range of logical blocks.  Interleaved: runs of kXcdRun logical
+// blocks go to the XCDs in turn (nb is then a multiple of kXcds * kXcdRun).
+__device__ __forceinline__ int place_block(int b, int nb, int placement)
 {
-    const int q = nb >> 3, r = nb & 7;
-    const int x = b & 7, k = b >> 3;
+    const int x = b % kXcds, k = b / kXcds;
+    if (placement == kPlaceInterleaved) return ((k / kXcdRun) * kXcds + x) * kXcdRun + k % kXcdRun;
+    const int q = nb / kXcds, r = nb % kXcds;
     return x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
 }
 
@@ -96,7 +100,7 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     const uint64_t *__restrict__ bmp, const int *__restrict__ vptr,
     const unsigned *__restrict__ rows, const int *__restrict__ colstart,
     const void *__restrict__ B_, float *__restrict__ C, const int *__restrict__ colidx, int ld,
-    int c_rows)
+    int c_rows, int placement)
 {
     constexpr bool F16 = PREC == TSP_PREC_FP16;
     constexpr int BN = tile_bn(BM, PREC);
@@ -124,7 +128,7 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
 
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform per wave
-    const int lb = xcd_remap(blockIdx.x, gridDim.x);
+    const int lb = place_block(blockIdx.x, gridDim.x, placement);
     const long long gw = (long long)lb * kWavesPerBlock + wid;
     const long long nranges = ((long long)ntasks + tasks_per_wave - 1) / tasks_per_wave;
     if (gw >= nranges * nchunks) return;
@@ -576,35 +580,52 @@ int default_chunk_major(int bm, int prec, int colB_p, int w)
     return 0;
 }
 
+// Resolves the variant defaults of a launch; false if the variant is invalid.
+static bool resolve_variant(int bm, int prec, int colB_p, int &w, int &s, int &nchunks, int ntasks, int &tpw,
+                            int order, int &cm)
+{
+    if (w <= 0) w = default_chunk_width(bm, colB_p);
+    if (colB_p % w != 0) return false;
+    if (s <= 0) s = default_stages(bm, prec, w);
+    if (!valid_variant(bm, w, s)) return false;
+    nchunks = colB_p / w;
+    if (tpw <= 0) tpw = default_tasks_per_wave(ntasks, nchunks);
+    cm = order > 0 ? (order == 2 ? 1 : 0) : default_chunk_major(bm, prec, colB_p, w);
+    return true;
+}
+
 int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint64_t *bmp,
            const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
-           const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order)
+           const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order,
+           int placement)
 {
     const bool packed = bmp != nullptr;
     if (packed && (bm == 64 || !vptr)) return TSP_EINVAL;
-    if (w <= 0) w = default_chunk_width(bm, colB_p);
-    if (colB_p % w != 0) return TSP_EINVAL;
-    if (s <= 0) s = default_stages(bm, prec, w);
-    if (!valid_variant(bm, w, s)) return TSP_EINVAL;
-    const int nchunks = colB_p / w;
-    if (tpw <= 0) tpw = default_tasks_per_wave(ntasks, nchunks);
-    const int cm = order > 0 ? (order == 2 ? 1 : 0) : default_chunk_major(bm, prec, colB_p, w);
+    if (placement != kPlaceContiguous && placement != kPlaceInterleaved) return TSP_EINVAL;
+    int nchunks = 0, cm = 0;
+    if (!resolve_variant(bm, prec, colB_p, w, s, nchunks, ntasks, tpw, order, cm)) return TSP_EINVAL;
     const long long ranges = ((long long)ntasks + tpw - 1) / tpw;
     const long long waves = ranges * nchunks;
-    const long long blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
+    long long blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
     if (blocks <= 0) return 0;
+    // interleaved: whole runs on every XCD (workgroups past the last
+    // logical block find no task range and exit)
+    if (placement == kPlaceInterleaved) {
+        const long long run = (long long)kXcds * kXcdRun;
+        blocks = (blocks + run - 1) / run * run;
+    }
     if (blocks > 0x7fffffffLL) return TSP_EINVAL;
-    const dim3 grid((unsigned)blocks);
+    const dim3 grid3((unsigned)blocks);
 #define TSP_L(BMv, Wv, Sv, PKv)                                                                 \
     if (packed == PKv && bm == BMv && w == Wv && s == Sv) {                                     \
         if (prec == TSP_PREC_FP16)                                                              \
-            spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, PKv><<<grid, kBlockThreads, 0, st>>>(        \
+            spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, PKv><<<grid3, kBlockThreads, 0, st>>>(       \
                 ntasks, nchunks, tpw, cm, val, bmp, vptr, rows, colstart, B, C, colidx, colB_p, \
-                c_rows);                                                                        \
+                c_rows, placement);                                                             \
         else                                                                                    \
-            spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, PKv><<<grid, kBlockThreads, 0, st>>>(        \
+            spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, PKv><<<grid3, kBlockThreads, 0, st>>>(       \
                 ntasks, nchunks, tpw, cm, val, bmp, vptr, rows, colstart, B, C, colidx, colB_p, \
-                c_rows);                                                                        \
+                c_rows, placement);                                                             \
         return (int)hipGetLastError();                                                          \
     }
 #define TSP_LD(BMv, Wv, Sv) TSP_L(BMv, Wv, Sv, false)

@@ -42,6 +42,7 @@ struct ClassDev {
     bool dev_built = false;       // tiles made on the device: `own` holds the host-side view
     Tile_matrix own{};            // tile_ptr, orig_tile_row_idx, schedule; no value arrays
     std::map<int, std::pair<std::vector<unsigned>, std::vector<int>>> cache;
+    int place = TSP_PLACE_CONTIGUOUS;   // workgroup placement on the XCDs
     bool active() const { return m && m->tilenum > 0; }
 };
 
@@ -179,16 +180,11 @@ static int upload_dense(tsp_plan *p, ClassDev &c)
 static int launch_class(tsp_plan *p, ClassDev &c)
 {
     if (!c.active() || c.ntasks == 0) return TSP_OK;
-    if (c.fmt == 2)
-        return tsp_spmm_launch_packed(c.bm, p->prec, c.ntasks, p->colB_p, c.d_pval, c.d_bmp, c.d_vptr,
-                                      c.d_rows, c.d_colstart, p->d_B, p->d_C, c.d_colidx, p->rowA,
-                                      c.stream, c.var_w, c.var_s, c.var_tpw, c.var_order);
-    if (c.var_w || c.var_s || c.var_tpw || c.var_order)
-        return tsp_spmm_launch_variant(c.bm, p->prec, c.ntasks, p->colB_p, c.d_val, c.d_rows,
-                                       c.d_colstart, p->d_B, p->d_C, c.d_colidx, p->rowA, c.stream,
-                                       c.var_w, c.var_s, c.var_tpw, c.var_order);
-    return tsp_spmm_launch(c.bm, p->prec, c.ntasks, p->colB_p, c.d_val, c.d_rows, c.d_colstart,
-                           p->d_B, p->d_C, c.d_colidx, p->rowA, c.stream);
+    const bool pk = c.fmt == 2;
+    return tsp_spmm_launch_placed(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val,
+                                  pk ? c.d_bmp : nullptr, pk ? c.d_vptr : nullptr, c.d_rows, c.d_colstart,
+                                  p->d_B, p->d_C, c.d_colidx, p->rowA, c.stream, c.var_w, c.var_s,
+                                  c.var_tpw, c.var_order, c.place);
 }
 
 extern "C" int tsp_plan_set_format(tsp_plan *p, int bm, int fmt)
@@ -229,6 +225,25 @@ extern "C" int tsp_plan_set_variant(tsp_plan *p, int bm, int w, int stages, int 
             return TSP_OK;
         }
     return TSP_EINVAL;
+}
+
+extern "C" int tsp_plan_set_placement(tsp_plan *p, int bm, int placement)
+{
+    if (!p || (placement != TSP_PLACE_CONTIGUOUS && placement != TSP_PLACE_INTERLEAVED)) return TSP_EINVAL;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) {
+            c.place = placement;
+            return TSP_OK;
+        }
+    return TSP_EINVAL;
+}
+
+extern "C" int tsp_plan_get_placement(tsp_plan *p, int bm)
+{
+    if (!p) return -1;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) return c.place;
+    return -1;
 }
 
 extern "C" int tsp_plan_get_variant(tsp_plan *p, int bm, int *w, int *stages, int *tasks_per_wave, int *order)
@@ -579,34 +594,55 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
             bool any_split = false;
             for (int i2 = 0; i2 < c.ntasks && !any_split; ++i2)
                 any_split = (c.m->blkcoostylerowidx[i2] & 0x80000000u) != 0;
-            struct Opt { int fmt, order, tpw; };
+            struct Opt { int fmt, order, tpw, place; };
             std::vector<Opt> cand;
             for (int fmt = 1; fmt <= (c.pack_ok ? 2 : 1); ++fmt)
                 for (int o = chunks ? 1 : 0; o <= (chunks ? 2 : 0); ++o)
-                    for (int tpw = 1; tpw <= (any_split ? 4 : 1); tpw += 3) cand.push_back({fmt, o, tpw});
+                    for (int tpw = 1; tpw <= (any_split ? 4 : 1); tpw += 3)
+                        cand.push_back({fmt, o, tpw, TSP_PLACE_CONTIGUOUS});
             // two interleaved rounds, best of each option: a drift of the
             // clock between options cannot decide the pick
-            std::vector<double> best_of(cand.size(), 1e30);
-            for (int round = 0; round < (cand.size() > 1 ? 2 : 0); ++round)
-                for (size_t j = 0; j < cand.size(); ++j) {
-                    TSP_TRY(tsp_plan_set_format(p, c.bm, cand[j].fmt));
-                    c.var_order = cand[j].order;
-                    c.var_tpw = cand[j].tpw;
-                    double warm = 0, ms = 0;
-                    TSP_TRY(tsp_plan_time_class(p, c.bm, 3, &warm));
-                    TSP_TRY(tsp_plan_time_class(p, c.bm, 10, &ms));
-                    best_of[j] = std::min(best_of[j], ms);
-                }
+            auto time_options = [&](const std::vector<Opt> &opts, std::vector<double> &best_of) -> int {
+                best_of.assign(opts.size(), 1e30);
+                for (int round = 0; round < (opts.size() > 1 ? 2 : 0); ++round)
+                    for (size_t j = 0; j < opts.size(); ++j) {
+                        TSP_TRY(tsp_plan_set_format(p, c.bm, opts[j].fmt));
+                        c.var_order = opts[j].order;
+                        c.var_tpw = opts[j].tpw;
+                        c.place = opts[j].place;
+                        double warm = 0, ms = 0;
+                        TSP_TRY(tsp_plan_time_class(p, c.bm, 3, &warm));
+                        TSP_TRY(tsp_plan_time_class(p, c.bm, 10, &ms));
+                        best_of[j] = std::min(best_of[j], ms);
+                    }
+                return TSP_OK;
+            };
+            std::vector<double> best_of;
+            TSP_TRY(time_options(cand, best_of));
             size_t pick = 0;
             for (size_t j = 1; j < cand.size(); ++j)
                 if (best_of[j] < best_of[pick]) pick = j;
-            if (getenv("TSP_TUNE_LOG"))
+            // XCD placement of the pick: contiguous eighths (neighbouring
+            // row-blocks share an L2) against runs dealt round-robin, which
+            // balances matrices whose heavy row-blocks sit together
+            std::vector<Opt> pl = {cand[pick], cand[pick]};
+            pl[1].place = TSP_PLACE_INTERLEAVED;
+            std::vector<double> pl_ms;
+            TSP_TRY(time_options(pl, pl_ms));
+            if (getenv("TSP_TUNE_LOG")) {
                 for (size_t j = 0; j < cand.size(); ++j)
                     fprintf(stderr, "tune bm=%d th=%d format=%d order=%d tasks/wave=%d: %.5f ms%s\n", c.bm, c.th,
                             cand[j].fmt, cand[j].order, cand[j].tpw, best_of[j], j == pick ? "  <- kept" : "");
-            TSP_TRY(tsp_plan_set_format(p, c.bm, cand[pick].fmt));
-            c.var_order = cand[pick].order;
-            c.var_tpw = cand[pick].tpw == 1 ? 0 : cand[pick].tpw;
+                for (int j = 0; j < 2; ++j)
+                    fprintf(stderr, "tune bm=%d placement=%s: %.5f ms%s\n", c.bm,
+                            j ? "interleaved" : "contiguous", pl_ms[j],
+                            (pl_ms[1] < pl_ms[0]) == (j == 1) ? "  <- kept" : "");
+            }
+            const Opt &o = pl[pl_ms[1] < pl_ms[0] ? 1 : 0];
+            TSP_TRY(tsp_plan_set_format(p, c.bm, o.fmt));
+            c.var_order = o.order;
+            c.var_tpw = o.tpw == 1 ? 0 : o.tpw;
+            c.place = o.place;
         }
         t3 = now_ms();
     }
