@@ -612,7 +612,10 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
                         c.place = opts[j].place;
                         double warm = 0, ms = 0;
                         TSP_TRY(tsp_plan_time_class(p, c.bm, 3, &warm));
-                        TSP_TRY(tsp_plan_time_class(p, c.bm, 10, &ms));
+                        // at least 10 launches and about 2 ms per timing, so
+                        // that short kernels are not decided by timer noise
+                        const int reps = (int)std::min(200.0, std::max(10.0, 2.0 / std::max(warm, 1e-4)));
+                        TSP_TRY(tsp_plan_time_class(p, c.bm, reps, &ms));
                         best_of[j] = std::min(best_of[j], ms);
                     }
                 return TSP_OK;
