@@ -95,6 +95,15 @@ def copy_calibration(hip, nbytes, reps):
     hip.tsp_free(dst)
 
 
+def default_width(hip, bm, prec, cbp):
+    """Output columns one wave covers when the plan keeps the library default."""
+    import ctypes as C
+    import tilespmm_amd as tsp
+    k = tsp.KernelInfo()
+    assert hip.tsp_kernel_probe(bm, prec, cbp, C.byref(k)) == 0
+    return k.cols_per_task
+
+
 def sweep(plan, tiles, cbp, args):
     """Time every kernel variant (chunk width W, pipeline stages S, tasks per
     wave) of each active class; one JSON line per class."""
@@ -138,6 +147,8 @@ def main():
                     help="pin the chunk order per class 64,16,8 (1 side by side, 2 chunk-major, 0 keep)")
     ap.add_argument("--tpw", type=ints3, default=None,
                     help="pin the tasks per wave per class 64,16,8 (0 keep)")
+    ap.add_argument("--width", type=ints3, default=None,
+                    help="pin the chunk width per class 64,16,8 (32, 64, 128; 0 keep)")
     ap.add_argument("--place", type=ints3, default=None,
                     help="pin the XCD placement per class 64,16,8 (1 contiguous, 2 interleaved, 0 keep)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -203,6 +214,10 @@ def main():
         if n:
             w, st, _, o = plan.get_variant(bm)
             plan.set_variant(bm, w, st, n, o)
+    for bm, wd in zip((64, 16, 8), args.width or ()):
+        if wd:
+            _, st, n, o = plan.get_variant(bm)
+            plan.set_variant(bm, wd, st, n, o)
     for bm, pl in zip((64, 16, 8), args.place or ()):
         if pl:
             plan.set_placement(bm, pl - 1)
@@ -233,6 +248,7 @@ def main():
                    "format": {1: "dense", 2: "packed"}.get(plan.get_format(bm), "?"),
                    "order": {0: "side-by-side", 1: "side-by-side", 2: "chunk-major"}[plan.get_variant(bm)[3]],
                    "tasks_per_wave": max(1, plan.get_variant(bm)[2]),
+                   "chunk_width": plan.get_variant(bm)[0] or default_width(hip, bm, prec, cbp),
                    "placement": {0: "contiguous", 1: "interleaved"}.get(plan.get_placement(bm), "?"),
                    "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9}
     dom = max(cls, key=lambda k: cls[k]["ms"])

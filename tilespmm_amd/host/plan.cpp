@@ -646,6 +646,24 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
             c.var_order = o.order;
             c.var_tpw = o.tpw == 1 ? 0 : o.tpw;
             c.place = o.place;
+            // 128-column chunks for the 8-row class: half the waves, each
+            // gathering 256-byte B row segments (fp16) instead of 128-byte ones
+            if (c.bm == 8 && k.cols_per_task != 128 && p->colB_p % 128 == 0) {
+                double ms[2] = {1e30, 1e30};
+                for (int round = 0; round < 2; ++round)
+                    for (int j = 0; j < 2; ++j) {
+                        c.var_w = j ? 128 : 0;
+                        double warm = 0, t = 0;
+                        TSP_TRY(tsp_plan_time_class(p, c.bm, 3, &warm));
+                        const int reps = (int)std::min(200.0, std::max(10.0, 2.0 / std::max(warm, 1e-4)));
+                        TSP_TRY(tsp_plan_time_class(p, c.bm, reps, &t));
+                        ms[j] = std::min(ms[j], t);
+                    }
+                c.var_w = ms[1] < ms[0] ? 128 : 0;
+                if (getenv("TSP_TUNE_LOG"))
+                    fprintf(stderr, "tune bm=%d chunk width default: %.5f ms, 128: %.5f ms%s\n", c.bm, ms[0], ms[1],
+                            c.var_w ? "  <- 128 kept" : "");
+            }
         }
         t3 = now_ms();
     }
