@@ -31,10 +31,8 @@ constexpr int kPlaceInterleaved = 1;
 // Kernel variant = (chunk width W, pipeline stages S, tasks per wave).
 int default_chunk_width(int bm, int colB_p);
 int default_stages(int bm, int prec, int w);
-int default_tasks_per_wave(int ntasks, int nchunks);
 bool valid_variant(int bm, int w, int s);
 const void *select_kernel(int bm, int prec, int w, int s, bool packed);
-int default_chunk_major(int bm, int prec, int colB_p, int w);
 // w, s, tpw <= 0 select the defaults; order 0 = default, 1 = chunks of one
 // task range adjacent, 2 = chunk-major.  bmp != nullptr selects the
 // bitmap-packed A format (val = packed values, vptr = per-tile offsets).

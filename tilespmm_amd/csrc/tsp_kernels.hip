@@ -487,11 +487,12 @@ __global__ __launch_bounds__(256) void copy_kernel(u4 *__restrict__ dst, const u
 // Dispatch.
 // ---------------------------------------------------------------------------
 // Defaults from the MI355X variant sweep (bench.py --sweep over configs 1-5):
-// one task per wave (the plan's runtime tuning tries four where row-blocks
-// are split), 64-column chunks for 8- and 64-row tiles, 128-column chunks for
-// 16-row tiles at widths that are multiples of 128, and one prefetch stage:
-// with the column indices prefetched S tiles ahead, more stages cost
-// occupancy for no gain.
+// 64-column chunks for 8- and 64-row tiles, 128-column chunks for 16-row
+// tiles at widths that are multiples of 128, one prefetch stage (with the
+// column indices prefetched S tiles ahead, more stages cost occupancy for no
+// gain), one task per wave and the chunks of a task range side by side.  The
+// plan's runtime tuning revisits the order, the tasks per wave, the XCD
+// placement and (8-row class) the chunk width per matrix.
 int default_chunk_width(int bm, int colB_p)
 {
     if (colB_p == 32) return 32;
@@ -549,48 +550,17 @@ const void *select_kernel(int bm, int prec, int w, int s, bool packed)
     return nullptr;
 }
 
-static int cu_count()
-{
-    static int n = 0;
-    if (n == 0) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-            n = v;
-        else
-            n = 256;
-    }
-    return n;
-}
-
-int default_tasks_per_wave(int ntasks, int nchunks)
-{
-    (void)ntasks;
-    (void)nchunks;
-    (void)cu_count;
-    return 1;
-}
-
-int default_chunk_major(int bm, int prec, int colB_p, int w)
-{
-    (void)bm;
-    (void)prec;
-    (void)colB_p;
-    (void)w;
-    return 0;
-}
-
 // Resolves the variant defaults of a launch; false if the variant is invalid.
-static bool resolve_variant(int bm, int prec, int colB_p, int &w, int &s, int &nchunks, int ntasks, int &tpw,
-                            int order, int &cm)
+static bool resolve_variant(int bm, int prec, int colB_p, int &w, int &s, int &nchunks, int &tpw, int order,
+                            int &cm)
 {
     if (w <= 0) w = default_chunk_width(bm, colB_p);
     if (colB_p % w != 0) return false;
     if (s <= 0) s = default_stages(bm, prec, w);
     if (!valid_variant(bm, w, s)) return false;
     nchunks = colB_p / w;
-    if (tpw <= 0) tpw = default_tasks_per_wave(ntasks, nchunks);
-    cm = order > 0 ? (order == 2 ? 1 : 0) : default_chunk_major(bm, prec, colB_p, w);
+    if (tpw <= 0) tpw = 1;
+    cm = order == 2 ? 1 : 0;
     return true;
 }
 
@@ -603,7 +573,7 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
     if (packed && (bm == 64 || !vptr)) return TSP_EINVAL;
     if (placement != kPlaceContiguous && placement != kPlaceInterleaved) return TSP_EINVAL;
     int nchunks = 0, cm = 0;
-    if (!resolve_variant(bm, prec, colB_p, w, s, nchunks, ntasks, tpw, order, cm)) return TSP_EINVAL;
+    if (!resolve_variant(bm, prec, colB_p, w, s, nchunks, tpw, order, cm)) return TSP_EINVAL;
     const long long ranges = ((long long)ntasks + tpw - 1) / tpw;
     const long long waves = ranges * nchunks;
     long long blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
