@@ -622,26 +622,35 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
             };
             std::vector<double> best_of;
             TSP_TRY(time_options(cand, best_of));
-            size_t pick = 0;
-            for (size_t j = 1; j < cand.size(); ++j)
-                if (best_of[j] < best_of[pick]) pick = j;
-            // XCD placement of the pick: contiguous eighths (neighbouring
+            std::vector<size_t> order(cand.size());
+            for (size_t j = 0; j < cand.size(); ++j) order[j] = j;
+            std::sort(order.begin(), order.end(), [&](size_t a, size_t b) { return best_of[a] < best_of[b]; });
+            // XCD placement of the two best: contiguous eighths (neighbouring
             // row-blocks share an L2) against runs dealt round-robin, which
-            // balances matrices whose heavy row-blocks sit together
-            std::vector<Opt> pl = {cand[pick], cand[pick]};
-            pl[1].place = TSP_PLACE_INTERLEAVED;
+            // balances matrices whose heavy row-blocks sit together (and can
+            // reverse a close call between the two)
+            std::vector<Opt> pl;
+            for (size_t j = 0; j < std::min<size_t>(2, order.size()); ++j)
+                for (int place = TSP_PLACE_CONTIGUOUS; place <= TSP_PLACE_INTERLEAVED; ++place) {
+                    Opt o = cand[order[j]];
+                    o.place = place;
+                    pl.push_back(o);
+                }
             std::vector<double> pl_ms;
             TSP_TRY(time_options(pl, pl_ms));
+            size_t best = 0;
+            for (size_t j = 1; j < pl.size(); ++j)
+                if (pl_ms[j] < pl_ms[best]) best = j;
             if (getenv("TSP_TUNE_LOG")) {
                 for (size_t j = 0; j < cand.size(); ++j)
-                    fprintf(stderr, "tune bm=%d th=%d format=%d order=%d tasks/wave=%d: %.5f ms%s\n", c.bm, c.th,
-                            cand[j].fmt, cand[j].order, cand[j].tpw, best_of[j], j == pick ? "  <- kept" : "");
-                for (int j = 0; j < 2; ++j)
-                    fprintf(stderr, "tune bm=%d placement=%s: %.5f ms%s\n", c.bm,
-                            j ? "interleaved" : "contiguous", pl_ms[j],
-                            (pl_ms[1] < pl_ms[0]) == (j == 1) ? "  <- kept" : "");
+                    fprintf(stderr, "tune bm=%d th=%d format=%d order=%d tasks/wave=%d: %.5f ms\n", c.bm, c.th,
+                            cand[j].fmt, cand[j].order, cand[j].tpw, best_of[j]);
+                for (size_t j = 0; j < pl.size(); ++j)
+                    fprintf(stderr, "tune bm=%d format=%d order=%d tasks/wave=%d placement=%s: %.5f ms%s\n", c.bm,
+                            pl[j].fmt, pl[j].order, pl[j].tpw, pl[j].place ? "interleaved" : "contiguous", pl_ms[j],
+                            j == best ? "  <- kept" : "");
             }
-            const Opt &o = pl[pl_ms[1] < pl_ms[0] ? 1 : 0];
+            const Opt &o = pl[best];
             TSP_TRY(tsp_plan_set_format(p, c.bm, o.fmt));
             c.var_order = o.order;
             c.var_tpw = o.tpw == 1 ? 0 : o.tpw;
