@@ -533,6 +533,17 @@ extern "C" int tsp_plan_warmup(tsp_plan *p, int iters)
     return tsp_device_sync();
 }
 
+// One tuning measurement of a class: a warm-up launch, then enough launches
+// to span about 2 ms (at least 3, at most 200), so that short kernels are not
+// decided by timer noise and long ones cost little.
+static int tune_time_class(tsp_plan *p, int bm, double *ms)
+{
+    double warm = 0;
+    TSP_TRY(tsp_plan_time_class(p, bm, 1, &warm));
+    const int reps = (int)std::min(200.0, std::max(3.0, 2.0 / std::max(warm, 1e-4)));
+    return tsp_plan_time_class(p, bm, reps, ms);
+}
+
 extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model_ms, double *tune_ms)
 {
     if (!p) return TSP_EINVAL;
@@ -610,12 +621,8 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
                         c.var_order = opts[j].order;
                         c.var_tpw = opts[j].tpw;
                         c.place = opts[j].place;
-                        double warm = 0, ms = 0;
-                        TSP_TRY(tsp_plan_time_class(p, c.bm, 3, &warm));
-                        // at least 10 launches and about 2 ms per timing, so
-                        // that short kernels are not decided by timer noise
-                        const int reps = (int)std::min(200.0, std::max(10.0, 2.0 / std::max(warm, 1e-4)));
-                        TSP_TRY(tsp_plan_time_class(p, c.bm, reps, &ms));
+                        double ms = 0;
+                        TSP_TRY(tune_time_class(p, c.bm, &ms));
                         best_of[j] = std::min(best_of[j], ms);
                     }
                 return TSP_OK;
@@ -662,10 +669,8 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
                 for (int round = 0; round < 2; ++round)
                     for (int j = 0; j < 2; ++j) {
                         c.var_w = j ? 128 : 0;
-                        double warm = 0, t = 0;
-                        TSP_TRY(tsp_plan_time_class(p, c.bm, 3, &warm));
-                        const int reps = (int)std::min(200.0, std::max(10.0, 2.0 / std::max(warm, 1e-4)));
-                        TSP_TRY(tsp_plan_time_class(p, c.bm, reps, &t));
+                        double t = 0;
+                        TSP_TRY(tune_time_class(p, c.bm, &t));
                         ms[j] = std::min(ms[j], t);
                     }
                 c.var_w = ms[1] < ms[0] ? 128 : 0;
