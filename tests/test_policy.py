@@ -63,6 +63,26 @@ def test_policy_against_exhaustive_tuning(tsp):
     assert np.mean(slow) < np.mean(prov)
 
 
+HELDOUT = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_heldout_config5.jsonl")
+
+
+def test_policy_on_held_out_config5(tsp):
+    """Configuration 5 (RMAT scale 22) is not in the training sweep.  Its
+    exhaustive sweep with the full shipped path (runtime tuning of every
+    candidate) puts the policy's pick within a few percent of the best
+    candidate: fp16 x1.002, tf32 x1.04 (colB 64) and x1.07 (colB 128)."""
+    g, d = tsp.policy_candidates()
+    recs = [json.loads(l) for l in open(HELDOUT) if l.strip()]
+    assert {(r["prec"], r["colB"]) for r in recs} == {(0, 64), (0, 128), (1, 64), (1, 128)}
+    slow = []
+    for r in recs:
+        pg, pd = tsp.predict(np.array(r["features"]), r["prec"])
+        a = [i for i in range(len(g)) if g[i] == np.float32(pg) and d[i] == np.float32(pd)]
+        assert a, (pg, pd)
+        slow.append(r["times_ms"][a[0]] / r["best_ms"])
+    assert max(slow) <= 1.08 and np.mean(slow) <= 1.03, slow
+
+
 TH_DATA = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_thsweep.jsonl")
 
 
