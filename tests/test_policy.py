@@ -57,7 +57,7 @@ def test_policy_against_exhaustive_tuning(tsp):
         assert a, (pg, pd)
         slow.append(r["times_ms"][a[0]] / r["best_ms"])
     # The retrained table is within a few percent of the exhaustive optimum on
-    # its sweep; the provisional single-leaf table (candidate 24) is x1.04.
+    # its sweep; the provisional single-leaf table (candidate 24) is x1.05.
     assert np.mean(slow) <= 1.03 and max(slow) <= 1.25, (np.mean(slow), max(slow))
     prov = [r["times_ms"][24] / r["best_ms"] for r in records()]
     assert np.mean(slow) < np.mean(prov)
