@@ -544,6 +544,100 @@ static int tune_time_class(tsp_plan *p, int bm, double *ms)
     return tsp_plan_time_class(p, bm, reps, ms);
 }
 
+// MI355X additions to the runtime tuning, measured for one class with its
+// threshold fixed (each option timed on the class's own stream, best of two
+// interleaved rounds, so a drift of the clock cannot decide a pick):
+//   1. A format (dense tiles, or bitmap-packed: fewer bytes against a per-lane
+//      decode) x chunk order (chunks of one task side by side share A tiles in
+//      L2; chunk-major shrinks the live B working set per phase) x tasks per
+//      wave (1, or 4 when row-blocks are split: consecutive tasks of a split
+//      row-block then merge into one flush instead of several atomic ones);
+//   2. the two best of step 1 under both XCD placements (contiguous eighths
+//      keep neighbouring row-blocks, which share B rows, on one L2; runs dealt
+//      round-robin balance matrices whose heavy row-blocks sit together);
+//   3. for the 8-row class, 128-column chunks (half the waves, 256-byte fp16
+//      B row segments) against the default width.
+// A class whose variant was pinned with tsp_plan_set_variant is left alone.
+static int tune_class(tsp_plan *p, ClassDev &c)
+{
+    if (!c.active() || c.ntasks == 0 || c.var_w || c.var_order || c.var_tpw) return TSP_OK;
+    tsp_kernel_info k;
+    TSP_TRY(tsp_kernel_probe(c.bm, p->prec, p->colB_p, &k));
+    const bool chunks = p->colB_p / k.cols_per_task >= 2;
+    bool any_split = false;
+    for (int i = 0; i < c.ntasks && !any_split; ++i) any_split = (c.m->blkcoostylerowidx[i] & 0x80000000u) != 0;
+    struct Opt {
+        int fmt, order, tpw, place;
+    };
+    auto time_options = [&](const std::vector<Opt> &opts, std::vector<double> &best_of) -> int {
+        best_of.assign(opts.size(), 1e30);
+        for (int round = 0; round < (opts.size() > 1 ? 2 : 0); ++round)
+            for (size_t j = 0; j < opts.size(); ++j) {
+                TSP_TRY(tsp_plan_set_format(p, c.bm, opts[j].fmt));
+                c.var_order = opts[j].order;
+                c.var_tpw = opts[j].tpw;
+                c.place = opts[j].place;
+                double ms = 0;
+                TSP_TRY(tune_time_class(p, c.bm, &ms));
+                best_of[j] = std::min(best_of[j], ms);
+            }
+        return TSP_OK;
+    };
+    const bool log = getenv("TSP_TUNE_LOG") != nullptr;
+
+    std::vector<Opt> cand;
+    for (int fmt = 1; fmt <= (c.pack_ok ? 2 : 1); ++fmt)
+        for (int o = chunks ? 1 : 0; o <= (chunks ? 2 : 0); ++o)
+            for (int tpw = 1; tpw <= (any_split ? 4 : 1); tpw += 3) cand.push_back({fmt, o, tpw, TSP_PLACE_CONTIGUOUS});
+    std::vector<double> cand_ms;
+    TSP_TRY(time_options(cand, cand_ms));
+    std::vector<size_t> rank(cand.size());
+    for (size_t j = 0; j < cand.size(); ++j) rank[j] = j;
+    std::sort(rank.begin(), rank.end(), [&](size_t a, size_t b) { return cand_ms[a] < cand_ms[b]; });
+    if (log)
+        for (size_t j = 0; j < cand.size(); ++j)
+            fprintf(stderr, "tune bm=%d th=%d format=%d order=%d tasks/wave=%d: %.5f ms\n", c.bm, c.th, cand[j].fmt,
+                    cand[j].order, cand[j].tpw, cand_ms[j]);
+
+    std::vector<Opt> pl;
+    for (size_t j = 0; j < std::min<size_t>(2, rank.size()); ++j)
+        for (int place = TSP_PLACE_CONTIGUOUS; place <= TSP_PLACE_INTERLEAVED; ++place) {
+            Opt o = cand[rank[j]];
+            o.place = place;
+            pl.push_back(o);
+        }
+    std::vector<double> pl_ms;
+    TSP_TRY(time_options(pl, pl_ms));
+    size_t best = 0;
+    for (size_t j = 1; j < pl.size(); ++j)
+        if (pl_ms[j] < pl_ms[best]) best = j;
+    if (log)
+        for (size_t j = 0; j < pl.size(); ++j)
+            fprintf(stderr, "tune bm=%d format=%d order=%d tasks/wave=%d placement=%s: %.5f ms%s\n", c.bm, pl[j].fmt,
+                    pl[j].order, pl[j].tpw, pl[j].place ? "interleaved" : "contiguous", pl_ms[j],
+                    j == best ? "  <- kept" : "");
+    TSP_TRY(tsp_plan_set_format(p, c.bm, pl[best].fmt));
+    c.var_order = pl[best].order;
+    c.var_tpw = pl[best].tpw == 1 ? 0 : pl[best].tpw;
+    c.place = pl[best].place;
+
+    if (c.bm == 8 && k.cols_per_task != 128 && p->colB_p % 128 == 0) {
+        double ms[2] = {1e30, 1e30};
+        for (int round = 0; round < 2; ++round)
+            for (int j = 0; j < 2; ++j) {
+                c.var_w = j ? 128 : 0;
+                double t = 0;
+                TSP_TRY(tune_time_class(p, c.bm, &t));
+                ms[j] = std::min(ms[j], t);
+            }
+        c.var_w = ms[1] < ms[0] ? 128 : 0;
+        if (log)
+            fprintf(stderr, "tune bm=%d chunk width default: %.5f ms, 128: %.5f ms%s\n", c.bm, ms[0], ms[1],
+                    c.var_w ? "  <- 128 kept" : "");
+    }
+    return TSP_OK;
+}
+
 extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model_ms, double *tune_ms)
 {
     if (!p) return TSP_EINVAL;
@@ -586,99 +680,7 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
         t3 = now_ms();
     }
     if (tune) {
-        // MI355X additions, measured per class: the A format (dense tiles or
-        // bitmap-packed -- fewer bytes against a per-lane decode) and the
-        // column-chunk order (chunks of one task side by side share A tiles
-        // in L2; chunk-major shrinks the live B working set per phase).
-        // Which wins depends on the matrix, |B| against the MALL and the
-        // class, so both are timed.
-        for (int i = 0; i < 3; ++i) {
-            ClassDev &c = p->cls[i];
-            if (!c.active() || c.ntasks == 0 || c.var_w || c.var_order || c.var_tpw) continue;
-            tsp_kernel_info k;
-            TSP_TRY(tsp_kernel_probe(c.bm, p->prec, p->colB_p, &k));
-            const bool chunks = p->colB_p / k.cols_per_task >= 2;
-            // Tasks per wave: one, or four consecutive tasks streamed by one
-            // wave (consecutive tasks of a split row-block then merge into
-            // one flush instead of several atomic ones); worth timing only
-            // when the schedule has split tasks.
-            bool any_split = false;
-            for (int i2 = 0; i2 < c.ntasks && !any_split; ++i2)
-                any_split = (c.m->blkcoostylerowidx[i2] & 0x80000000u) != 0;
-            struct Opt { int fmt, order, tpw, place; };
-            std::vector<Opt> cand;
-            for (int fmt = 1; fmt <= (c.pack_ok ? 2 : 1); ++fmt)
-                for (int o = chunks ? 1 : 0; o <= (chunks ? 2 : 0); ++o)
-                    for (int tpw = 1; tpw <= (any_split ? 4 : 1); tpw += 3)
-                        cand.push_back({fmt, o, tpw, TSP_PLACE_CONTIGUOUS});
-            // two interleaved rounds, best of each option: a drift of the
-            // clock between options cannot decide the pick
-            auto time_options = [&](const std::vector<Opt> &opts, std::vector<double> &best_of) -> int {
-                best_of.assign(opts.size(), 1e30);
-                for (int round = 0; round < (opts.size() > 1 ? 2 : 0); ++round)
-                    for (size_t j = 0; j < opts.size(); ++j) {
-                        TSP_TRY(tsp_plan_set_format(p, c.bm, opts[j].fmt));
-                        c.var_order = opts[j].order;
-                        c.var_tpw = opts[j].tpw;
-                        c.place = opts[j].place;
-                        double ms = 0;
-                        TSP_TRY(tune_time_class(p, c.bm, &ms));
-                        best_of[j] = std::min(best_of[j], ms);
-                    }
-                return TSP_OK;
-            };
-            std::vector<double> best_of;
-            TSP_TRY(time_options(cand, best_of));
-            std::vector<size_t> order(cand.size());
-            for (size_t j = 0; j < cand.size(); ++j) order[j] = j;
-            std::sort(order.begin(), order.end(), [&](size_t a, size_t b) { return best_of[a] < best_of[b]; });
-            // XCD placement of the two best: contiguous eighths (neighbouring
-            // row-blocks share an L2) against runs dealt round-robin, which
-            // balances matrices whose heavy row-blocks sit together (and can
-            // reverse a close call between the two)
-            std::vector<Opt> pl;
-            for (size_t j = 0; j < std::min<size_t>(2, order.size()); ++j)
-                for (int place = TSP_PLACE_CONTIGUOUS; place <= TSP_PLACE_INTERLEAVED; ++place) {
-                    Opt o = cand[order[j]];
-                    o.place = place;
-                    pl.push_back(o);
-                }
-            std::vector<double> pl_ms;
-            TSP_TRY(time_options(pl, pl_ms));
-            size_t best = 0;
-            for (size_t j = 1; j < pl.size(); ++j)
-                if (pl_ms[j] < pl_ms[best]) best = j;
-            if (getenv("TSP_TUNE_LOG")) {
-                for (size_t j = 0; j < cand.size(); ++j)
-                    fprintf(stderr, "tune bm=%d th=%d format=%d order=%d tasks/wave=%d: %.5f ms\n", c.bm, c.th,
-                            cand[j].fmt, cand[j].order, cand[j].tpw, best_of[j]);
-                for (size_t j = 0; j < pl.size(); ++j)
-                    fprintf(stderr, "tune bm=%d format=%d order=%d tasks/wave=%d placement=%s: %.5f ms%s\n", c.bm,
-                            pl[j].fmt, pl[j].order, pl[j].tpw, pl[j].place ? "interleaved" : "contiguous", pl_ms[j],
-                            j == best ? "  <- kept" : "");
-            }
-            const Opt &o = pl[best];
-            TSP_TRY(tsp_plan_set_format(p, c.bm, o.fmt));
-            c.var_order = o.order;
-            c.var_tpw = o.tpw == 1 ? 0 : o.tpw;
-            c.place = o.place;
-            // 128-column chunks for the 8-row class: half the waves, each
-            // gathering 256-byte B row segments (fp16) instead of 128-byte ones
-            if (c.bm == 8 && k.cols_per_task != 128 && p->colB_p % 128 == 0) {
-                double ms[2] = {1e30, 1e30};
-                for (int round = 0; round < 2; ++round)
-                    for (int j = 0; j < 2; ++j) {
-                        c.var_w = j ? 128 : 0;
-                        double t = 0;
-                        TSP_TRY(tune_time_class(p, c.bm, &t));
-                        ms[j] = std::min(ms[j], t);
-                    }
-                c.var_w = ms[1] < ms[0] ? 128 : 0;
-                if (getenv("TSP_TUNE_LOG"))
-                    fprintf(stderr, "tune bm=%d chunk width default: %.5f ms, 128: %.5f ms%s\n", c.bm, ms[0], ms[1],
-                            c.var_w ? "  <- 128 kept" : "");
-            }
-        }
+        for (ClassDev &c : p->cls) TSP_TRY(tune_class(p, c));
         t3 = now_ms();
     }
     if (tune_ms) *tune_ms = t3 - t2;
