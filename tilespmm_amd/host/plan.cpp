@@ -177,14 +177,15 @@ static int upload_dense(tsp_plan *p, ClassDev &c)
     return tsp_memcpy_h2d(c.d_val, c.m->Blockdense_Val, vs * c.m->dnssize);
 }
 
-static int launch_class(tsp_plan *p, ClassDev &c)
+// Launch one class on `stream` (its own stream unless given another).
+static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
 {
     if (!c.active() || c.ntasks == 0) return TSP_OK;
     const bool pk = c.fmt == 2;
     return tsp_spmm_launch_placed(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val,
                                   pk ? c.d_bmp : nullptr, pk ? c.d_vptr : nullptr, c.d_rows, c.d_colstart,
-                                  p->d_B, p->d_C, c.d_colidx, p->rowA, c.stream, c.var_w, c.var_s,
-                                  c.var_tpw, c.var_order, c.place);
+                                  p->d_B, p->d_C, c.d_colidx, p->rowA, stream ? stream : c.stream, c.var_w,
+                                  c.var_s, c.var_tpw, c.var_order, c.place);
 }
 
 extern "C" int tsp_plan_set_format(tsp_plan *p, int bm, int fmt)
@@ -298,6 +299,7 @@ static int plan_begin(std::unique_ptr<tsp_plan> &p, int device_id, int rowA, int
     p->rowA = rowA;
     p->colA = colA;
     p->colB_p = colB_p;
+    TSP_TRY(tsp_stream_create_nonblocking(&p->main));
     const size_t vs = tsph::val_size(prec);
     const size_t bbytes = vs * (size_t)colA * colB_p, cbytes = sizeof(float) * (size_t)rowA * colB_p;
     TSP_TRY(tsp_malloc(&p->d_B, bbytes));
@@ -318,7 +320,6 @@ static int class_finish(ClassDev &c)
 
 static int plan_end(tsp_plan *p)
 {
-    TSP_TRY(tsp_stream_create_nonblocking(&p->main));
     TSP_TRY(tsp_event_create(&p->ev0));
     TSP_TRY(tsp_event_create(&p->ev1));
     for (void *&e : p->done) TSP_TRY(tsp_event_create(&e));
@@ -471,6 +472,20 @@ extern "C" int tsp_plan_set_th(tsp_plan *p, int th64, int th16, int th8)
 // join back on main.
 static int fork_join(tsp_plan *p, int reps)
 {
+    // a plan with one active class launches it on the main stream: there is
+    // nothing to overlap, and the cross-stream fork and join cost about a
+    // microsecond per step on the small matrices
+    ClassDev *only = nullptr;
+    int active = 0;
+    for (ClassDev &c : p->cls)
+        if (c.active() && c.ntasks > 0) {
+            ++active;
+            only = &c;
+        }
+    if (active == 1) {
+        for (int r = 0; r < reps; ++r) TSP_TRY(launch_class(p, *only, p->main));
+        return TSP_OK;
+    }
     TSP_TRY(tsp_event_record(p->ev0, p->main));
     for (int i = 0; i < 3; ++i) {
         ClassDev &c = p->cls[i];
