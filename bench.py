@@ -36,8 +36,10 @@ def alg_bytes(rows, nnz, s_a, k_rows, n, s_b):
 
 
 def gather_calibration(hip, reps):
-    """Random 128/256-byte row gathers from tables of 2 MB .. 2 GB
-    (tsp_gather_kernel): the bandwidth ceiling of B-row gathers."""
+    """Random 128/256-byte row gathers from tables of 2 MB .. 2 GB, and
+    16-64-byte rows from 1 GB (tsp_gather_kernel): the bandwidth ceiling of
+    B-row gathers, and its unit (one request per cache line, whatever the
+    row's size)."""
     import ctypes as C
     maxb = 2 << 30
     tab, sink = C.c_void_p(), C.c_void_p()
@@ -47,22 +49,24 @@ def gather_calibration(hip, reps):
     hip.tsp_event_create(C.byref(e0))
     hip.tsp_event_create(C.byref(e1))
     iters = 64
-    for rowb in (128, 256):
-        for mb in (2, 8, 32, 128, 256, 512, 1024, 2048):
-            nb = mb << 20
-            for w in range(3):
-                assert hip.tsp_gather_kernel(tab, nb, rowb, iters, w, sink, None) == 0
-            hip.tsp_event_record(e0, None)
-            for r in range(reps):
-                hip.tsp_gather_kernel(tab, nb, rowb, iters, 100 + r, sink, None)
-            hip.tsp_event_record(e1, None)
-            hip.tsp_event_sync(e1)
-            ms = C.c_float()
-            hip.tsp_event_elapsed_ms(C.byref(ms), e0, e1)
-            t = ms.value / reps
-            nbytes = 8192 * 256 * 16 * iters
-            print(json.dumps({"gather_row_bytes": rowb, "table_mb": mb, "ms": round(t, 5),
-                              "gbs": round(nbytes / (t * 1e-3) / 1e9, 1)}), flush=True)
+    cases = [(rowb, mb) for rowb in (128, 256) for mb in (2, 8, 32, 128, 256, 512, 1024, 2048)]
+    cases += [(rowb, 1024) for rowb in (16, 32, 64)]
+    for rowb, mb in cases:
+        nb = mb << 20
+        for w in range(3):
+            assert hip.tsp_gather_kernel(tab, nb, rowb, iters, w, sink, None) == 0
+        hip.tsp_event_record(e0, None)
+        for r in range(reps):
+            hip.tsp_gather_kernel(tab, nb, rowb, iters, 100 + r, sink, None)
+        hip.tsp_event_record(e1, None)
+        hip.tsp_event_sync(e1)
+        ms = C.c_float()
+        hip.tsp_event_elapsed_ms(C.byref(ms), e0, e1)
+        t = ms.value / reps
+        nbytes = 8192 * 256 * 16 * iters
+        print(json.dumps({"gather_row_bytes": rowb, "table_mb": mb, "ms": round(t, 5),
+                          "gbs": round(nbytes / (t * 1e-3) / 1e9, 1),
+                          "g_rows_per_s": round(nbytes / rowb / (t * 1e-3) / 1e9, 2)}), flush=True)
     hip.tsp_free(tab)
     hip.tsp_free(sink)
 

@@ -188,7 +188,7 @@ int tsp_vendor_spmm(int prec, int m, int k, long long nnz, const int *rowptr, co
 int tsp_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
 /* Random row gathers (the access pattern of SpMM's B rows): 8192 x 256
  * threads, each group of row_bytes/16 lanes reads `iters` uniformly random
- * rows of row_bytes (128 or 256) from `table`; one launch reads
+ * rows of row_bytes (16, 32, 64, 128 or 256) from `table`; one launch reads
  * 8192 * 256 * 16 * iters bytes.  sink: 8192 * 256 uint32 of device memory
  * (written only on an improbable value pattern).  Calibrates the gather
  * bandwidth ceiling; no reference counterpart. */

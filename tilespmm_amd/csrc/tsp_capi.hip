@@ -260,7 +260,8 @@ int tsp_copy_kernel(void *dst, const void *src, size_t bytes, void *stream)
 int tsp_gather_kernel(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed,
                       void *sink, void *stream)
 {
-    if (!table || !sink || (row_bytes != 128 && row_bytes != 256) || iters <= 0) return TSP_EINVAL;
+    const bool rb_ok = row_bytes == 16 || row_bytes == 32 || row_bytes == 64 || row_bytes == 128 || row_bytes == 256;
+    if (!table || !sink || !rb_ok || iters <= 0) return TSP_EINVAL;
     if (table_bytes < (size_t)row_bytes || table_bytes / (size_t)row_bytes > 0xffffffffull) return TSP_EINVAL;
     if ((uintptr_t)table & 15) return TSP_EINVAL;
     return tsp::launch_gather(table, table_bytes, row_bytes, iters, seed, sink, (hipStream_t)stream);

@@ -643,10 +643,16 @@ int launch_gather(const void *table, size_t table_bytes, int row_bytes, int iter
                   hipStream_t s)
 {
     const uint32_t nrows = (uint32_t)(table_bytes / (size_t)row_bytes);
-    if (row_bytes == 128)
-        gather_kernel<128><<<kGatherBlocks, 256, 0, s>>>((const u4 *)table, nrows, iters, seed, (uint32_t *)sink);
-    else
-        gather_kernel<256><<<kGatherBlocks, 256, 0, s>>>((const u4 *)table, nrows, iters, seed, (uint32_t *)sink);
+    const u4 *t = (const u4 *)table;
+    uint32_t *k = (uint32_t *)sink;
+    switch (row_bytes) {
+    case 16: gather_kernel<16><<<kGatherBlocks, 256, 0, s>>>(t, nrows, iters, seed, k); break;
+    case 32: gather_kernel<32><<<kGatherBlocks, 256, 0, s>>>(t, nrows, iters, seed, k); break;
+    case 64: gather_kernel<64><<<kGatherBlocks, 256, 0, s>>>(t, nrows, iters, seed, k); break;
+    case 128: gather_kernel<128><<<kGatherBlocks, 256, 0, s>>>(t, nrows, iters, seed, k); break;
+    case 256: gather_kernel<256><<<kGatherBlocks, 256, 0, s>>>(t, nrows, iters, seed, k); break;
+    default: return TSP_EINVAL;
+    }
     return (int)hipGetLastError();
 }
 
