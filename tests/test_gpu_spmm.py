@@ -96,7 +96,7 @@ def random_b(tsp, rng, cols, colB, prec):
 
 
 @pytest.mark.parametrize("prec", [0, 1])
-@pytest.mark.parametrize("colB", [8, 32, 64, 100, 128, 192, 256])
+@pytest.mark.parametrize("colB", [8, 32, 64, 100, 128, 192, 256, 320, 512])
 def test_random_all_classes(gpu, orc, prec, colB):
     tsp = gpu
     rng = np.random.default_rng(prec * 1000 + colB)
