@@ -87,3 +87,33 @@ def test_cli_usage_and_errors(tmp_path):
     p.write_text("%%MatrixMarket matrix coordinate pattern general\n2 2 1\n1 1\n")
     r = subprocess.run([exe, "-d", "0", str(p), "0"], capture_output=True, text=True)
     assert r.returncode == 1 and "colB" in r.stderr
+
+
+def test_cli_rejects_malformed_and_oversized_inputs(tmp_path, tsp):
+    """Fail-fast paths the reference leaves undefined (it ignores
+    mmio_allinone's status): every bad input ends with exit status 1 and a
+    message, never a signal.  The oversized header runs under a 2 GB address
+    space limit, so the reader's allocation fails instead of the machine
+    swapping."""
+    import resource
+    exe = os.path.join(ROOT, "tilespmm_amd", "bin", "tilespmm_fp16")
+    files = {
+        "truncated": "%%MatrixMarket matrix coordinate real general\n3 3 2\n1 1 1.0\n",
+        "no_header": "garbage\n1 2 3\n",
+        "out_of_range": "%%MatrixMarket matrix coordinate real general\n3 3 2\n1 1 1.0\n9 1 2.0\n",
+        "bad_number": "%%MatrixMarket matrix coordinate real general\n3 3 1\n1 x 1.0\n",
+        "huge": "%%MatrixMarket matrix coordinate real general\n300000000 300000000 900000000\n1 1 1.0\n",
+    }
+    limit = lambda: resource.setrlimit(resource.RLIMIT_AS, (2 << 30, 2 << 30))
+    for name, text in files.items():
+        p = tmp_path / f"{name}.mtx"
+        p.write_text(text)
+        r = subprocess.run([exe, "-d", "0", str(p), "32"], capture_output=True, text=True, timeout=120,
+                           preexec_fn=limit if name == "huge" else None)
+        assert r.returncode == 1, (name, r.returncode, r.stderr[-500:])
+        assert "Cannot read Matrix Market file" in r.stderr, (name, r.stderr[-500:])
+    if not tsp.device_available():
+        p = tmp_path / "ok.mtx"
+        p.write_text("%%MatrixMarket matrix coordinate real general\n4 4 2\n1 1 1.0\n2 3 2.0\n")
+        r = subprocess.run([exe, "-d", "0", str(p), "32"], capture_output=True, text=True, timeout=120)
+        assert r.returncode == 1 and "not a usable gfx950" in r.stderr, r.stderr[-500:]
