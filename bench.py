@@ -1,13 +1,14 @@
 """Benchmark driver: SpMM TFLOPS (2*nnz*colB/t) and % of the MI355X HBM
 roofline for one synthetic configuration, on one GPU.
 
-A step is one full tiled SpMM C = A*B (the three row-block class kernels,
-each on its own stream, joined on the null stream) with A's tiles, the
-schedule, B and C already resident in HBM.  Default workload: configuration 2
+A step is one full tiled SpMM C = A*B (the row-block class kernels, each on
+its own stream, forked from and joined on the plan's main stream; a plan
+with one class launches it on the main stream) with A's tiles, the schedule,
+B and C already resident in HBM.  Default workload: configuration 2
 (5-point Laplacian 512x512, fp16, colB 128).  Prints ONE JSON line.
 
   python bench.py [--steps K] [--warmup W] [--config 1..5] [--prec fp16|tf32]
-                  [--colB N] [--no-cpu] [--no-vendor] [--gpus 1]
+                  [--colB N] [--no-cpu] [--no-vendor] [--cold-reps N] [--gpus 1]
 """
 import argparse
 import json
@@ -99,6 +100,54 @@ def copy_calibration(hip, nbytes, reps):
     hip.tsp_free(dst)
 
 
+def cold_steps(hip, plan, reps, stream_bytes, flush_bytes=512 << 20):
+    """Median time of one step after a plain copy over 2 x flush_bytes of
+    other memory, which evicts L2 (8 x 4 MB) and the 256 MB MALL, so A, B and
+    C come from HBM; of the same single step repeated right after it, with
+    the caches warm; and of a plain copy moving stream_bytes (half read, half
+    written) after the same eviction, the cold streaming rate at that size.
+    The headline steps are back to back, as the reference times them: these
+    medians separate what caches carry across steps from the fixed cost of
+    timing one step alone."""
+    import ctypes as C
+    half = max(16, stream_bytes // 32 * 16)
+    bufs = [C.c_void_p() for _ in range(4)]
+    sizes = (flush_bytes, flush_bytes, half, half)
+    if any(hip.tsp_malloc(C.byref(b), n) for b, n in zip(bufs, sizes)):
+        raise SystemExit("bench.py: cannot allocate the cache-flush buffers")
+    src, dst, csrc, cdst = bufs
+    hip.tsp_memset(src, 1, flush_bytes)
+    hip.tsp_memset(csrc, 1, half)
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    hip.tsp_event_create(C.byref(e0))
+    hip.tsp_event_create(C.byref(e1))
+
+    def flush():
+        if hip.tsp_copy_kernel(dst, src, flush_bytes, None) or hip.tsp_device_sync():
+            raise SystemExit("bench.py: cache-flush copy failed")
+
+    cold, warm, copy = [], [], []
+    try:
+        for _ in range(reps):
+            flush()
+            cold.append(plan.time(1))
+            warm.append(plan.time(1))
+            flush()
+            hip.tsp_event_record(e0, None)
+            hip.tsp_copy_kernel(cdst, csrc, half, None)
+            hip.tsp_event_record(e1, None)
+            hip.tsp_event_sync(e1)
+            ms = C.c_float()
+            hip.tsp_event_elapsed_ms(C.byref(ms), e0, e1)
+            copy.append(ms.value)
+    finally:
+        for b in bufs:
+            hip.tsp_free(b)
+        hip.tsp_event_destroy(e0)
+        hip.tsp_event_destroy(e1)
+    return float(np.median(cold)), float(np.median(warm)), float(np.median(copy)), 2 * half
+
+
 def default_width(hip, bm, prec, cbp):
     """Output columns one wave covers when the plan keeps the library default."""
     import ctypes as C
@@ -153,11 +202,15 @@ def main():
                     help="pin the tasks per wave per class 64,16,8 (0 keep)")
     ap.add_argument("--width", type=ints3, default=None,
                     help="pin the chunk width per class 64,16,8 (32, 64, 128; 0 keep)")
+    ap.add_argument("--stages", type=ints3, default=None,
+                    help="pin the pipeline depth per class 64,16,8 (1-4; 0 keep)")
     ap.add_argument("--place", type=ints3, default=None,
                     help="pin the XCD placement per class 64,16,8 (1 contiguous, 2 interleaved, 0 keep)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-vendor", action="store_true")
     ap.add_argument("--class-reps", type=int, default=200)
+    ap.add_argument("--cold-reps", type=int, default=50,
+                    help="single steps timed after evicting L2 and MALL (0 skips)")
     ap.add_argument("--sweep", action="store_true", help="time every kernel variant per class instead")
     ap.add_argument("--gather", action="store_true",
                     help="only run the random row-gather probe (gather bandwidth ceiling)")
@@ -222,6 +275,10 @@ def main():
         if wd:
             _, st, n, o = plan.get_variant(bm)
             plan.set_variant(bm, wd, st, n, o)
+    for bm, sg in zip((64, 16, 8), args.stages or ()):
+        if sg:
+            wd, _, n, o = plan.get_variant(bm)
+            plan.set_variant(bm, wd, sg, n, o)
     for bm, pl in zip((64, 16, 8), args.place or ()):
         if pl:
             plan.set_placement(bm, pl - 1)
@@ -232,26 +289,30 @@ def main():
         plan.close()
         return
 
-    # warmup, then K timed steps bracketed by device syncs and null-stream events
+    # warmup, then K timed steps bracketed by device syncs and main-stream events
     plan.warmup(args.warmup)
     plan.run(zero_c=True)
     hip.tsp_device_sync()
     ms = plan.time(args.steps)
     hip.tsp_device_sync()
     tflops = 2.0 * A.nnz * colB / (ms * 1e-3) / 1e12
-
     # per-class kernel time (each class alone on its own stream)
     cls = {}
     for t, sb, bm in zip(tiles, subs, (64, 16, 8)):
         if t.tilenum == 0:
             continue
-        cms = plan.time_class(bm, args.class_reps)
+        # one untimed round first (the clock drops while the device idles),
+        # then enough launches to span at least 20 ms
+        warm = plan.time_class(bm, args.class_reps)
+        reps = int(min(20000, max(args.class_reps, 20.0 / max(warm, 1e-4))))
+        cms = plan.time_class(bm, reps)
         k_rows = int(np.unique(t.arrays()["tile_colidx"]).size)
         b = alg_bytes(sb.rows, sb.nnz, s, k_rows, colB, s)
-        cls[bm] = {"ms": cms, "rows": sb.rows, "nnz": int(sb.nnz), "tiles": t.tilenum,
+        cls[bm] = {"ms": cms, "reps": reps, "rows": sb.rows, "nnz": int(sb.nnz), "tiles": t.tilenum,
                    "format": {1: "dense", 2: "packed"}.get(plan.get_format(bm), "?"),
                    "order": {0: "side-by-side", 1: "side-by-side", 2: "chunk-major"}[plan.get_variant(bm)[3]],
                    "tasks_per_wave": max(1, plan.get_variant(bm)[2]),
+                   "stages": max(1, plan.get_variant(bm)[1]),
                    "chunk_width": plan.get_variant(bm)[0] or default_width(hip, bm, prec, cbp),
                    "placement": {0: "contiguous", 1: "interleaved"}.get(plan.get_placement(bm), "?"),
                    "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9}
@@ -279,6 +340,20 @@ def main():
     dplan = tsp.Plan.from_csr(subs, A.rows, A.cols, cbp, prec, B)
     dev_tiles_ms = dplan.tile_ms
     dplan.close()
+
+    # after every other device measurement: the eviction copies must not
+    # disturb the class timings above
+    cold = None
+    if args.cold_reps > 0:
+        sb = step_bytes
+        cms, wms, cpms, cpb = cold_steps(hip, plan, args.cold_reps, sb)
+        cold = {"ms_per_step": round(cms, 6), "tflops": round(2.0 * A.nnz * colB / (cms * 1e-3) / 1e12, 4),
+                "alg_gbs": round(sb / (cms * 1e-3) / 1e9, 1), "warm_single_ms": round(wms, 6),
+                "copy_cold_ms": round(cpms, 6), "copy_cold_gbs": round(cpb / (cpms * 1e-3) / 1e9, 1),
+                "reps": args.cold_reps,
+                "protocol": "median of single steps, each after a 1 GB copy that evicts L2 and the 256 MB MALL; "
+                            "warm_single_ms: the same single step again right after; copy_cold: a plain copy "
+                            "moving the step's algorithmic bytes after the same eviction"}
 
     vendor = None
     if not args.no_vendor:
@@ -331,6 +406,7 @@ def main():
         "roofline": roof,
         "classes": {f"bm{k}": {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in cls.items()},
+        "cold_cache": cold,
         "vendor": vendor,
         "cpu_baseline": cpu,
         "pre_ms": {"split": round(split_ms, 1), "tiles_host": round(host_tiles_ms, 1),

@@ -210,9 +210,10 @@ int tsp_plan_get_placement(tsp_plan *plan, int bm);
 int tsp_plan_run(tsp_plan *plan, int zero_c);
 /* Clock-stabilising warmup (src/csr2tile.h:798-823 analogue). */
 int tsp_plan_warmup(tsp_plan *plan, int max_iters);
-/* Time `reps` back-to-back runs bracketed by events on the null stream. */
+/* Time `reps` back-to-back runs bracketed by events on the plan's main stream. */
 int tsp_plan_time(tsp_plan *plan, int reps, double *ms_per_iter);
-/* Time one class alone on its stream (reps launches). */
+/* Time one class alone (reps launches) on the stream a step launches it on:
+   its own stream, or the main stream when it is the plan's only class. */
 int tsp_plan_time_class(tsp_plan *plan, int bm, int reps, double *ms_per_launch);
 int tsp_plan_download_c(tsp_plan *plan, float *h_C);
 /* Device pointers of the plan (for external drivers). */

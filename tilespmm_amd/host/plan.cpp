@@ -470,11 +470,12 @@ extern "C" int tsp_plan_set_th(tsp_plan *p, int th64, int th16, int th8)
 
 // Fork from main (event ev0), `reps` launches per class on its own stream,
 // join back on main.
-static int fork_join(tsp_plan *p, int reps)
+// The class a plan launches alone, or nullptr when several classes have
+// tasks.  A plan with one active class launches it on the main stream: there
+// is nothing to overlap, and the cross-stream fork and join cost about a
+// microsecond per step on the small matrices.
+static ClassDev *only_class(tsp_plan *p)
 {
-    // a plan with one active class launches it on the main stream: there is
-    // nothing to overlap, and the cross-stream fork and join cost about a
-    // microsecond per step on the small matrices
     ClassDev *only = nullptr;
     int active = 0;
     for (ClassDev &c : p->cls)
@@ -482,7 +483,12 @@ static int fork_join(tsp_plan *p, int reps)
             ++active;
             only = &c;
         }
-    if (active == 1) {
+    return active == 1 ? only : nullptr;
+}
+
+static int fork_join(tsp_plan *p, int reps)
+{
+    if (ClassDev *only = only_class(p)) {
         for (int r = 0; r < reps; ++r) TSP_TRY(launch_class(p, *only, p->main));
         return TSP_OK;
     }
@@ -531,9 +537,13 @@ extern "C" int tsp_plan_time_class(tsp_plan *p, int bm, int reps, double *ms)
     for (ClassDev &x : p->cls)
         if (x.bm == bm) c = &x;
     if (!c || !c->active()) { *ms = 0.0; return TSP_OK; }
-    TSP_TRY(tsp_event_record(p->ev0, c->stream));
-    for (int r = 0; r < reps; ++r) TSP_TRY(launch_class(p, *c));
-    TSP_TRY(tsp_event_record(p->ev1, c->stream));
+    // on the stream a step launches the class on (launches of a few
+    // microseconds have timed up to twice as long on a class stream as on the
+    // main stream)
+    void *s = only_class(p) == c ? p->main : c->stream;
+    TSP_TRY(tsp_event_record(p->ev0, s));
+    for (int r = 0; r < reps; ++r) TSP_TRY(launch_class(p, *c, s));
+    TSP_TRY(tsp_event_record(p->ev1, s));
     TSP_TRY(tsp_event_sync(p->ev1));
     float t = 0.f;
     TSP_TRY(tsp_event_elapsed_ms(&t, p->ev0, p->ev1));
@@ -560,8 +570,9 @@ static int tune_time_class(tsp_plan *p, int bm, double *ms)
 }
 
 // MI355X additions to the runtime tuning, measured for one class with its
-// threshold fixed (each option timed on the class's own stream, best of two
-// interleaved rounds, so a drift of the clock cannot decide a pick):
+// threshold fixed (each option timed on the stream a step launches the class
+// on, best of two interleaved rounds, so a drift of the clock cannot decide a
+// pick):
 //   1. A format (dense tiles, or bitmap-packed: fewer bytes against a per-lane
 //      decode) x chunk order (chunks of one task side by side share A tiles in
 //      L2; chunk-major shrinks the live B working set per phase) x tasks per
