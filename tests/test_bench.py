@@ -1,0 +1,54 @@
+"""bench.py's one-line JSON contract: the fields the driver reads, their
+types and the relations between them (value from ms_per_step, roofline.frac
+from achieved / peak), and the refusal of more than one GPU."""
+import json
+import os
+import subprocess
+import sys
+
+import pytest
+
+from conftest import ROOT
+
+BENCH = os.path.join(ROOT, "bench.py")
+
+
+def test_bench_refuses_several_gpus():
+    r = subprocess.run([sys.executable, BENCH, "--gpus", "2"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
+
+
+@pytest.mark.gpu
+def test_bench_json_line(tsp):
+    if not tsp.device_available():
+        pytest.fail("no gfx950 device: GPU tests need an MI355X")
+    print("bench.py --config 1 --steps 20 --warmup 5", flush=True)
+    r = subprocess.run([sys.executable, "-u", BENCH, "--config", "1", "--steps", "20", "--warmup", "5",
+                        "--class-reps", "10", "--cold-reps", "3"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [l for l in r.stdout.splitlines() if l.strip()]
+    assert len(lines) == 1, r.stdout
+    d = json.loads(lines[0])
+    for k in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
+              "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
+        assert k in d, k
+    assert d["n_gpus"] == 1 and d["steps"] == 20 and d["warmup"] == 5
+    assert d["unit"] == "TFLOPS" and d["higher_is_better"] is True and d["vs_baseline"] is None
+    assert d["dtype"] == "fp16" and d["data"] == "synthetic" and "workload" in d["config"]
+    cfg = d["config"]
+    assert cfg["nnz"] == 32768 and cfg["colB"] == 32
+    # value is 2 nnz colB / step time
+    assert d["ms_per_step"] > 0
+    assert d["value"] == pytest.approx(2 * cfg["nnz"] * cfg["colB"] / (d["ms_per_step"] * 1e-3) / 1e12, rel=2e-3)
+    roof = d["roofline"]
+    for k in ("bound", "achieved", "peak", "unit", "frac", "traffic"):
+        assert k in roof, k
+    assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and roof["peak"] == 8000.0
+    assert roof["frac"] == pytest.approx(roof["achieved"] / roof["peak"], rel=1e-2, abs=1e-4)
+    cpu = d["cpu_baseline"]
+    for k in ("value", "unit", "cores", "kind", "sample"):
+        assert k in cpu, k
+    assert cpu["kind"] in ("port", "reference") and cpu["value"] > 0 and cpu["cores"] >= 1
+    cold = d["cold_cache"]
+    assert cold["reps"] == 3 and cold["ms_per_step"] > 0 and cold["copy_cold_ms"] > 0
