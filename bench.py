@@ -390,9 +390,12 @@ def main():
             _, used = oracle.spmm_f32_omp(r_end, A.rowptr[:r_end + 1], A.colidx, a32, b32, colB, out)
             times.append(time.perf_counter() - t1)
         tm = float(np.median(times))
+        nproc = len(os.sched_getaffinity(0))
         cpu = {"value": round(2.0 * nz * colB / tm / 1e12, 5), "unit": "TFLOPS", "cores": int(used), "kind": "port",
                "sample": f"rows 0..{r_end} ({nz} of {A.nnz} nnz), colB {colB}, fp32 accumulate, "
-                         f"OpenMP dynamic(64), median of 5 after 1 warmup, {tm * 1e3:.2f} ms"}
+                         f"OpenMP dynamic(64) on {used} threads ({nproc} cpus usable, "
+                         f"OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS', 'unset')}), "
+                         f"median of 5 after 1 warmup, {tm * 1e3:.2f} ms"}
 
     line = {
         "metric": "SpMM TFLOPS (2*nnz*colB/t) + % HBM roofline",

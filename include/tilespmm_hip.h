@@ -110,7 +110,8 @@ int tsp_stream_wait_event(void *stream, void *event);
  * rows of C that may be written (rows >= c_rows of a short last row-block are
  * skipped instead of relying on padding rows).  Asynchronous on `stream`;
  * returns the launch status.  C must be zeroed first when any task is split
- * (bit 31 of its row word). */
+ * (bit 31 of its row word); split tasks are added atomically, in any order of
+ * the schedule, as in the reference. */
 int tsp_spmm_launch(int bm, int prec, int rowblkblock, int colB_p,
                     const void *d_val, const unsigned *d_rows, const int *d_colstart,
                     const void *d_B, float *d_C, const int *d_colidx,
@@ -122,8 +123,11 @@ int tsp_spmm_launch(int bm, int prec, int rowblkblock, int colB_p,
  * tasks_per_wave (consecutive tasks one wave streams) and the order of the
  * column chunks (1: the chunks of one task range run side by side, 2:
  * chunk-major, every range of chunk 0 first).  Values <= 0 pick the defaults
- * tsp_spmm_launch uses.  No counterpart in the reference (its kernels have
- * one fixed shape per class). */
+ * tsp_spmm_launch uses.  With tasks_per_wave > 1 the tasks of a split
+ * row-block must be consecutive in the schedule (tsp_tile_pretreatment's
+ * always are): a wave that runs all of them stores their sum without
+ * atomics.  No counterpart in the reference (its kernels have one fixed
+ * shape per class). */
 int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p,
                             const void *d_val, const unsigned *d_rows, const int *d_colstart,
                             const void *d_B, float *d_C, const int *d_colidx,

@@ -248,6 +248,76 @@ def test_direct_kernel_boundary(gpu, orc):
         assert_close(out[:, :colB], Cref, Cabs, 0, f"direct v16 {place}")
 
 
+def test_split_tasks_in_any_order(gpu, orc):
+    """A split task (bit 31) is added atomically whatever the order of the
+    schedule, as in the reference: every row-block is cut in two pieces, all
+    first pieces come before all second pieces (tiles laid out in task
+    order), and tsp_switch_v8 / tsp_spmm_launch_placed (one task per wave)
+    still match the oracle."""
+    tsp = gpu
+    hip, _ = tsp.load()
+    rng = np.random.default_rng(12)
+    A = random_matrix(tsp, rng, 200, 400, 40, 0)
+    colB = 64
+    B, cbp = random_b(tsp, rng, A.cols, colB, 0)
+    sub = tsp.Csr(A.rows, A.cols, A.rowptr, A.colidx, A.val, 0)
+    sub.orig_row = np.arange(A.rows, dtype=np.int32)
+    t = tsp.tile_create(sub, A.cols, 8, 0)
+    arr = t.arrays()
+    tp, orig, bn = arr["tile_ptr"], arr["orig_tile_row_idx"], 16
+    first, second = [], []
+    for rb in range(len(tp) - 1):
+        t0, t1 = int(tp[rb]), int(tp[rb + 1])
+        if t1 - t0 >= 2:
+            mid = (t0 + t1) // 2
+            first.append((rb, t0, mid, True))
+            second.append((rb, mid, t1, True))
+        elif t1 > t0:
+            first.append((rb, t0, t1, False))
+    tasks = first + second
+    assert sum(sp for *_, sp in tasks) >= 20
+    perm = np.concatenate([np.arange(a, b) for _, a, b, _ in tasks])
+    rows = np.array([int(orig[rb]) | (0x80000000 if sp else 0) for rb, _, _, sp in tasks], dtype=np.uint32)
+    cs = np.concatenate([[0], np.cumsum([b - a for _, a, b, _ in tasks])]).astype(np.int32)
+    val = arr["dense"].reshape(t.tilenum, 8 * bn)[perm]
+    col = arr["tile_colidx"].reshape(t.tilenum, bn)[perm]
+    bufs = {}
+
+    def up(name, a):
+        a = np.ascontiguousarray(a)
+        p = C.c_void_p()
+        assert hip.tsp_malloc(C.byref(p), max(a.nbytes, 4)) == 0
+        assert hip.tsp_memcpy_h2d(p, a.ctypes.data_as(C.c_void_p), a.nbytes) == 0
+        bufs[name] = p
+
+    outs = []
+    try:
+        up("val", val); up("col", col); up("rows", rows); up("cs", cs); up("B", B)
+        Cz = np.zeros((A.rows, cbp), dtype=np.float32)
+        up("C", Cz)
+        for place in (None, 0, 1):
+            say(f"split tasks in any order: placement {place}")
+            assert hip.tsp_memcpy_h2d(bufs["C"], Cz.ctypes.data_as(C.c_void_p), Cz.nbytes) == 0
+            if place is None:
+                st = hip.tsp_switch_v8(0, len(rows), cbp, bufs["val"], bufs["rows"], bufs["cs"], bufs["B"],
+                                       bufs["C"], bufs["col"], A.rows, None)
+            else:
+                st = hip.tsp_spmm_launch_placed(8, 0, len(rows), cbp, bufs["val"], None, None, bufs["rows"],
+                                                bufs["cs"], bufs["B"], bufs["C"], bufs["col"], A.rows, None,
+                                                0, 0, 1, 0, place)
+            assert st == 0
+            assert hip.tsp_device_sync() == 0
+            out = np.zeros_like(Cz)
+            assert hip.tsp_memcpy_d2h(out.ctypes.data_as(C.c_void_p), bufs["C"], out.nbytes) == 0
+            outs.append(out)
+    finally:
+        for p in bufs.values():
+            hip.tsp_free(p)
+    Cref, Cabs = reference(orc, A, B, colB)
+    for place, out in zip(("switch", "contiguous", "interleaved"), outs):
+        assert_close(out[:, :colB], Cref, Cabs, 0, f"split tasks in any order, {place}")
+
+
 def test_edge_shapes(gpu, orc):
     tsp = gpu
     rng = np.random.default_rng(9)

@@ -12,10 +12,11 @@
 //     the wave streams them through one software pipeline that never drains
 //     at task boundaries; at a boundary it only flushes its accumulators to C
 //     and clears them.  Consecutive tasks of one split row-block keep
-//     accumulating; a flush is a plain vector store unless other waves also
-//     write the row-block, then fp32 atomics whose lanes cover whole rows
-//     (the slab is transposed through LDS first).  A 256-thread block runs
-//     four independent waves: there is no block barrier;
+//     accumulating.  A split task is flushed with fp32 atomics whose lanes
+//     cover whole rows (the slab is transposed through LDS first), unless
+//     the wave ran every task of its row-block; then, like an unsplit task,
+//     with plain vector stores.  A 256-thread block runs four independent
+//     waves: there is no block barrier;
 //   * S tiles are in flight per wave: the B row panel (BN rows x W columns,
 //     16-byte vector loads) and the A fragment of tile t+S are loaded while
 //     tile t is computed, and the column indices of tile t+2S (they feed the
@@ -282,13 +283,17 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
             dst[i] = *(const u4 *)(Bb + ((size_t)cid[i] * ld + col0 + pcol[i]) * sizeof(VT));
     };
     // Flush the accumulators of tasks first..last, which this wave ran back
-    // to back and which share one row-block.  A split row-block (bit 31)
-    // needs atomics unless this wave ran every task of it.
+    // to back and which share one row-block.  A split task (bit 31) is added
+    // atomically, as the reference does, whatever the order of the schedule.
+    // Only a group of several tasks of one split row-block may store: when
+    // the tasks just before and after the group belong to other row-blocks,
+    // this wave ran every task of it (a split row-block's tasks are
+    // consecutive, as tile_pretreatment emits them).
     auto flush = [&](int first, int last) {
         const unsigned rw = uload(rows, last);
         const int row0 = (int)(rw & 0x7fffffffu);
         bool split = (rw & 0x80000000u) != 0;
-        if (split) {
+        if (split && first < last) {
             const bool from_start = first == 0 || (int)(uload(rows, first - 1) & 0x7fffffffu) != row0;
             const bool to_end = last + 1 >= ntasks || (int)(uload(rows, last + 1) & 0x7fffffffu) != row0;
             split = !(from_start && to_end);
