@@ -208,7 +208,10 @@ def main():
                     help="pin the XCD placement per class 64,16,8 (1 contiguous, 2 interleaved, 0 keep)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-vendor", action="store_true")
-    ap.add_argument("--class-reps", type=int, default=200)
+    ap.add_argument("--class-reps", type=int, default=200,
+                    help="launches per class in the class-alone timing (at least)")
+    ap.add_argument("--class-min-ms", type=float, default=20.0,
+                    help="lengthen the class-alone timing to span at least this long")
     ap.add_argument("--cold-reps", type=int, default=50,
                     help="single steps timed after evicting L2 and MALL (0 skips)")
     ap.add_argument("--sweep", action="store_true", help="time every kernel variant per class instead")
@@ -302,9 +305,9 @@ def main():
         if t.tilenum == 0:
             continue
         # one untimed round first (the clock drops while the device idles),
-        # then enough launches to span at least 20 ms
+        # then enough launches to span at least --class-min-ms
         warm = plan.time_class(bm, args.class_reps)
-        reps = int(min(20000, max(args.class_reps, 20.0 / max(warm, 1e-4))))
+        reps = int(min(20000, max(args.class_reps, args.class_min_ms / max(warm, 1e-4))))
         cms = plan.time_class(bm, reps)
         k_rows = int(np.unique(t.arrays()["tile_colidx"]).size)
         b = alg_bytes(sb.rows, sb.nnz, s, k_rows, colB, s)
