@@ -198,14 +198,15 @@ int tsp_plan_set_variant(tsp_plan *plan, int bm, int w, int stages, int tasks_pe
 int tsp_plan_set_format(tsp_plan *plan, int bm, int fmt);
 int tsp_plan_get_format(tsp_plan *plan, int bm);
 /* The variant a class is pinned to (0 = library default), e.g. after
- * tsp_plan_tune picked the chunk order. */
+ * tsp_plan_tune picked the chunk width and order. */
 int tsp_plan_get_variant(tsp_plan *plan, int bm, int *w, int *stages, int *tasks_per_wave, int *order);
 /* Workgroup placement of one class on the XCDs (TSP_PLACE_CONTIGUOUS or
  * TSP_PLACE_INTERLEAVED, see tsp_spmm_launch_placed); tsp_plan_tune times
  * both.  get returns -1 on a bad argument. */
 int tsp_plan_set_placement(tsp_plan *plan, int bm, int placement);
 int tsp_plan_get_placement(tsp_plan *plan, int bm);
-/* Launch the three classes once (each on its own stream, joined on the null
+/* Launch the classes once (each on its own stream, forked from and joined on
+ * the plan's main stream; a plan with one class launches it on the main
  * stream).  zero_c != 0 clears C first. */
 int tsp_plan_run(tsp_plan *plan, int zero_c);
 /* Clock-stabilising warmup (src/csr2tile.h:798-823 analogue). */

@@ -497,7 +497,7 @@ __global__ __launch_bounds__(256) void copy_kernel(u4 *__restrict__ dst, const u
 // column indices prefetched S tiles ahead, more stages cost occupancy for no
 // gain), one task per wave and the chunks of a task range side by side.  The
 // plan's runtime tuning revisits the order, the tasks per wave, the XCD
-// placement and (8-row class) the chunk width per matrix.
+// placement and the chunk width per class.
 int default_chunk_width(int bm, int colB_p)
 {
     if (colB_p == 32) return 32;

@@ -581,8 +581,10 @@ static int tune_time_class(tsp_plan *p, int bm, double *ms)
 //   2. the two best of step 1 under both XCD placements (contiguous eighths
 //      keep neighbouring row-blocks, which share B rows, on one L2; runs dealt
 //      round-robin balance matrices whose heavy row-blocks sit together);
-//   3. for the 8-row class, 128-column chunks (half the waves, 256-byte fp16
-//      B row segments) against the default width.
+//   3. the other chunk widths (32, 64, 128 columns; 32 or 64 for 64-row
+//      tiles) against the default, each with both chunk orders: wider chunks
+//      mean fewer waves and longer B row segments, narrower ones a smaller B
+//      working set per wave and more waves (tf32 RMAT gains 11% at 32).
 // A class whose variant was pinned with tsp_plan_set_variant is left alone.
 static int tune_class(tsp_plan *p, ClassDev &c)
 {
@@ -647,19 +649,40 @@ static int tune_class(tsp_plan *p, ClassDev &c)
     c.var_tpw = pl[best].tpw == 1 ? 0 : pl[best].tpw;
     c.place = pl[best].place;
 
-    if (c.bm == 8 && k.cols_per_task != 128 && p->colB_p % 128 == 0) {
-        double ms[2] = {1e30, 1e30};
+    // 3. the other chunk widths, each with both chunk orders when it leaves
+    //    several chunks; format, tasks per wave and placement stay as kept
+    struct WOpt {
+        int w, order;
+    };
+    std::vector<WOpt> wo{{0, c.var_order}};
+    for (int w : {32, 64, 128}) {
+        if (w == k.cols_per_task || p->colB_p % w != 0 || (c.bm == 64 && w == 128)) continue;
+        if (p->colB_p / w >= 2) {
+            wo.push_back({w, 1});
+            wo.push_back({w, 2});
+        } else {
+            wo.push_back({w, 0});
+        }
+    }
+    if (wo.size() > 1) {
+        std::vector<double> wms(wo.size(), 1e30);
         for (int round = 0; round < 2; ++round)
-            for (int j = 0; j < 2; ++j) {
-                c.var_w = j ? 128 : 0;
+            for (size_t j = 0; j < wo.size(); ++j) {
+                c.var_w = wo[j].w;
+                c.var_order = wo[j].order;
                 double t = 0;
                 TSP_TRY(tune_time_class(p, c.bm, &t));
-                ms[j] = std::min(ms[j], t);
+                wms[j] = std::min(wms[j], t);
             }
-        c.var_w = ms[1] < ms[0] ? 128 : 0;
+        size_t bw = 0;
+        for (size_t j = 1; j < wo.size(); ++j)
+            if (wms[j] < wms[bw]) bw = j;
+        c.var_w = wo[bw].w;
+        c.var_order = wo[bw].order;
         if (log)
-            fprintf(stderr, "tune bm=%d chunk width default: %.5f ms, 128: %.5f ms%s\n", c.bm, ms[0], ms[1],
-                    c.var_w ? "  <- 128 kept" : "");
+            for (size_t j = 0; j < wo.size(); ++j)
+                fprintf(stderr, "tune bm=%d chunk width %d order=%d: %.5f ms%s\n", c.bm,
+                        wo[j].w ? wo[j].w : k.cols_per_task, wo[j].order, wms[j], j == bw ? "  <- kept" : "");
     }
     return TSP_OK;
 }
