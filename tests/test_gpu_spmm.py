@@ -359,14 +359,15 @@ def test_config_full_parity(gpu, orc, config):
 
 @pytest.mark.parametrize("config,prec,colB", [(4, -1, -1), (5, -1, -1), (3, 0, 128), (5, 0, 128)])
 def test_config_sampled_rows(gpu, orc, config, prec, colB):
-    """Large configurations: full GPU run, oracle on a row sample that includes
-    the heaviest rows and a uniform stride."""
+    """Large configurations: full GPU run with the runtime tuning (the variant
+    the bench ships), oracle on a row sample that includes the heaviest rows
+    and a uniform stride."""
     tsp = gpu
     say(f"config {config} prec {prec} colB {colB}: generating")
     A, B, colB, cbp = tsp.gen_config(config, prec, colB)
     g, d = tsp.predict(tsp.features(A, 9.5, colB), A.prec)
     say(f"config {config}: split+tiles+run gamma={g} delta={d}")
-    Cg, _ = run_tiles(tsp, A, B, cbp, g, d, tune=False, th=(32, 32, 32))
+    Cg, _ = run_tiles(tsp, A, B, cbp, g, d, tune=True)
     lens = np.diff(A.rowptr)
     rows = np.unique(np.concatenate([np.argsort(lens)[-64:], np.arange(0, A.rows, max(1, A.rows // 3000))]))
     Cref, Cabs = reference(orc, A, B, colB, rows)
