@@ -581,10 +581,11 @@ static int tune_time_class(tsp_plan *p, int bm, double *ms)
 //   2. the two best of step 1 under both XCD placements (contiguous eighths
 //      keep neighbouring row-blocks, which share B rows, on one L2; runs dealt
 //      round-robin balance matrices whose heavy row-blocks sit together);
-//   3. the other chunk widths (32, 64, 128 columns; 32 or 64 for 64-row
-//      tiles) against the default, each with both chunk orders: wider chunks
-//      mean fewer waves and longer B row segments, narrower ones a smaller B
-//      working set per wave and more waves (tf32 RMAT gains 11% at 32).
+//   3. every chunk width (32, 64, 128 columns; 32 or 64 for 64-row tiles),
+//      each with both chunk orders, under both placements: wider chunks mean
+//      fewer waves and longer B row segments, narrower ones a smaller B
+//      working set per wave and more waves (tf32 RMAT gains 11% at 32 when
+//      interleaved).  Step 2's choice stays unless another is 1% faster.
 // A class whose variant was pinned with tsp_plan_set_variant is left alone.
 static int tune_class(tsp_plan *p, ClassDev &c)
 {
@@ -649,27 +650,33 @@ static int tune_class(tsp_plan *p, ClassDev &c)
     c.var_tpw = pl[best].tpw == 1 ? 0 : pl[best].tpw;
     c.place = pl[best].place;
 
-    // 3. the other chunk widths, each with both chunk orders when it leaves
-    //    several chunks; format, tasks per wave and placement stay as kept
+    // 3. every chunk width, each with both chunk orders when it leaves
+    //    several chunks, under both placements (width and placement interact:
+    //    narrow chunks gain most when interleaved); format and tasks per wave
+    //    stay as kept
     struct WOpt {
-        int w, order;
+        int w, order, place;
     };
-    std::vector<WOpt> wo{{0, c.var_order}};
-    for (int w : {32, 64, 128}) {
-        if (w == k.cols_per_task || p->colB_p % w != 0 || (c.bm == 64 && w == 128)) continue;
-        if (p->colB_p / w >= 2) {
-            wo.push_back({w, 1});
-            wo.push_back({w, 2});
-        } else {
-            wo.push_back({w, 0});
+    std::vector<WOpt> wo;
+    for (int place = TSP_PLACE_CONTIGUOUS; place <= TSP_PLACE_INTERLEAVED; ++place) {
+        wo.push_back({0, c.var_order, place});
+        for (int w : {32, 64, 128}) {
+            if (w == k.cols_per_task || p->colB_p % w != 0 || (c.bm == 64 && w == 128)) continue;
+            if (p->colB_p / w >= 2) {
+                wo.push_back({w, 1, place});
+                wo.push_back({w, 2, place});
+            } else {
+                wo.push_back({w, 0, place});
+            }
         }
     }
-    if (wo.size() > 1) {
+    if (wo.size() > 2) {
         std::vector<double> wms(wo.size(), 1e30);
         for (int round = 0; round < 2; ++round)
             for (size_t j = 0; j < wo.size(); ++j) {
                 c.var_w = wo[j].w;
                 c.var_order = wo[j].order;
+                c.place = wo[j].place;
                 double t = 0;
                 TSP_TRY(tune_time_class(p, c.bm, &t));
                 wms[j] = std::min(wms[j], t);
@@ -677,12 +684,20 @@ static int tune_class(tsp_plan *p, ClassDev &c)
         size_t bw = 0;
         for (size_t j = 1; j < wo.size(); ++j)
             if (wms[j] < wms[bw]) bw = j;
+        // keep the step-2 choice unless another option is clearly faster
+        const WOpt keep{0, pl[best].order, pl[best].place};
+        size_t kj = 0;
+        for (size_t j = 0; j < wo.size(); ++j)
+            if (wo[j].w == 0 && wo[j].place == keep.place) kj = j;
+        if (wms[bw] > 0.99 * wms[kj]) bw = kj;
         c.var_w = wo[bw].w;
         c.var_order = wo[bw].order;
+        c.place = wo[bw].place;
         if (log)
             for (size_t j = 0; j < wo.size(); ++j)
-                fprintf(stderr, "tune bm=%d chunk width %d order=%d: %.5f ms%s\n", c.bm,
-                        wo[j].w ? wo[j].w : k.cols_per_task, wo[j].order, wms[j], j == bw ? "  <- kept" : "");
+                fprintf(stderr, "tune bm=%d chunk width %d order=%d placement=%s: %.5f ms%s\n", c.bm,
+                        wo[j].w ? wo[j].w : k.cols_per_task, wo[j].order,
+                        wo[j].place ? "interleaved" : "contiguous", wms[j], j == bw ? "  <- kept" : "");
     }
     return TSP_OK;
 }
