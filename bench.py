@@ -324,16 +324,24 @@ def main():
     step_bytes = alg_bytes(A.rows, A.nnz, s, k_all, colB, s)
     step_gbs = step_bytes / (ms * 1e-3) / 1e9
 
-    traffic = None
+    # the dominant kernel's instantiation spmm_kernel<BM, W, PREC, S, PK>; the
+    # profiled HBM traffic applies only to the same instantiation
+    dk = cls[dom]
+    kname = (f"spmm_kernel<{dom}, {dk['chunk_width']}, {prec}, {dk['stages']}, "
+             f"{'true' if dk['format'] == 'packed' else 'false'}>")
+    traffic, traffic_note = None, "no profile of this workload in profiles/"
     prof = os.path.join(ROOT, "profiles", f"traffic_config{args.config}_{'fp16' if prec == 0 else 'tf32'}_{colB}.json")
     if os.path.exists(prof):
         with open(prof) as fh:
-            tr = json.load(fh)
-        traffic = tr.get(f"bm{dom}", {}).get("hbm_bytes_per_launch")
+            tp = json.load(fh).get(f"bm{dom}", {})
+        if tp.get("kernel", "").endswith(kname):
+            traffic, traffic_note = tp.get("hbm_bytes_per_launch"), os.path.relpath(prof, ROOT)
+        else:
+            traffic_note = f"{os.path.relpath(prof, ROOT)} profiles {tp.get('kernel', '?')}, not the tuned {kname}"
 
     roof = {"bound": "hbm", "achieved": round(cls[dom]["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(cls[dom]["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": f"spmm_kernel<BM={dom}>", "kernel_ms": round(cls[dom]["ms"], 5),
+            "traffic_source": traffic_note, "kernel": kname, "kernel_ms": round(cls[dom]["ms"], 5),
             "alg_bytes_per_launch": cls[dom]["alg_bytes"],
             "step_achieved": round(step_gbs, 2), "step_frac": round(step_gbs / HBM_PEAK_GBS, 4),
             "step_alg_bytes": step_bytes}
