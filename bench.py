@@ -206,6 +206,8 @@ def main():
                     help="pin the pipeline depth per class 64,16,8 (1-4; 0 keep)")
     ap.add_argument("--place", type=ints3, default=None,
                     help="pin the XCD placement per class 64,16,8 (1 contiguous, 2 interleaved, 0 keep)")
+    ap.add_argument("--hot-bytes", type=int, default=None,
+                    help="pin the hot B row budget in bytes after tuning (0: no hot rows)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-vendor", action="store_true")
     ap.add_argument("--class-reps", type=int, default=200,
@@ -285,7 +287,10 @@ def main():
     for bm, pl in zip((64, 16, 8), args.place or ()):
         if pl:
             plan.set_placement(bm, pl - 1)
-    log(f"thresholds {th} (model {model_ms:.1f} ms, tuning {tune_ms:.1f} ms)")
+    if args.hot_bytes is not None:
+        plan.set_hot_rows(args.hot_bytes)
+    hot_n, hot_b = plan.get_hot_rows()
+    log(f"thresholds {th} (model {model_ms:.1f} ms, tuning {tune_ms:.1f} ms), hot B rows {hot_n} ({hot_b} bytes)")
 
     if args.sweep:
         sweep(plan, tiles, cbp, args)
@@ -416,6 +421,7 @@ def main():
         "config": {"workload": f"{NAMES[args.config]}, {'fp16' if prec == 0 else 'tf32'}, colB {colB}",
                    "config_id": args.config, "rows": A.rows, "nnz": A.nnz, "colB": colB, "colB_padded": cbp,
                    "gamma": g, "delta": d, "th": list(th), "tilenum": [t.tilenum for t in tiles],
+                   "hot_rows": hot_n, "hot_bytes": hot_b,
                    "parallelism": "single GPU"},
         "roofline": roof,
         "classes": {f"bm{k}": {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}

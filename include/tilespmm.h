@@ -205,6 +205,18 @@ int tsp_plan_get_variant(tsp_plan *plan, int bm, int *w, int *stages, int *tasks
  * both.  get returns -1 on a bad argument. */
 int tsp_plan_set_placement(tsp_plan *plan, int bm, int placement);
 int tsp_plan_get_placement(tsp_plan *plan, int bm);
+/* Hot B rows (see tsp_hot_rows_gather): copy the most-gathered B rows, at
+ * most budget_bytes of them (and at most TSP_HOT_MAX_BYTES), into spare rows
+ * of the plan's B and point every class's tile columns at the copies; every
+ * step then re-copies them before the class kernels run.  Only columns
+ * gathered at least TSP_HOT_MIN_GATHERS times qualify.  budget_bytes 0
+ * restores the canonical column indices.  tsp_plan_tune times a few budgets
+ * (0 among them) and keeps the fastest.  get: the current slot count and
+ * bytes.  No counterpart in the reference. */
+#define TSP_HOT_MAX_BYTES (32LL << 20)
+#define TSP_HOT_MIN_GATHERS 4
+int tsp_plan_set_hot_rows(tsp_plan *plan, long long budget_bytes);
+int tsp_plan_get_hot_rows(tsp_plan *plan, int *nhot, long long *bytes);
 /* Launch the classes once (each on its own stream, forked from and joined on
  * the plan's main stream; a plan with one class launches it on the main
  * stream).  zero_c != 0 clears C first. */

@@ -199,6 +199,31 @@ int tsp_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
 int tsp_gather_kernel(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed,
                       void *sink, void *stream);
 
+/* ---- Hot B rows ------------------------------------------------------------
+ * B is allocated with spare rows after row colA; hot slot s is row colA + s
+ * and holds a copy of B row hot[s].  A tile column index colA + s then reads
+ * the copy.  Copying the most-gathered rows of a skewed matrix into
+ * consecutive rows spreads their cache lines over every L2 and memory
+ * channel.  No counterpart in the reference (it gathers every row from its
+ * place in B).
+ *
+ * tsp_colidx_count: counts[c] += number of entries of d_colidx[n] naming
+ *   column c (entries >= colA are first decoded through d_hot[nhot]).
+ *   d_counts[colA] must be zeroed by the caller.
+ * tsp_colidx_remap: d_colidx[i] = map[decode(d_colidx[i])], where decode
+ *   undoes an earlier remap through d_old_hot[old_nhot] and d_map[colA] names
+ *   each column's new index (itself or colA + slot); d_map NULL restores the
+ *   canonical column indices.
+ * tsp_hot_rows_gather: rows colA + s = rows d_hot[s] of d_B (row_bytes per
+ *   row, a multiple of 16), s < nhot; d_B must hold colA + nhot rows.
+ * All three are asynchronous on `stream`. */
+int tsp_colidx_count(const int *d_colidx, long long n, int colA, const int *d_hot, int nhot,
+                     unsigned *d_counts, void *stream);
+int tsp_colidx_remap(int *d_colidx, long long n, int colA, const int *d_old_hot, int old_nhot,
+                     const int *d_map, void *stream);
+int tsp_hot_rows_gather(void *d_B, int colA, long long row_bytes, const int *d_hot, int nhot,
+                        void *stream);
+
 /* ---- CSR -> tiles on the device ------------------------------------------
  * Device counterpart of Tile_create (src/csr2tile.h:724-795, convert_step1-3
  * at :15-379) producing the same arrays as the host tsp_tile_create, bit for

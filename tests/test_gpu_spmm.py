@@ -372,3 +372,108 @@ def test_config_sampled_rows(gpu, orc, config, prec, colB):
     rows = np.unique(np.concatenate([np.argsort(lens)[-64:], np.arange(0, A.rows, max(1, A.rows // 3000))]))
     Cref, Cabs = reference(orc, A, B, colB, rows)
     assert_close(Cg[rows, :colB], Cref, Cabs, A.prec, f"config {config} sampled")
+
+
+def skewed_matrix(tsp, rng, rows, cols, maxlen, prec):
+    """Rows of random length whose columns follow an RMAT-like marginal:
+    each bit of the column index is set with probability 0.24, so columns
+    with few set bits are gathered far more often than the rest."""
+    bits = int(np.log2(cols))
+    lens = rng.integers(0, maxlen + 1, rows)
+    rp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    ci = []
+    for ln in lens:
+        draw = (rng.random((4 * int(ln) + 8, bits)) < 0.24).astype(np.int64) @ (1 << np.arange(bits))
+        ci.append(np.unique(draw)[: int(ln)])
+    lens = np.array([len(c) for c in ci])
+    rp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    ci = np.concatenate(ci).astype(np.int32)
+    v = rng.uniform(-1, 1, rp[-1]).astype(np.float32)
+    val = v.astype(np.float16).view(np.uint16) if prec == 0 else v
+    return tsp.Csr(rows, cols, rp, ci, val, prec)
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+def test_hot_rows_bit_identical(gpu, orc, prec):
+    """Hot B rows (copies of the most-gathered rows in spare rows of B) leave
+    C bit-identical to the plan without them: the kernels multiply the same
+    values in the same order.  Budgets change in sequence, so slot indices of
+    one selection are decoded before the next is applied; one plan has every
+    class (fork/join path), one a single class; B changes between steps."""
+    tsp = gpu
+    rng = np.random.default_rng(77 + prec)
+    A = skewed_matrix(tsp, rng, 3000, 4096, 60, prec)
+    for colB in (32, 128):
+        B, cbp = random_b(tsp, rng, A.cols, colB, prec)
+        Cref, Cabs = reference(orc, A, B, colB)
+        unsplit = (1 << 20,) * 3        # no split tasks: no atomics, so C is reproducible bit for bit
+        for g, d in [(2.0, 1.5), (5.0, 3.0)]:
+            base, _ = run_tiles(tsp, A, B, cbp, g, d, unsplit)
+            assert_close(base[:, :colB], Cref, Cabs, prec, f"no hot rows colB={colB} g={g}")
+            subs = tsp.matrix_split(A, g, d)
+            tiles = [tsp.tile_create(s, A.cols, bm, A.prec) for s, bm in zip(subs, (64, 16, 8))]
+            plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, A.prec, B)
+            try:
+                rb = cbp * (2 if prec == 0 else 4)
+                for budget in (rb, 4096, 1 << 20, 0, 32 << 20, 64 * rb):
+                    say(f"hot rows prec={prec} colB={colB} g={g} d={d} budget={budget}")
+                    plan.set_th(*unsplit)
+                    plan.set_hot_rows(budget)
+                    n, nb = plan.get_hot_rows()
+                    assert nb == n * rb and nb <= max(budget, 0) and (budget == 0) == (n == 0)
+                    plan.run(zero_c=True)
+                    Cg = plan.download_c()
+                    assert np.array_equal(Cg.view(np.uint32), base.view(np.uint32)), f"budget {budget}"
+                    # hot rows are re-copied every step
+                    plan.time(3)
+                    plan.run(zero_c=True)
+                    assert np.array_equal(plan.download_c().view(np.uint32), base.view(np.uint32))
+                    # split tasks (atomic flushes) read the same slots
+                    plan.set_th(8, 8, 8)
+                    plan.run(zero_c=True)
+                    assert_close(plan.download_c()[:, :colB], Cref, Cabs, prec, f"split, budget {budget}")
+            finally:
+                plan.close()
+
+
+def test_hot_row_device_helpers(gpu):
+    """tsp_colidx_count / tsp_colidx_remap / tsp_hot_rows_gather against numpy."""
+    tsp = gpu
+    hip = tsp.load()[0]
+    rng = np.random.default_rng(5)
+    colA, n, rb = 1000, 50000, 48
+    ci = (rng.pareto(1.2, n) * 20).astype(np.int64) % colA
+    ci = ci.astype(np.int32)
+    hot = np.sort(rng.choice(colA, 37, replace=False)).astype(np.int32)
+    mp = np.arange(colA, dtype=np.int32)
+    mp[hot] = colA + np.arange(len(hot), dtype=np.int32)
+    Bh = rng.integers(0, 2 ** 32, (colA + len(hot)) * rb // 4, dtype=np.uint64).astype(np.uint32)
+    bufs = {k: tsp._DevBuf(v) for k, v in
+            dict(ci=ci, hot=hot, mp=mp, cnt=np.zeros(colA, np.uint32), B=Bh).items()}
+    try:
+        P = lambda k: bufs[k].p
+        get = lambda k, m, dt: tsp._d2h(bufs[k].p, m, dt)
+        assert hip.tsp_colidx_count(P("ci"), n, colA, None, 0, P("cnt"), None) == 0
+        assert hip.tsp_device_sync() == 0
+        assert np.array_equal(get("cnt", colA, np.uint32), np.bincount(ci, minlength=colA))
+        assert hip.tsp_colidx_remap(P("ci"), n, colA, None, 0, P("mp"), None) == 0
+        assert hip.tsp_device_sync() == 0
+        assert np.array_equal(get("ci", n, np.int32), mp[ci])
+        # counting decodes remapped entries
+        hip.tsp_memset(P("cnt"), 0, colA * 4)
+        assert hip.tsp_colidx_count(P("ci"), n, colA, P("hot"), len(hot), P("cnt"), None) == 0
+        assert hip.tsp_device_sync() == 0
+        assert np.array_equal(get("cnt", colA, np.uint32), np.bincount(ci, minlength=colA))
+        assert hip.tsp_colidx_remap(P("ci"), n, colA, P("hot"), len(hot), None, None) == 0
+        assert hip.tsp_device_sync() == 0
+        assert np.array_equal(get("ci", n, np.int32), ci)
+        assert hip.tsp_hot_rows_gather(P("B"), colA, rb, P("hot"), len(hot), None) == 0
+        assert hip.tsp_device_sync() == 0
+        got = get("B", Bh.size, np.uint32).reshape(colA + len(hot), rb // 4)
+        want = Bh.reshape(colA + len(hot), rb // 4).copy()
+        want[colA:] = want[hot]
+        assert np.array_equal(got, want)
+        assert hip.tsp_hot_rows_gather(P("B"), colA, 40, P("hot"), len(hot), None) != 0   # not 16-byte rows
+    finally:
+        for b in bufs.values():
+            b.free()

@@ -170,6 +170,9 @@ HIP_SYMBOLS = {
                                   C.POINTER(C.c_double)]),
     "tsp_copy_kernel": (C.c_int, [_P, _P, C.c_size_t, _P]),
     "tsp_gather_kernel": (C.c_int, [_P, C.c_size_t, C.c_int, C.c_int, C.c_uint, _P, _P]),
+    "tsp_colidx_count": (C.c_int, [_P, C.c_longlong, C.c_int, _P, C.c_int, _P, _P]),
+    "tsp_colidx_remap": (C.c_int, [_P, C.c_longlong, C.c_int, _P, C.c_int, _P, _P]),
+    "tsp_hot_rows_gather": (C.c_int, [_P, C.c_int, C.c_longlong, _P, C.c_int, _P]),
     "tsp_tile_create_device": (C.c_int, [C.POINTER(DevTiles), C.c_int, C.c_int, C.c_longlong, _P, _P, _P,
                                          C.c_int, C.c_int, C.c_int, _P]),
     "tsp_dev_tiles_free": (C.c_int, [C.POINTER(DevTiles)]),
@@ -219,6 +222,8 @@ HOST_SYMBOLS = {
     "tsp_plan_get_variant": (C.c_int, [_P, C.c_int, _IP, _IP, _IP, _IP]),
     "tsp_plan_set_placement": (C.c_int, [_P, C.c_int, C.c_int]),
     "tsp_plan_get_placement": (C.c_int, [_P, C.c_int]),
+    "tsp_plan_set_hot_rows": (C.c_int, [_P, C.c_longlong]),
+    "tsp_plan_get_hot_rows": (C.c_int, [_P, _IP, C.POINTER(C.c_longlong)]),
     "tsp_plan_run": (C.c_int, [_P, C.c_int]),
     "tsp_plan_warmup": (C.c_int, [_P, C.c_int]),
     "tsp_plan_time": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double)]),
@@ -632,6 +637,17 @@ class Plan:
 
     def get_placement(self, bm: int) -> int:
         return load()[1].tsp_plan_get_placement(self.p, bm)
+
+    def set_hot_rows(self, budget_bytes: int):
+        """Copy the most-gathered B rows (at most budget_bytes) into spare rows
+        of B before every step; 0 restores the canonical column indices."""
+        _check("tsp_plan_set_hot_rows", load()[1].tsp_plan_set_hot_rows(self.p, int(budget_bytes)))
+
+    def get_hot_rows(self):
+        """(hot slots, bytes) currently copied per step."""
+        n, b = C.c_int(), C.c_longlong()
+        _check("tsp_plan_get_hot_rows", load()[1].tsp_plan_get_hot_rows(self.p, C.byref(n), C.byref(b)))
+        return n.value, b.value
 
     def run(self, zero_c: bool = True):
         _check("tsp_plan_run", load()[1].tsp_plan_run(self.p, int(zero_c)))

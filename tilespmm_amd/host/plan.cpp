@@ -62,7 +62,11 @@ double now_ms()
 // launch pays an implicit null-stream synchronisation.
 struct tsp_plan {
     int dev = 0, prec = 0, rowA = 0, colA = 0, colB_p = 0;
-    void *d_B = nullptr;
+    void *d_B = nullptr;          // colA rows of B, then hot_cap spare rows for hot-row copies
+    int hot_cap = 0;              // spare rows after row colA
+    int nhot = 0;                 // hot slots in use: row colA + s copies B row d_hot[s]
+    int *d_hot = nullptr;
+    std::vector<unsigned> col_gathers;   // gathers per column over every class (canonical indices)
     float *d_C = nullptr;
     ClassDev cls[3];
     void *main = nullptr;
@@ -277,6 +281,7 @@ extern "C" int tsp_plan_destroy(tsp_plan *p)
         if (c.dev_built) tsp_tile_destroy(&c.own);
     }
     tsp_free(p->d_B);
+    tsp_free(p->d_hot);
     tsp_free(p->d_C);
     tsp_event_destroy(p->ev0);
     tsp_event_destroy(p->ev1);
@@ -302,7 +307,12 @@ static int plan_begin(std::unique_ptr<tsp_plan> &p, int device_id, int rowA, int
     TSP_TRY(tsp_stream_create_nonblocking(&p->main));
     const size_t vs = tsph::val_size(prec);
     const size_t bbytes = vs * (size_t)colA * colB_p, cbytes = sizeof(float) * (size_t)rowA * colB_p;
-    TSP_TRY(tsp_malloc(&p->d_B, bbytes));
+    // spare rows for hot-row copies (tsp_plan_set_hot_rows); slot indices
+    // colA + s must stay valid int column indices
+    const long long row_bytes = (long long)vs * colB_p;
+    p->hot_cap = (int)std::min<long long>({(long long)colA, TSP_HOT_MAX_BYTES / row_bytes, 0x7fffffffLL - colA});
+    TSP_TRY(tsp_malloc(&p->d_B, bbytes + (size_t)row_bytes * p->hot_cap));
+    if (p->hot_cap > 0) TSP_TRY(tsp_malloc((void **)&p->d_hot, sizeof(int) * (size_t)p->hot_cap));
     TSP_TRY(tsp_malloc((void **)&p->d_C, cbytes));
     if (h_B) TSP_TRY(tsp_memcpy_h2d(p->d_B, h_B, bbytes));
     return tsp_memset(p->d_C, 0, cbytes);
@@ -486,7 +496,15 @@ static ClassDev *only_class(tsp_plan *p)
     return active == 1 ? only : nullptr;
 }
 
-static int fork_join(tsp_plan *p, int reps)
+static long long b_row_bytes(const tsp_plan *p) { return (long long)tsph::val_size(p->prec) * p->colB_p; }
+
+// Copy the hot B rows into their slots (on main, ahead of the class kernels).
+static int hot_gather(tsp_plan *p)
+{
+    return p->nhot ? tsp_hot_rows_gather(p->d_B, p->colA, b_row_bytes(p), p->d_hot, p->nhot, p->main) : TSP_OK;
+}
+
+static int fork_join_once(tsp_plan *p, int reps)
 {
     if (ClassDev *only = only_class(p)) {
         for (int r = 0; r < reps; ++r) TSP_TRY(launch_class(p, *only, p->main));
@@ -501,6 +519,90 @@ static int fork_join(tsp_plan *p, int reps)
         TSP_TRY(tsp_event_record(p->done[i], c.stream));
         TSP_TRY(tsp_stream_wait_event(p->main, p->done[i]));
     }
+    return TSP_OK;
+}
+
+// `reps` steps.  With hot rows every step first re-copies them (B may have
+// changed since the last step), and the class kernels of one step finish
+// before the next step's copy rewrites the slots they read.
+static int fork_join(tsp_plan *p, int reps)
+{
+    if (!p->nhot) return fork_join_once(p, reps);
+    for (int r = 0; r < reps; ++r) {
+        TSP_TRY(hot_gather(p));
+        TSP_TRY(fork_join_once(p, 1));
+    }
+    return TSP_OK;
+}
+
+// Gathers per column over every class's tile column indices (what each
+// kernel launch reads from B), counted once on the canonical indices.
+static int count_gathers(tsp_plan *p)
+{
+    if (!p->col_gathers.empty() || p->colA == 0) return TSP_OK;
+    unsigned *d_cnt = nullptr;
+    TSP_TRY(tsp_malloc((void **)&d_cnt, sizeof(unsigned) * (size_t)p->colA));
+    std::unique_ptr<void, int (*)(void *)> guard(d_cnt, tsp_free);
+    TSP_TRY(tsp_memset(d_cnt, 0, sizeof(unsigned) * (size_t)p->colA));
+    for (ClassDev &c : p->cls)
+        if (c.active())
+            TSP_TRY(tsp_colidx_count(c.d_colidx, (long long)c.m->tilenum * c.m->bn, p->colA, p->d_hot, p->nhot,
+                                     d_cnt, p->main));
+    TSP_TRY(tsp_stream_sync(p->main));
+    p->col_gathers.resize((size_t)p->colA);
+    return tsp_memcpy_d2h(p->col_gathers.data(), d_cnt, sizeof(unsigned) * (size_t)p->colA);
+}
+
+extern "C" int tsp_plan_set_hot_rows(tsp_plan *p, long long budget_bytes)
+{
+    if (!p || budget_bytes < 0) return TSP_EINVAL;
+    const long long rb = b_row_bytes(p);
+    const long long want = std::min<long long>(p->hot_cap, std::min(budget_bytes, TSP_HOT_MAX_BYTES) / rb);
+    std::vector<int> hot;
+    if (want > 0) {
+        TSP_TRY(count_gathers(p));
+        std::vector<int> cand;
+        for (int col = 0; col < p->colA; ++col)
+            if (p->col_gathers[(size_t)col] >= TSP_HOT_MIN_GATHERS) cand.push_back(col);
+        if ((long long)cand.size() > want) {
+            const auto more = [&](int a, int b) {
+                const unsigned ga = p->col_gathers[(size_t)a], gb = p->col_gathers[(size_t)b];
+                return ga != gb ? ga > gb : a < b;
+            };
+            std::nth_element(cand.begin(), cand.begin() + want, cand.end(), more);
+            cand.resize((size_t)want);
+        }
+        std::sort(cand.begin(), cand.end());
+        hot.swap(cand);
+    }
+    // kernels of an earlier run may still read the column indices and slots
+    TSP_TRY(tsp_device_sync());
+    int *d_map = nullptr;
+    std::unique_ptr<void, int (*)(void *)> guard(nullptr, tsp_free);
+    if (!hot.empty()) {
+        std::vector<int> map((size_t)p->colA);
+        for (int col = 0; col < p->colA; ++col) map[(size_t)col] = col;
+        for (size_t s = 0; s < hot.size(); ++s) map[(size_t)hot[s]] = p->colA + (int)s;
+        TSP_TRY(tsp_malloc((void **)&d_map, sizeof(int) * (size_t)p->colA));
+        guard.reset(d_map);
+        TSP_TRY(tsp_memcpy_h2d(d_map, map.data(), sizeof(int) * (size_t)p->colA));
+    }
+    for (ClassDev &c : p->cls)
+        if (c.active())
+            TSP_TRY(tsp_colidx_remap(c.d_colidx, (long long)c.m->tilenum * c.m->bn, p->colA, p->d_hot, p->nhot,
+                                     d_map, p->main));
+    TSP_TRY(tsp_stream_sync(p->main));
+    p->nhot = (int)hot.size();
+    if (p->nhot) TSP_TRY(tsp_memcpy_h2d(p->d_hot, hot.data(), sizeof(int) * hot.size()));
+    TSP_TRY(hot_gather(p));
+    return tsp_stream_sync(p->main);
+}
+
+extern "C" int tsp_plan_get_hot_rows(tsp_plan *p, int *nhot, long long *bytes)
+{
+    if (!p) return TSP_EINVAL;
+    if (nhot) *nhot = p->nhot;
+    if (bytes) *bytes = (long long)p->nhot * b_row_bytes(p);
     return TSP_OK;
 }
 
@@ -541,6 +643,10 @@ extern "C" int tsp_plan_time_class(tsp_plan *p, int bm, int reps, double *ms)
     // microseconds have timed up to twice as long on a class stream as on the
     // main stream)
     void *s = only_class(p) == c ? p->main : c->stream;
+    if (p->nhot) {                   // slots valid before the class runs alone
+        TSP_TRY(hot_gather(p));
+        TSP_TRY(tsp_stream_sync(p->main));
+    }
     TSP_TRY(tsp_event_record(p->ev0, s));
     for (int r = 0; r < reps; ++r) TSP_TRY(launch_class(p, *c, s));
     TSP_TRY(tsp_event_record(p->ev1, s));
@@ -702,6 +808,56 @@ static int tune_class(tsp_plan *p, ClassDev &c)
     return TSP_OK;
 }
 
+// One tuning measurement of whole steps: a warm-up step, then enough steps to
+// span about 2 ms (at least 3, at most 200).
+static int tune_time_step(tsp_plan *p, double *ms)
+{
+    double warm = 0;
+    TSP_TRY(tsp_plan_time(p, 1, &warm));
+    const int reps = (int)std::min(200.0, std::max(3.0, 2.0 / std::max(warm, 1e-4)));
+    return tsp_plan_time(p, reps, ms);
+}
+
+// Hot B rows: whole steps timed with no hot rows and with 4, 8, 16 and 32 MB
+// of them (budgets that select the same rows are timed once), best of two
+// interleaved rounds; a budget is kept only if it beats no hot rows by 2%.
+// Run before the threshold and class tuning (with the model's thresholds and
+// default variants) and again after it.
+// TSP_HOT_BYTES=<bytes> pins the budget instead.
+static int tune_hot_rows(tsp_plan *p, int tune)
+{
+    if (p->hot_cap == 0) return TSP_OK;
+    if (const char *env = getenv("TSP_HOT_BYTES")) return tsp_plan_set_hot_rows(p, atoll(env));
+    if (!tune) return TSP_OK;
+    TSP_TRY(count_gathers(p));
+    long long ncand = 0;
+    for (unsigned g : p->col_gathers) ncand += g >= TSP_HOT_MIN_GATHERS;
+    const long long rb = b_row_bytes(p);
+    std::vector<long long> slots{0};
+    for (long long mb : {4, 8, 16, 32}) {
+        const long long n = std::min<long long>({(long long)p->hot_cap, (mb << 20) / rb, ncand});
+        if (n > slots.back()) slots.push_back(n);
+    }
+    if (slots.size() < 2) return TSP_OK;
+    std::vector<double> best(slots.size(), 1e30);
+    for (int round = 0; round < 2; ++round)
+        for (size_t j = 0; j < slots.size(); ++j) {
+            TSP_TRY(tsp_plan_set_hot_rows(p, slots[j] * rb));
+            double ms = 0;
+            TSP_TRY(tune_time_step(p, &ms));
+            best[j] = std::min(best[j], ms);
+        }
+    size_t bj = 0;
+    for (size_t j = 1; j < slots.size(); ++j)
+        if (best[j] < best[bj]) bj = j;
+    if (best[bj] > 0.98 * best[0]) bj = 0;
+    if (getenv("TSP_TUNE_LOG"))
+        for (size_t j = 0; j < slots.size(); ++j)
+            fprintf(stderr, "tune hot rows %lld (%.1f MB): %.5f ms%s\n", slots[j], slots[j] * rb / 1048576.0, best[j],
+                    j == bj ? "  <- kept" : "");
+    return tsp_plan_set_hot_rows(p, slots[bj] * rb);
+}
+
 extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model_ms, double *tune_ms)
 {
     if (!p) return TSP_EINVAL;
@@ -725,6 +881,7 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
     int best[3] = {opts[0][0], opts[1][0], opts[2][0]};
     TSP_TRY(tsp_plan_set_th(p, best[0], best[1], best[2]));
     double t2 = now_ms(), t3 = t2;
+    TSP_TRY(tune_hot_rows(p, tune));
     const size_t combos = opts[0].size() * opts[1].size() * opts[2].size();
     if (tune && combos > 1) {
         double best_ms = 1e30;
@@ -745,6 +902,9 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
     }
     if (tune) {
         for (ClassDev &c : p->cls) TSP_TRY(tune_class(p, c));
+        // the class variants change how much the hot rows save: time the
+        // budgets again with the tuned variants
+        TSP_TRY(tune_hot_rows(p, tune));
         t3 = now_ms();
     }
     if (tune_ms) *tune_ms = t3 - t2;
