@@ -4,11 +4,15 @@ roofline for one synthetic configuration, on one GPU.
 A step is one full tiled SpMM C = A*B (the row-block class kernels, each on
 its own stream, forked from and joined on the plan's main stream; a plan
 with one class launches it on the main stream) with A's tiles, the schedule,
-B and C already resident in HBM.  Default workload: configuration 2
-(5-point Laplacian 512x512, fp16, colB 128).  Prints ONE JSON line.
+B and C already resident in HBM.  Default workload: configuration 5 as
+stated (RMAT scale 22, tf32, colB 64), the largest single-GPU configuration;
+the fp16 / colB 128 targets on the configuration 3 and 5 structures (T3, T5)
+are timed in the same run and reported under "targets".  Prints ONE JSON
+line.
 
   python bench.py [--steps K] [--warmup W] [--config 1..5] [--prec fp16|tf32]
-                  [--colB N] [--no-cpu] [--no-vendor] [--cold-reps N] [--gpus 1]
+                  [--colB N] [--targets 3,5] [--no-cpu] [--no-vendor]
+                  [--cold-reps N] [--gpus 1]
 """
 import argparse
 import json
@@ -157,11 +161,11 @@ def default_width(hip, bm, prec, cbp):
     return k.cols_per_task
 
 
-def sweep(plan, tiles, cbp, args):
+def sweep(plan, tilenum, cbp, args):
     """Time every kernel variant (chunk width W, pipeline stages S, tasks per
     wave) of each active class; one JSON line per class."""
-    for t, bm in zip(tiles, (64, 16, 8)):
-        if t.tilenum == 0:
+    for tn, bm in zip(tilenum, (64, 16, 8)):
+        if tn == 0:
             continue
         widths = [w for w in ((32, 64) if bm == 64 else (32, 64, 128)) if cbp % w == 0]
         res = {}
@@ -176,9 +180,279 @@ def sweep(plan, tiles, cbp, args):
                         res[f"w{w}_s{s}_t{tpw}_o{order}"] = plan.time_class(bm, args.class_reps)
         plan.set_variant(bm)
         best = min(res, key=res.get)
-        print(json.dumps({"sweep": args.config, "bm": bm, "tiles": t.tilenum, "best": best,
+        print(json.dumps({"sweep": args.config, "bm": bm, "tiles": tn, "best": best,
                           "best_ms": round(res[best], 5), "default_ms": round(res["default"], 5),
                           "ms": {k: round(v, 5) for k, v in res.items()}}), flush=True)
+
+
+def gather_ceiling(hip, reps=5):
+    """Uniform random 128-byte row gathers from a 1 GB table: the line-request
+    rate (G lines/s) that the B-row gathers of a uniform-column matrix can
+    reach, measured in the same process as the headline."""
+    import ctypes as C
+    nb = 1 << 30
+    tab, sink = C.c_void_p(), C.c_void_p()
+    if hip.tsp_malloc(C.byref(tab), nb) or hip.tsp_malloc(C.byref(sink), 8192 * 256 * 4):
+        raise SystemExit("bench.py: cannot allocate the gather probe")
+    try:
+        hip.tsp_memset(tab, 1, nb)
+        e0, e1 = C.c_void_p(), C.c_void_p()
+        hip.tsp_event_create(C.byref(e0))
+        hip.tsp_event_create(C.byref(e1))
+        iters = 64
+        for w in range(2):
+            hip.tsp_gather_kernel(tab, nb, 128, iters, w, sink, None)
+        hip.tsp_event_record(e0, None)
+        for r in range(reps):
+            hip.tsp_gather_kernel(tab, nb, 128, iters, 10 + r, sink, None)
+        hip.tsp_event_record(e1, None)
+        hip.tsp_event_sync(e1)
+        ms = C.c_float()
+        hip.tsp_event_elapsed_ms(C.byref(ms), e0, e1)
+        hip.tsp_event_destroy(e0)
+        hip.tsp_event_destroy(e1)
+    finally:
+        hip.tsp_free(tab)
+        hip.tsp_free(sink)
+    lines = 8192 * 256 * 16 * iters / 128
+    return lines / (ms.value / reps * 1e-3) / 1e9
+
+
+def apply_pins(plan, args):
+    """--th / --format / --order / --tpw / --width / --stages / --place /
+    --hot-bytes pin what the tuning chose (profiling runs replay a tuned
+    configuration with --no-tune)."""
+    th = None
+    if args.th:
+        plan.set_th(*args.th)
+        th = tuple(args.th)
+    for bm, f in zip((64, 16, 8), args.format or ()):
+        if f:
+            plan.set_format(bm, f)
+    for bm, o in zip((64, 16, 8), args.order or ()):
+        if o:
+            w, st, tpw, _ = plan.get_variant(bm)
+            plan.set_variant(bm, w, st, tpw, o)
+    for bm, n in zip((64, 16, 8), args.tpw or ()):
+        if n:
+            w, st, _, o = plan.get_variant(bm)
+            plan.set_variant(bm, w, st, n, o)
+    for bm, wd in zip((64, 16, 8), args.width or ()):
+        if wd:
+            _, st, n, o = plan.get_variant(bm)
+            plan.set_variant(bm, wd, st, n, o)
+    for bm, sg in zip((64, 16, 8), args.stages or ()):
+        if sg:
+            wd, _, n, o = plan.get_variant(bm)
+            plan.set_variant(bm, wd, sg, n, o)
+    for bm, pl in zip((64, 16, 8), args.place or ()):
+        if pl:
+            plan.set_placement(bm, pl - 1)
+    if args.hot_bytes is not None:
+        plan.set_hot_rows(args.hot_bytes)
+    return th
+
+
+def pins_of(plan, th, cls):
+    """The bench flags that replay this plan's tuned configuration."""
+    f, o, t, w, s, p = [], [], [], [], [], []
+    for bm in (64, 16, 8):
+        c = cls.get(bm)
+        f.append({"dense": 1, "packed": 2}[c["format"]] if c else 0)
+        o.append({"side-by-side": 1, "chunk-major": 2}[c["order"]] if c else 0)
+        t.append(c["tasks_per_wave"] if c else 0)
+        w.append(c["chunk_width"] if c else 0)
+        s.append(c["stages"] if c else 0)
+        p.append({"contiguous": 1, "interleaved": 2}[c["placement"]] if c else 0)
+    j = lambda v: ",".join(str(x) for x in v)
+    return (f"--no-tune --th {j(th)} --format {j(f)} --order {j(o)} --tpw {j(t)} --width {j(w)} "
+            f"--stages {j(s)} --place {j(p)} --hot-bytes {plan.get_hot_rows()[1]}")
+
+
+def measure(tsp, hip, config, prec, colB, args, headline):
+    """Build, tune and time one workload.  headline=True also runs the host
+    tiling, the device tiling comparison, the cold-cache leg and rocSPARSE;
+    returns (record, A, subs, plan) with the plan still open."""
+    t0 = time.time()
+    A, B, colB, cbp = tsp.gen_config(config, prec, colB)
+    prec = A.prec
+    s = 2 if prec == 0 else 4
+    pname = "fp16" if prec == 0 else "tf32"
+    log(f"generated {NAMES[config]}: {A.rows} rows, nnz {A.nnz}, {pname}, colB {colB} ({time.time() - t0:.1f}s)")
+
+    t0 = time.time()
+    f = tsp.features(A, 9.5, colB)
+    g, d = tsp.predict(f, prec)
+    if args.gamma is not None:
+        g = args.gamma
+    if args.delta is not None:
+        d = args.delta
+    subs = tsp.matrix_split(A, g, d)
+    split_ms = (time.time() - t0) * 1e3
+    pre = {"split": round(split_ms, 1)}
+    if headline:
+        t0 = time.time()
+        tiles = [tsp.tile_create(sb, A.cols, bm, prec) for sb, bm in zip(subs, (64, 16, 8))]
+        pre["tiles_host"] = round((time.time() - t0) * 1e3, 1)
+        tilenum = [t.tilenum for t in tiles]
+        kcols = {bm: int(np.unique(t.arrays()["tile_colidx"]).size) for t, bm in zip(tiles, (64, 16, 8))
+                 if t.tilenum}
+        plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
+        del tiles
+        # the same tiles built on the GPU (upload of the class sub-CSRs +
+        # device conversion), the alternative to the host conversion above
+        dplan = tsp.Plan.from_csr(subs, A.rows, A.cols, cbp, prec, B)
+        pre["tiles_device"] = round(dplan.tile_ms, 1)
+        dplan.close()
+    else:
+        plan = tsp.Plan.from_csr(subs, A.rows, A.cols, cbp, prec, B)
+        pre["tiles_device"] = round(plan.tile_ms, 1)
+        tilenum = [plan.tilenum(bm) for bm in (64, 16, 8)]
+        kcols = {bm: int(np.unique(sb.colidx).size) for sb, bm in zip(subs, (64, 16, 8)) if sb.nnz}
+    if not headline:
+        del B
+    log(f"split gamma={g} delta={d} ({split_ms:.0f} ms); tilenum {tilenum}")
+
+    th, model_ms, tune_ms = plan.tune(not args.no_tune)
+    th = apply_pins(plan, args) or th
+    hot_n, hot_b = plan.get_hot_rows()
+    pre.update({"model": round(model_ms, 2), "tune": round(tune_ms, 1)})
+    log(f"thresholds {th} (model {model_ms:.1f} ms, tuning {tune_ms:.1f} ms), hot B rows {hot_n} ({hot_b} bytes)")
+
+    # W untimed warm-up steps, a clock-stable warm-up (batches until the GFX
+    # clock settles, at most 1000 steps), then exactly K timed steps between
+    # device syncs and events on the plan's main stream
+    for _ in range(args.warmup):
+        plan.run(zero_c=False)
+    hip.tsp_device_sync()
+    wit, mhz = plan.warmup(1000)
+    plan.run(zero_c=True)
+    hip.tsp_device_sync()
+    ms = plan.time(args.steps)
+    hip.tsp_device_sync()
+    # a cross-check over a long window (at least 200 ms)
+    long_reps = int(min(100000, max(args.steps, np.ceil(200.0 / max(ms, 1e-4)))))
+    ms_long = plan.time(long_reps)
+    tflops = 2.0 * A.nnz * colB / (ms * 1e-3) / 1e12
+
+    # per-class kernel time, each class alone on the stream a step launches it on
+    cls = {}
+    for sb, bm, tn in zip(subs, (64, 16, 8), tilenum):
+        if tn == 0:
+            continue
+        warm = plan.time_class(bm, args.class_reps)
+        reps = int(min(20000, max(args.class_reps, args.class_min_ms / max(warm, 1e-4))))
+        cms = plan.time_class(bm, reps)
+        b = alg_bytes(sb.rows, sb.nnz, s, kcols[bm], colB, s)
+        v = plan.get_variant(bm)
+        w = v[0] or default_width(hip, bm, prec, cbp)
+        bn = tsp.tile_bn(bm, prec)
+        lines = tn * bn * (cbp // w) * max(1, -(-w * s // 128))
+        cls[bm] = {"ms": cms, "reps": reps, "rows": sb.rows, "nnz": int(sb.nnz), "tiles": tn,
+                   "format": {1: "dense", 2: "packed"}.get(plan.get_format(bm), "?"),
+                   "order": {0: "side-by-side", 1: "side-by-side", 2: "chunk-major"}[v[3]],
+                   "tasks_per_wave": max(1, v[2]), "stages": max(1, v[1]), "chunk_width": w,
+                   "placement": {0: "contiguous", 1: "interleaved"}.get(plan.get_placement(bm), "?"),
+                   "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9,
+                   "gathered_lines": lines, "glines_per_s": lines / (cms * 1e-3) / 1e9}
+    dom = max(cls, key=lambda k: cls[k]["ms"])
+    dk = cls[dom]
+    k_all = int(np.unique(A.colidx).size)
+    step_bytes = alg_bytes(A.rows, A.nnz, s, k_all, colB, s)
+    step_gbs = step_bytes / (ms * 1e-3) / 1e9
+
+    # the dominant kernel's instantiation spmm_kernel<BM, W, PREC, S, PK>; the
+    # profiled HBM traffic applies only to the same instantiation and hot rows
+    kname = (f"spmm_kernel<{dom}, {dk['chunk_width']}, {prec}, {dk['stages']}, "
+             f"{'true' if dk['format'] == 'packed' else 'false'}>")
+    traffic, traffic_note = None, "no profile of this workload in profiles/"
+    prof = os.path.join(ROOT, "profiles", f"traffic_config{config}_{pname}_{colB}.json")
+    if os.path.exists(prof):
+        with open(prof) as fh:
+            tp = json.load(fh).get(f"bm{dom}", {})
+        if tp.get("kernel", "").endswith(kname) and tp.get("hot_rows", 0) == hot_n:
+            traffic, traffic_note = tp.get("hbm_bytes_per_launch"), os.path.relpath(prof, ROOT)
+        else:
+            traffic_note = (f"{os.path.relpath(prof, ROOT)} profiles {tp.get('kernel', '?')} with "
+                            f"{tp.get('hot_rows', 0)} hot rows, not the tuned {kname} with {hot_n}")
+    roof = {"bound": "hbm", "achieved": round(dk["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "traffic_over_alg": round(traffic / dk["alg_bytes"], 3) if traffic else None,
+            "traffic_source": traffic_note, "kernel": kname, "kernel_ms": round(dk["ms"], 5),
+            "alg_bytes_per_launch": dk["alg_bytes"],
+            "step_achieved": round(step_gbs, 2), "step_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+            "step_alg_bytes": step_bytes}
+
+    rec = {"workload": f"{NAMES[config]}, {pname}, colB {colB}", "config_id": config, "dtype": pname,
+           "rows": A.rows, "nnz": A.nnz, "colB": colB, "colB_padded": cbp, "gamma": g, "delta": d,
+           "th": list(th), "tilenum": tilenum, "hot_rows": hot_n, "hot_bytes": hot_b,
+           "ms_per_step": ms, "tflops": tflops, "steps": args.steps, "window_ms": ms * args.steps,
+           "long_window": {"steps": long_reps, "ms_per_step": round(ms_long, 6),
+                           "tflops": round(2.0 * A.nnz * colB / (ms_long * 1e-3) / 1e12, 4)},
+           "warmup_clock": {"steps": wit, "gfx_mhz": mhz},
+           "roofline": roof, "classes": cls, "pre_ms": pre,
+           "replay": pins_of(plan, th, cls)}
+
+    if headline:
+        if args.cold_reps > 0:
+            cms, wms, cpms, cpb = cold_steps(hip, plan, args.cold_reps, step_bytes)
+            rec["cold_cache"] = {
+                "ms_per_step": round(cms, 6), "tflops": round(2.0 * A.nnz * colB / (cms * 1e-3) / 1e12, 4),
+                "alg_gbs": round(step_bytes / (cms * 1e-3) / 1e9, 1), "warm_single_ms": round(wms, 6),
+                "copy_cold_ms": round(cpms, 6), "copy_cold_gbs": round(cpb / (cpms * 1e-3) / 1e9, 1),
+                "reps": args.cold_reps,
+                "protocol": "median of single steps, each after a 1 GB copy that evicts L2 and the 256 MB "
+                            "MALL; warm_single_ms: the same single step again right after; copy_cold: a "
+                            "plain copy moving the step's algorithmic bytes after the same eviction"}
+        if not args.no_vendor:
+            rec["vendor"] = vendor_spmm(hip, A, B, colB, cbp, prec)
+        if not args.no_cpu:
+            rec["cpu_baseline"] = cpu_baseline(A, B, colB, prec)
+    return rec, A, subs, plan
+
+
+def vendor_spmm(hip, A, B, colB, cbp, prec):
+    """rocSPARSE spmm (CSR, alg default) on the same A and B."""
+    import ctypes as C
+    vp, vm = C.c_double(), C.c_double()
+    Cv = np.zeros((A.rows, colB), dtype=np.float32)
+    st = hip.tsp_vendor_spmm(prec, A.rows, A.cols, A.nnz, A.rowptr.ctypes.data_as(C.c_void_p),
+                             A.colidx.ctypes.data_as(C.c_void_p), A.val.ctypes.data_as(C.c_void_p), colB, cbp,
+                             np.ascontiguousarray(B).ctypes.data_as(C.c_void_p),
+                             Cv.ctypes.data_as(C.c_void_p), 20, 200, C.byref(vp), C.byref(vm))
+    if st:
+        return {"lib": "rocSPARSE", "status": st}
+    return {"lib": "rocSPARSE spmm (CSR, alg default)", "ms": round(vm.value, 5),
+            "tflops": round(2.0 * A.nnz * colB / (vm.value * 1e-3) / 1e12, 4)}
+
+
+def cpu_baseline(A, B, colB, prec):
+    """The oracle's OpenMP CSR SpMM (fp32 accumulate, dynamic(64)) over the
+    WHOLE matrix on the host's cores: one warm-up run, then timed runs until
+    three are done or 20 s have passed; the median is reported."""
+    import oracle
+    a32 = oracle.values_f64(A.val, prec).astype(np.float32)
+    b32 = oracle.values_f64(B[:, :colB].reshape(-1), prec).astype(np.float32).reshape(A.cols, colB)
+    out = np.zeros((A.rows, colB), dtype=np.float32)
+    t1 = time.perf_counter()
+    _, used = oracle.spmm_f32_omp(A.rows, A.rowptr, A.colidx, a32, b32, colB, out)
+    first = time.perf_counter() - t1
+    times, spent = [], 0.0
+    while len(times) < 3 and spent < 20.0:
+        t1 = time.perf_counter()
+        oracle.spmm_f32_omp(A.rows, A.rowptr, A.colidx, a32, b32, colB, out)
+        times.append(time.perf_counter() - t1)
+        spent += times[-1]
+    tm = float(np.median(times))
+    nproc = len(os.sched_getaffinity(0))
+    return {"value": round(2.0 * A.nnz * colB / tm / 1e12, 5), "unit": "TFLOPS", "cores": int(used), "kind": "port",
+            "sample": f"whole matrix: {A.rows} rows, {A.nnz} nnz, colB {colB}, fp32 accumulate, OpenMP "
+                      f"dynamic(64) on {used} threads ({nproc} cpus usable, OMP_NUM_THREADS="
+                      f"{os.environ.get('OMP_NUM_THREADS', 'unset')}), median of {len(times)} after one warm-up "
+                      f"run ({first * 1e3:.0f} ms), {tm * 1e3:.1f} ms per run"}
+
+
+TARGETS = {3: "T3", 5: "T5"}
 
 
 def main():
@@ -186,9 +460,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--config", type=int, default=5,
+                    help="headline configuration (default 5: RMAT scale 22, tf32, colB 64, the largest)")
     ap.add_argument("--prec", choices=["fp16", "tf32"], default=None)
     ap.add_argument("--colB", type=int, default=-1)
+    ap.add_argument("--targets", default="3,5",
+                    help="configurations also run as fp16 / colB 128 targets (T3, T5); empty for none")
     ap.add_argument("--gamma", type=float, default=None)
     ap.add_argument("--delta", type=float, default=None)
     ap.add_argument("--no-tune", action="store_true")
@@ -239,200 +516,65 @@ def main():
         return
 
     prec = {"fp16": 0, "tf32": 1, None: -1}[args.prec]
-    t0 = time.time()
-    A, B, colB, cbp = tsp.gen_config(args.config, prec, args.colB)
-    prec = A.prec
-    s = 2 if prec == 0 else 4
-    log(f"generated {NAMES[args.config]}: {A.rows} rows, nnz {A.nnz}, colB {colB} ({time.time() - t0:.1f}s)")
-
-    t0 = time.time()
-    f = tsp.features(A, 9.5, colB)
-    g, d = tsp.predict(f, prec)
-    if args.gamma is not None:
-        g = args.gamma
-    if args.delta is not None:
-        d = args.delta
-    subs = tsp.matrix_split(A, g, d)
-    split_ms = (time.time() - t0) * 1e3
-    t0 = time.time()
-    tiles = [tsp.tile_create(sb, A.cols, bm, prec) for sb, bm in zip(subs, (64, 16, 8))]
-    host_tiles_ms = (time.time() - t0) * 1e3
-    log(f"split gamma={g} delta={d} ({split_ms:.0f} ms); host tiles: tilenum {[t.tilenum for t in tiles]} "
-        f"({host_tiles_ms:.0f} ms)")
-
-    plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
-    th, model_ms, tune_ms = plan.tune(not args.no_tune)
-    if args.th:
-        plan.set_th(*args.th)
-        th = tuple(args.th)
-    for bm, f in zip((64, 16, 8), args.format or ()):
-        if f:
-            plan.set_format(bm, f)
-    for bm, o in zip((64, 16, 8), args.order or ()):
-        if o:
-            w, st, tpw, _ = plan.get_variant(bm)
-            plan.set_variant(bm, w, st, tpw, o)
-    for bm, n in zip((64, 16, 8), args.tpw or ()):
-        if n:
-            w, st, _, o = plan.get_variant(bm)
-            plan.set_variant(bm, w, st, n, o)
-    for bm, wd in zip((64, 16, 8), args.width or ()):
-        if wd:
-            _, st, n, o = plan.get_variant(bm)
-            plan.set_variant(bm, wd, st, n, o)
-    for bm, sg in zip((64, 16, 8), args.stages or ()):
-        if sg:
-            wd, _, n, o = plan.get_variant(bm)
-            plan.set_variant(bm, wd, sg, n, o)
-    for bm, pl in zip((64, 16, 8), args.place or ()):
-        if pl:
-            plan.set_placement(bm, pl - 1)
-    if args.hot_bytes is not None:
-        plan.set_hot_rows(args.hot_bytes)
-    hot_n, hot_b = plan.get_hot_rows()
-    log(f"thresholds {th} (model {model_ms:.1f} ms, tuning {tune_ms:.1f} ms), hot B rows {hot_n} ({hot_b} bytes)")
-
     if args.sweep:
-        sweep(plan, tiles, cbp, args)
+        args.no_vendor = args.no_cpu = True
+        args.cold_reps = 0
+    rec, A, subs, plan = measure(tsp, hip, args.config, prec, args.colB, args, headline=True)
+    if args.sweep:
+        sweep(plan, rec["tilenum"], rec["colB_padded"], args)
         plan.close()
         return
+    plan.close()
+    del A, subs
+    ceiling = gather_ceiling(hip)
 
-    # warmup, then K timed steps bracketed by device syncs and main-stream events
-    plan.warmup(args.warmup)
-    plan.run(zero_c=True)
-    hip.tsp_device_sync()
-    ms = plan.time(args.steps)
-    hip.tsp_device_sync()
-    tflops = 2.0 * A.nnz * colB / (ms * 1e-3) / 1e12
-    # per-class kernel time (each class alone on its own stream)
-    cls = {}
-    for t, sb, bm in zip(tiles, subs, (64, 16, 8)):
-        if t.tilenum == 0:
-            continue
-        # one untimed round first (the clock drops while the device idles),
-        # then enough launches to span at least --class-min-ms
-        warm = plan.time_class(bm, args.class_reps)
-        reps = int(min(20000, max(args.class_reps, args.class_min_ms / max(warm, 1e-4))))
-        cms = plan.time_class(bm, reps)
-        k_rows = int(np.unique(t.arrays()["tile_colidx"]).size)
-        b = alg_bytes(sb.rows, sb.nnz, s, k_rows, colB, s)
-        cls[bm] = {"ms": cms, "reps": reps, "rows": sb.rows, "nnz": int(sb.nnz), "tiles": t.tilenum,
-                   "format": {1: "dense", 2: "packed"}.get(plan.get_format(bm), "?"),
-                   "order": {0: "side-by-side", 1: "side-by-side", 2: "chunk-major"}[plan.get_variant(bm)[3]],
-                   "tasks_per_wave": max(1, plan.get_variant(bm)[2]),
-                   "stages": max(1, plan.get_variant(bm)[1]),
-                   "chunk_width": plan.get_variant(bm)[0] or default_width(hip, bm, prec, cbp),
-                   "placement": {0: "contiguous", 1: "interleaved"}.get(plan.get_placement(bm), "?"),
-                   "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9}
-    dom = max(cls, key=lambda k: cls[k]["ms"])
-    k_all = int(np.unique(A.colidx).size)
-    step_bytes = alg_bytes(A.rows, A.nnz, s, k_all, colB, s)
-    step_gbs = step_bytes / (ms * 1e-3) / 1e9
+    def gather_stats(r):
+        dk = r["classes"][max(r["classes"], key=lambda k: r["classes"][k]["ms"])]
+        return {"glines_per_s": round(dk["glines_per_s"], 2), "ceiling_glines_per_s": round(ceiling, 2),
+                "frac_of_ceiling": round(dk["glines_per_s"] / ceiling, 3)}
 
-    # the dominant kernel's instantiation spmm_kernel<BM, W, PREC, S, PK>; the
-    # profiled HBM traffic applies only to the same instantiation
-    dk = cls[dom]
-    kname = (f"spmm_kernel<{dom}, {dk['chunk_width']}, {prec}, {dk['stages']}, "
-             f"{'true' if dk['format'] == 'packed' else 'false'}>")
-    traffic, traffic_note = None, "no profile of this workload in profiles/"
-    prof = os.path.join(ROOT, "profiles", f"traffic_config{args.config}_{'fp16' if prec == 0 else 'tf32'}_{colB}.json")
-    if os.path.exists(prof):
-        with open(prof) as fh:
-            tp = json.load(fh).get(f"bm{dom}", {})
-        if tp.get("kernel", "").endswith(kname):
-            traffic, traffic_note = tp.get("hbm_bytes_per_launch"), os.path.relpath(prof, ROOT)
-        else:
-            traffic_note = f"{os.path.relpath(prof, ROOT)} profiles {tp.get('kernel', '?')}, not the tuned {kname}"
-
-    roof = {"bound": "hbm", "achieved": round(cls[dom]["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(cls[dom]["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "traffic_source": traffic_note, "kernel": kname, "kernel_ms": round(cls[dom]["ms"], 5),
-            "alg_bytes_per_launch": cls[dom]["alg_bytes"],
-            "step_achieved": round(step_gbs, 2), "step_frac": round(step_gbs / HBM_PEAK_GBS, 4),
-            "step_alg_bytes": step_bytes}
-
-    # the same tiles built on the GPU (upload of the class sub-CSRs + device
-    # conversion), the alternative to the host conversion timed above
-    dplan = tsp.Plan.from_csr(subs, A.rows, A.cols, cbp, prec, B)
-    dev_tiles_ms = dplan.tile_ms
-    dplan.close()
-
-    # after every other device measurement: the eviction copies must not
-    # disturb the class timings above
-    cold = None
-    if args.cold_reps > 0:
-        sb = step_bytes
-        cms, wms, cpms, cpb = cold_steps(hip, plan, args.cold_reps, sb)
-        cold = {"ms_per_step": round(cms, 6), "tflops": round(2.0 * A.nnz * colB / (cms * 1e-3) / 1e12, 4),
-                "alg_gbs": round(sb / (cms * 1e-3) / 1e9, 1), "warm_single_ms": round(wms, 6),
-                "copy_cold_ms": round(cpms, 6), "copy_cold_gbs": round(cpb / (cpms * 1e-3) / 1e9, 1),
-                "reps": args.cold_reps,
-                "protocol": "median of single steps, each after a 1 GB copy that evicts L2 and the 256 MB MALL; "
-                            "warm_single_ms: the same single step again right after; copy_cold: a plain copy "
-                            "moving the step's algorithmic bytes after the same eviction"}
-
-    vendor = None
-    if not args.no_vendor:
-        import ctypes as C
-        vp, vm = C.c_double(), C.c_double()
-        Cv = np.zeros((A.rows, colB), dtype=np.float32)
-        st = hip.tsp_vendor_spmm(prec, A.rows, A.cols, A.nnz, A.rowptr.ctypes.data_as(C.c_void_p),
-                                 A.colidx.ctypes.data_as(C.c_void_p), A.val.ctypes.data_as(C.c_void_p), colB, cbp,
-                                 np.ascontiguousarray(B).ctypes.data_as(C.c_void_p),
-                                 Cv.ctypes.data_as(C.c_void_p), 20, 200, C.byref(vp), C.byref(vm))
-        if st == 0:
-            vendor = {"lib": "rocSPARSE spmm (CSR, alg default)", "ms": round(vm.value, 5),
-                      "tflops": round(2.0 * A.nnz * colB / (vm.value * 1e-3) / 1e12, 4)}
-        else:
-            vendor = {"lib": "rocSPARSE", "status": st}
-        del Cv
-
-    cpu = None
-    if not args.no_cpu:
-        import oracle
-        a32 = oracle.values_f64(A.val, prec).astype(np.float32)
-        b32 = oracle.values_f64(B[:, :colB].reshape(-1), prec).astype(np.float32).reshape(A.cols, colB)
-        # bounded sample: the first rows holding ~min(nnz, 4M) entries
-        lim = min(A.nnz, 4_000_000)
-        r_end = int(np.searchsorted(A.rowptr, lim, side="right")) - 1
-        r_end = max(1, min(A.rows, r_end))
-        nz = int(A.rowptr[r_end])
-        out = np.zeros((r_end, colB), dtype=np.float32)
-        oracle.spmm_f32_omp(r_end, A.rowptr[:r_end + 1], A.colidx, a32, b32, colB, out)   # warmup
-        times = []
-        used = 1
-        for _ in range(5):
-            t1 = time.perf_counter()
-            _, used = oracle.spmm_f32_omp(r_end, A.rowptr[:r_end + 1], A.colidx, a32, b32, colB, out)
-            times.append(time.perf_counter() - t1)
-        tm = float(np.median(times))
-        nproc = len(os.sched_getaffinity(0))
-        cpu = {"value": round(2.0 * nz * colB / tm / 1e12, 5), "unit": "TFLOPS", "cores": int(used), "kind": "port",
-               "sample": f"rows 0..{r_end} ({nz} of {A.nnz} nnz), colB {colB}, fp32 accumulate, "
-                         f"OpenMP dynamic(64) on {used} threads ({nproc} cpus usable, "
-                         f"OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS', 'unset')}), "
-                         f"median of 5 after 1 warmup, {tm * 1e3:.2f} ms"}
+    targets = {}
+    for cfg in [int(x) for x in args.targets.split(",") if x.strip()]:
+        targ = argparse.Namespace(**vars(args))
+        for k in ("th", "format", "order", "tpw", "width", "stages", "place", "hot_bytes", "gamma", "delta"):
+            setattr(targ, k, None)
+        targ.no_tune = False
+        t, _, _, tplan = measure(tsp, hip, cfg, 0, 128, targ, headline=False)
+        tplan.close()
+        targets[TARGETS.get(cfg, f"C{cfg}")] = {
+            "workload": t["workload"], "ms_per_step": round(t["ms_per_step"], 6), "tflops": round(t["tflops"], 4),
+            "long_window": t["long_window"], "kernel": t["roofline"]["kernel"],
+            "kernel_ms": t["roofline"]["kernel_ms"], "frac": t["roofline"]["frac"],
+            "alg_bytes_per_launch": t["roofline"]["alg_bytes_per_launch"], "traffic": t["roofline"]["traffic"],
+            "traffic_over_alg": t["roofline"]["traffic_over_alg"], "traffic_source": t["roofline"]["traffic_source"],
+            "gather": gather_stats(t), "hot_rows": t["hot_rows"], "th": t["th"], "tilenum": t["tilenum"],
+            "classes": {f"bm{k}": {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                        for k, v in t["classes"].items()},
+            "replay": t["replay"]}
 
     line = {
         "metric": "SpMM TFLOPS (2*nnz*colB/t) + % HBM roofline",
-        "value": round(tflops, 4), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp16" if prec == 0 else "tf32", "data": "synthetic",
-        "config": {"workload": f"{NAMES[args.config]}, {'fp16' if prec == 0 else 'tf32'}, colB {colB}",
-                   "config_id": args.config, "rows": A.rows, "nnz": A.nnz, "colB": colB, "colB_padded": cbp,
-                   "gamma": g, "delta": d, "th": list(th), "tilenum": [t.tilenum for t in tiles],
-                   "hot_rows": hot_n, "hot_bytes": hot_b,
-                   "parallelism": "single GPU"},
-        "roofline": roof,
+        "value": round(rec["tflops"], 4), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(rec["ms_per_step"], 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": rec["dtype"], "data": "synthetic",
+        "config": {"workload": rec["workload"], "config_id": rec["config_id"], "rows": rec["rows"],
+                   "nnz": rec["nnz"], "colB": rec["colB"], "colB_padded": rec["colB_padded"],
+                   "gamma": rec["gamma"], "delta": rec["delta"], "th": rec["th"], "tilenum": rec["tilenum"],
+                   "hot_rows": rec["hot_rows"], "hot_bytes": rec["hot_bytes"], "parallelism": "single GPU"},
+        "roofline": rec["roofline"],
+        "cpu_baseline": rec.get("cpu_baseline"),
+        "gather": gather_stats(rec),
+        "targets": targets,
+        "window_ms": round(rec["window_ms"], 3),
+        "long_window": rec["long_window"],
+        "warmup_clock": rec["warmup_clock"],
         "classes": {f"bm{k}": {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                    for k, v in cls.items()},
-        "cold_cache": cold,
-        "vendor": vendor,
-        "cpu_baseline": cpu,
-        "pre_ms": {"split": round(split_ms, 1), "tiles_host": round(host_tiles_ms, 1),
-                   "tiles_device": round(dev_tiles_ms, 1), "model": round(model_ms, 2), "tune": round(tune_ms, 1)},
+                    for k, v in rec["classes"].items()},
+        "cold_cache": rec.get("cold_cache"),
+        "vendor": rec.get("vendor"),
+        "pre_ms": rec["pre_ms"],
+        "replay": rec["replay"],
     }
-    plan.close()
     print(json.dumps(line), flush=True)
 
 

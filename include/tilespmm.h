@@ -221,7 +221,16 @@ int tsp_plan_get_hot_rows(tsp_plan *plan, int *nhot, long long *bytes);
  * the plan's main stream; a plan with one class launches it on the main
  * stream).  zero_c != 0 clears C first. */
 int tsp_plan_run(tsp_plan *plan, int zero_c);
-/* Clock-stabilising warmup (src/csr2tile.h:798-823 analogue). */
+/* Warm-up before timing, replacing warmup_gpu (src/csr2tile.h:798-823):
+ * steps in batches of 20, then 50, reading the GFX clock
+ * (tsp_gpu_clock_mhz) after each batch, until two successive readings agree
+ * within 2% and are at least 95% of the maximum clock, or three successive
+ * readings agree within 2% (MI355X power management can settle a
+ * memory-bound load below 95% of the maximum); at most max_iters steps.
+ * Without a readable clock it runs min(max_iters, 100) steps, the
+ * reference's fallback.  *iters_run / *clock_mhz (may be NULL): steps run and
+ * the last clock reading. */
+int tsp_plan_warmup_clock(tsp_plan *plan, int max_iters, int *iters_run, unsigned *clock_mhz);
 int tsp_plan_warmup(tsp_plan *plan, int max_iters);
 /* Time `reps` back-to-back runs bracketed by events on the plan's main stream. */
 int tsp_plan_time(tsp_plan *plan, int reps, double *ms_per_iter);
@@ -242,6 +251,8 @@ typedef struct {
     double time_ms;          /* per iteration */
     double tflops;           /* 2 * nnz * logical_colB / t */
     double model_ms, tune_ms;
+    int warmup_iters;        /* steps of the last clock-stable warm-up */
+    unsigned clock_mhz;      /* GFX clock at its end (0: not readable) */
 } tsp_run_result;
 int tsp_call_tilespmm(int device_id, Tile_matrix *m64, Tile_matrix *m16, Tile_matrix *m8, int rowA,
                       int colA, int colB_p, long long total_nnz, int prec, const void *h_B,

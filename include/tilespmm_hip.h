@@ -78,6 +78,12 @@ typedef struct {
 } tsp_kernel_info;
 int tsp_kernel_probe(int bm, int prec, int colB_p, tsp_kernel_info *out);
 
+/* Current and maximum GFX clock of a device in MHz, read through AMD SMI
+ * (libamd_smi.so, loaded on first use).  Replaces get_gpu_clock
+ * (src/common.h:96-119), which reads the SM clock through NVML.  *mhz = 0
+ * (status TSP_OK) when the clock cannot be read. */
+int tsp_gpu_clock_mhz(int device_id, unsigned *mhz, unsigned *max_mhz);
+
 /* Memory and copies (hipMalloc / hipMemcpy / hipMemset wrappers). */
 int tsp_malloc(void **ptr, size_t bytes);
 int tsp_free(void *ptr);

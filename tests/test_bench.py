@@ -23,9 +23,10 @@ def test_bench_refuses_several_gpus():
 def test_bench_json_line(tsp):
     if not tsp.device_available():
         pytest.fail("no gfx950 device: GPU tests need an MI355X")
-    print("bench.py --config 1 --steps 20 --warmup 5", flush=True)
-    r = subprocess.run([sys.executable, "-u", BENCH, "--config", "1", "--steps", "20", "--warmup", "5",
-                        "--class-reps", "10", "--cold-reps", "3"], capture_output=True, text=True, timeout=300)
+    print("bench.py --config 1 --targets 1 --steps 20 --warmup 5", flush=True)
+    r = subprocess.run([sys.executable, "-u", BENCH, "--config", "1", "--targets", "1", "--steps", "20",
+                        "--warmup", "5", "--class-reps", "10", "--cold-reps", "3"], capture_output=True, text=True,
+                       timeout=300)
     assert r.returncode == 0, r.stderr[-2000:]
     lines = [l for l in r.stdout.splitlines() if l.strip()]
     assert len(lines) == 1, r.stdout
@@ -50,5 +51,18 @@ def test_bench_json_line(tsp):
     for k in ("value", "unit", "cores", "kind", "sample"):
         assert k in cpu, k
     assert cpu["kind"] in ("port", "reference") and cpu["value"] > 0 and cpu["cores"] >= 1
+    assert "whole matrix" in cpu["sample"]
     cold = d["cold_cache"]
     assert cold["reps"] == 3 and cold["ms_per_step"] > 0 and cold["copy_cold_ms"] > 0
+    # the roofline's kernel runs inside the step: its time cannot exceed the
+    # step's (C1's 4-microsecond steps are launch-bound and excepted)
+    if d["ms_per_step"] > 0.05:
+        assert roof["kernel_ms"] <= d["ms_per_step"] * 1.05
+    assert d["warmup_clock"]["steps"] >= 1 and d["long_window"]["steps"] >= 20
+    assert d["gather"]["ceiling_glines_per_s"] > 0
+    # the fp16 / colB 128 target record of the same run
+    t = d["targets"]["C1"]
+    assert "fp16, colB 128" in t["workload"] and t["tflops"] > 0
+    assert t["tflops"] == pytest.approx(2 * 32768 * 128 / (t["ms_per_step"] * 1e-3) / 1e12, rel=2e-3)
+    assert t["frac"] > 0 and t["kernel"].startswith("spmm_kernel<")
+    assert d["replay"].startswith("--no-tune --th ")

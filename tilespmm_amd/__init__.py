@@ -122,7 +122,7 @@ class RunResult(C.Structure):
     _fields_ = [
         ("th64", C.c_int), ("th16", C.c_int), ("th8", C.c_int), ("pre_time_ms", C.c_double),
         ("time_ms", C.c_double), ("tflops", C.c_double), ("model_ms", C.c_double),
-        ("tune_ms", C.c_double),
+        ("tune_ms", C.c_double), ("warmup_iters", C.c_int), ("clock_mhz", C.c_uint),
     ]
 
 
@@ -136,6 +136,7 @@ HIP_SYMBOLS = {
     "tsp_device_init": (C.c_int, [C.c_int]),
     "tsp_device_probe": (C.c_int, [C.c_int, C.POINTER(DeviceInfo)]),
     "tsp_kernel_probe": (C.c_int, [C.c_int, C.c_int, C.c_int, C.POINTER(KernelInfo)]),
+    "tsp_gpu_clock_mhz": (C.c_int, [C.c_int, C.POINTER(C.c_uint), C.POINTER(C.c_uint)]),
     "tsp_malloc": (C.c_int, [C.POINTER(C.c_void_p), C.c_size_t]),
     "tsp_free": (C.c_int, [_P]),
     "tsp_memcpy_h2d": (C.c_int, [_P, _P, C.c_size_t]),
@@ -226,6 +227,7 @@ HOST_SYMBOLS = {
     "tsp_plan_get_hot_rows": (C.c_int, [_P, _IP, C.POINTER(C.c_longlong)]),
     "tsp_plan_run": (C.c_int, [_P, C.c_int]),
     "tsp_plan_warmup": (C.c_int, [_P, C.c_int]),
+    "tsp_plan_warmup_clock": (C.c_int, [_P, C.c_int, _IP, C.POINTER(C.c_uint)]),
     "tsp_plan_time": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double)]),
     "tsp_plan_time_class": (C.c_int, [_P, C.c_int, C.c_int, C.POINTER(C.c_double)]),
     "tsp_plan_download_c": (C.c_int, [_P, _P]),
@@ -605,6 +607,10 @@ class Plan:
     def __del__(self):
         self.close()
 
+    def tilenum(self, bm: int) -> int:
+        """Tiles of one class (0 when the class is empty)."""
+        return load()[1].tsp_plan_tilenum(self.p, bm)
+
     def set_th(self, th64: int, th16: int, th8: int):
         _check("tsp_plan_set_th", load()[1].tsp_plan_set_th(self.p, th64, th16, th8))
 
@@ -653,7 +659,11 @@ class Plan:
         _check("tsp_plan_run", load()[1].tsp_plan_run(self.p, int(zero_c)))
 
     def warmup(self, iters: int):
-        _check("tsp_plan_warmup", load()[1].tsp_plan_warmup(self.p, iters))
+        """Clock-stable warm-up of at most `iters` steps; returns (steps run,
+        last GFX clock reading in MHz, 0 when unreadable)."""
+        n, mhz = C.c_int(), C.c_uint()
+        _check("tsp_plan_warmup_clock", load()[1].tsp_plan_warmup_clock(self.p, iters, C.byref(n), C.byref(mhz)))
+        return n.value, mhz.value
 
     def time(self, reps: int) -> float:
         ms = C.c_double()

@@ -4,9 +4,13 @@
 // point returns an int status; none of them exits the process.  Argument
 // checks happen here, on the host, before anything is launched: a launch whose
 // shapes do not match what the kernels assume is refused with TSP_EINVAL.
+#include <amd_smi/amdsmi.h>
+#include <dlfcn.h>
 #include <hip/hip_runtime.h>
 #include <stdio.h>
 #include <string.h>
+
+#include <mutex>
 
 #include "../../include/tilespmm_hip.h"
 #include "tsp_kernels.h"
@@ -83,6 +87,65 @@ int tsp_kernel_probe(int bm, int prec, int colB_p, tsp_kernel_info *out)
     out->shared_bytes = (long long)a.sharedSizeBytes;
     out->cols_per_task = w;
     out->iteration_bytes = tsp::kWavesPerBlock * (bm * bn + bn * w) * (prec == TSP_PREC_FP16 ? 2 : 4);
+    return TSP_OK;
+}
+
+// GFX clock through AMD SMI, loaded at run time (as the reference loads NVML
+// for its warm-up, src/common.h:96-119) so the library does not depend on it.
+// The device is matched to its SMI handle by PCI bus id.
+namespace {
+struct Smi {
+    std::mutex mu;
+    bool tried = false;
+    decltype(&amdsmi_get_processor_handle_from_bdf) from_bdf = nullptr;
+    decltype(&amdsmi_get_clock_info) clock_info = nullptr;
+    static constexpr int kMaxDev = 64;
+    amdsmi_processor_handle handle[kMaxDev] = {};
+    bool looked[kMaxDev] = {};
+};
+Smi g_smi;
+}  // namespace
+
+int tsp_gpu_clock_mhz(int device_id, unsigned *mhz, unsigned *max_mhz)
+{
+    if (!mhz) return TSP_EINVAL;
+    *mhz = 0;
+    if (max_mhz) *max_mhz = 0;
+    if (device_id < 0 || device_id >= Smi::kMaxDev) return TSP_EINVAL;
+    std::lock_guard<std::mutex> lk(g_smi.mu);
+    if (!g_smi.tried) {
+        g_smi.tried = true;
+        void *lib = dlopen("libamd_smi.so", RTLD_LAZY | RTLD_LOCAL);
+        if (!lib) lib = dlopen("/opt/rocm/lib/libamd_smi.so", RTLD_LAZY | RTLD_LOCAL);
+        auto init = lib ? (decltype(&amdsmi_init))dlsym(lib, "amdsmi_init") : nullptr;
+        g_smi.from_bdf = lib ? (decltype(g_smi.from_bdf))dlsym(lib, "amdsmi_get_processor_handle_from_bdf") : nullptr;
+        g_smi.clock_info = lib ? (decltype(g_smi.clock_info))dlsym(lib, "amdsmi_get_clock_info") : nullptr;
+        if (!init || !g_smi.from_bdf || !g_smi.clock_info || init(AMDSMI_INIT_AMD_GPUS) != AMDSMI_STATUS_SUCCESS)
+            g_smi.clock_info = nullptr;
+    }
+    if (!g_smi.clock_info) return TSP_OK;
+    if (!g_smi.looked[device_id]) {
+        g_smi.looked[device_id] = true;
+        char pci[64] = {0};
+        unsigned dom = 0, bus = 0, dv = 0, fn = 0;
+        if (hipDeviceGetPCIBusId(pci, sizeof pci, device_id) == hipSuccess &&
+            sscanf(pci, "%x:%x:%x.%x", &dom, &bus, &dv, &fn) == 4) {
+            amdsmi_bdf_t bdf;
+            bdf.as_uint = 0;
+            bdf.domain_number = dom;
+            bdf.bus_number = bus;
+            bdf.device_number = dv;
+            bdf.function_number = fn;
+            amdsmi_processor_handle h = nullptr;
+            if (g_smi.from_bdf(bdf, &h) == AMDSMI_STATUS_SUCCESS) g_smi.handle[device_id] = h;
+        }
+    }
+    if (!g_smi.handle[device_id]) return TSP_OK;
+    amdsmi_clk_info_t info;
+    memset(&info, 0, sizeof info);
+    if (g_smi.clock_info(g_smi.handle[device_id], AMDSMI_CLK_TYPE_GFX, &info) != AMDSMI_STATUS_SUCCESS) return TSP_OK;
+    *mhz = info.clk;
+    if (max_mhz) *max_mhz = info.max_clk;
     return TSP_OK;
 }
 

@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <chrono>
 #include <map>
 #include <memory>
@@ -657,11 +658,37 @@ extern "C" int tsp_plan_time_class(tsp_plan *p, int bm, int reps, double *ms)
     return TSP_OK;
 }
 
-extern "C" int tsp_plan_warmup(tsp_plan *p, int iters)
+// warmup_gpu (src/csr2tile.h:798-823) with the clock read through AMD SMI.
+extern "C" int tsp_plan_warmup_clock(tsp_plan *p, int max_iters, int *iters_run, unsigned *clock_mhz)
 {
-    if (!p) return TSP_EINVAL;
-    for (int i = 0; i < iters; ++i) TSP_TRY(tsp_plan_run(p, 0));
+    if (!p || max_iters < 0) return TSP_EINVAL;
+    unsigned cur = 0, maxc = 0;
+    TSP_TRY(tsp_gpu_clock_mhz(p->dev, &cur, &maxc));
+    const bool clocked = cur > 0;
+    const int limit = clocked ? max_iters : std::min(max_iters, 100);
+    const auto agree = [](unsigned a, unsigned b) { return a && b && std::fabs((double)a / b - 1.0) <= 0.02; };
+    unsigned prev = 0, prev2 = 0;
+    int total = 0;
+    while (total < limit) {
+        const int count = std::min(total == 0 ? 20 : 50, limit - total);
+        for (int i = 0; i < count; ++i) TSP_TRY(tsp_plan_run(p, 0));
+        TSP_TRY(tsp_stream_sync(p->main));
+        total += count;
+        if (!clocked) continue;
+        TSP_TRY(tsp_gpu_clock_mhz(p->dev, &cur, nullptr));
+        const bool high = maxc == 0 || (cur >= 0.95 * maxc && prev >= 0.95 * maxc);
+        if (agree(cur, prev) && (high || agree(prev, prev2))) break;
+        prev2 = prev;
+        prev = cur;
+    }
+    if (iters_run) *iters_run = total;
+    if (clock_mhz) *clock_mhz = clocked ? cur : 0;
     return tsp_device_sync();
+}
+
+extern "C" int tsp_plan_warmup(tsp_plan *p, int max_iters)
+{
+    return tsp_plan_warmup_clock(p, max_iters, nullptr, nullptr);
 }
 
 // One tuning measurement of a class: a warm-up launch, then enough launches
@@ -942,10 +969,14 @@ extern "C" int tsp_plan_execute(tsp_plan *p, long long total_nnz, float *h_C, do
     int th[3];
     double model_ms = 0, tune_ms = 0;
     TSP_TRY(tsp_plan_tune(p, tune, th, &model_ms, &tune_ms));
-    TSP_TRY(tsp_plan_warmup(p, 100));
+    // as call_tilespmm_cuda: warm-up (up to 1000 steps with a readable
+    // clock), result run, download, warm-up again, then the timed loop
+    int wit = 0;
+    unsigned mhz = 0;
+    TSP_TRY(tsp_plan_warmup_clock(p, 1000, &wit, &mhz));
     TSP_TRY(tsp_plan_run(p, 1));
     if (h_C) TSP_TRY(tsp_plan_download_c(p, h_C));
-    TSP_TRY(tsp_plan_warmup(p, 100));
+    TSP_TRY(tsp_plan_warmup_clock(p, 1000, &wit, &mhz));
     TSP_TRY(tsp_plan_run(p, 1));
     double ms = 0;
     TSP_TRY(tsp_plan_time(p, repeat > 0 ? repeat : 1000, &ms));
@@ -962,6 +993,8 @@ extern "C" int tsp_plan_execute(tsp_plan *p, long long total_nnz, float *h_C, do
         out->tflops = tflops;
         out->model_ms = model_ms;
         out->tune_ms = tune_ms;
+        out->warmup_iters = wit;
+        out->clock_mhz = mhz;
     }
     return TSP_OK;
 }
