@@ -210,10 +210,11 @@ int tsp_plan_get_placement(tsp_plan *plan, int bm);
  * of the plan's B and point every class's tile columns at the copies; every
  * step then re-copies them before the class kernels run.  Only columns
  * gathered at least TSP_HOT_MIN_GATHERS times qualify.  budget_bytes 0
- * restores the canonical column indices.  tsp_plan_tune times a few budgets
- * (0 among them) and keeps the fastest.  get: the current slot count and
- * bytes.  No counterpart in the reference. */
-#define TSP_HOT_MAX_BYTES (32LL << 20)
+ * restores the canonical column indices.  tsp_plan_tune times steps with
+ * no hot rows against 16 MB of them and keeps the hot rows when they are 2%
+ * faster.  get: the current slot count and bytes.  No counterpart in the
+ * reference. */
+#define TSP_HOT_MAX_BYTES (64LL << 20)
 #define TSP_HOT_MIN_GATHERS 4
 int tsp_plan_set_hot_rows(tsp_plan *plan, long long budget_bytes);
 int tsp_plan_get_hot_rows(tsp_plan *plan, int *nhot, long long *bytes);
