@@ -266,6 +266,25 @@ int tsp_tiles_pack_device(int tilenum, int bm, int bn, int prec, const void *d_v
                           const unsigned long long *d_bitmap, long long *nvals, void **d_pval,
                           int **d_vptr, void *stream);
 
+/* Allocation-free variant of tsp_tiles_pack_device.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * The caller passes the outputs: d_vptr [tilenum + 1] ints and d_pval, room
+ * for pval_capacity elements of the value type, which must hold the packed
+ * values plus 4 padding elements.  *nvals = number of packed values (also
+ * on failure for lack of room, which returns TSP_EINVAL, so the caller can
+ * size the buffer).  The scan's per-block sums live in a static 1 MiB
+ * device array, so tilenum is limited to TSP_PACK_NOALLOC_MAX_TILES (larger
+ * requests return TSP_EINVAL).  Calls no hipMalloc/hipFree; synchronises
+ * `stream`.  Every call on one GPU shares that array: calls that overlap on
+ * the same GPU (other threads, other streams) race and must be serialised
+ * by the caller. */
+#define TSP_PACK_NOALLOC_MAX_TILES (((1LL << 18) - 1) * 2048)
+int tsp_tiles_pack_device_noalloc(int tilenum, int bm, int bn, int prec, const void *d_val,
+                                  const unsigned long long *d_bitmap, void *d_pval,
+                                  long long pval_capacity, int *d_vptr, long long *nvals,
+                                  void *stream);
+
 #ifdef __cplusplus
 }
 #endif

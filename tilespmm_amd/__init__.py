@@ -179,6 +179,8 @@ HIP_SYMBOLS = {
     "tsp_dev_tiles_free": (C.c_int, [C.POINTER(DevTiles)]),
     "tsp_tiles_pack_device": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, C.POINTER(C.c_longlong),
                                         C.POINTER(C.c_void_p), C.POINTER(C.c_void_p), _P]),
+    "tsp_tiles_pack_device_noalloc": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, C.c_longlong, _P,
+                                                C.POINTER(C.c_longlong), _P]),
 }
 HOST_SYMBOLS = {
     "tsp_mm_read": (C.c_int, [C.c_char_p, _IP, _IP, C.POINTER(C.c_longlong), _IP,

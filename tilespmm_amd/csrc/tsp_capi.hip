@@ -45,7 +45,8 @@ int tsp_device_init(int device_id)
     e = hipGetDeviceProperties(&p, device_id);
     if (e != hipSuccess) return (int)e;
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0) return TSP_ENODEV;
-    return TSP_OK;
+    // per-device address of the allocation-free entry points' scratch
+    return tsp::scratch_init_current_device(nullptr);
 }
 
 int tsp_device_probe(int device_id, tsp_device_info *out)

@@ -45,4 +45,8 @@ constexpr int kGatherBlocks = 8192;      // gather probe grid: 8192 x 256 thread
 int launch_gather(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed, void *sink,
                   hipStream_t s);
 
+// Address of the allocation-free entry points' `scratch` array on the current
+// device (looked up once per device; tsp_device_init calls it).
+int scratch_init_current_device(int **ptr);
+
 }  // namespace tsp

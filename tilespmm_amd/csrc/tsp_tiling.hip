@@ -26,7 +26,19 @@
 #include <rocprim/rocprim.hpp>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/tilespmm_hip.h"
+#include "tsp_kernels.h"
+
+// Scratch of the allocation-free packing entry point
+// (tsp_tiles_pack_device_noalloc): per-block partial sums of the per-tile
+// value counts, one int per kPackBlockTiles tiles, plus the total.  Every
+// GPU the library runs on holds one copy for the life of the process; host
+// code uses only its per-device address from hipGetSymbolAddress
+// (tsp::scratch_init_current_device), never this name.
+constexpr int kScratchInts = 1 << 18;                 // 1 MiB
+static __device__ __align__(256) int scratch[kScratchInts];
 
 namespace {
 
@@ -159,24 +171,107 @@ __global__ void popcount_kernel(const unsigned long long *__restrict__ bmp, int 
     cnt[t] = k;
 }
 
-// one thread per tile: the values at the set bits, in bit (row-major) order
+// one thread per tile: the values at the set bits, in bit (row-major) order;
+// writes at or past `cap` elements are dropped
 template <typename V>
 __global__ void pack_kernel(const V *__restrict__ dense, const unsigned long long *__restrict__ bmp,
                             const int *__restrict__ vptr, int tilenum, int words, int slots,
-                            V *__restrict__ pval)
+                            V *__restrict__ pval, long long cap)
 {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= tilenum) return;
-    int o = vptr[t];
+    long long o = vptr[t];
     const V *src = dense + (size_t)t * slots;
     for (int w = 0; w < words; ++w) {
         unsigned long long m = bmp[(size_t)t * words + w];
         while (m) {
             const int b = __ffsll((long long)m) - 1;
-            pval[o++] = src[w * 64 + b];
+            if (o < cap) pval[o] = src[w * 64 + b];
+            ++o;
             m &= m - 1;
         }
     }
+}
+
+// ---- allocation-free packing: a three-pass scan through `scratch` -----------
+// Tiles are taken in blocks of kPackBlockTiles (kPackPer consecutive tiles per
+// thread).  Pass 1 stores each tile's value count in vptr[t] and each block's
+// sum in sums[b]; pass 2 (one workgroup) turns sums[0..nb) into exclusive
+// block offsets and stores the total in sums[nb]; pass 3 turns the counts of
+// each block into exclusive offsets.  The output array vptr doubles as the
+// count buffer, so the only scratch is nb + 1 ints.
+constexpr int kPackPer = 8;
+constexpr int kPackBlockTiles = kThreads * kPackPer;
+
+__global__ __launch_bounds__(kThreads) void pack_count_kernel(const unsigned long long *__restrict__ bmp, int tilenum,
+                                                              int words, int *__restrict__ vptr,
+                                                              int *__restrict__ sums)
+{
+    using BR = rocprim::block_reduce<int, kThreads>;
+    __shared__ typename BR::storage_type st;
+    const long long base = (long long)blockIdx.x * kPackBlockTiles + (long long)threadIdx.x * kPackPer;
+    int s = 0;
+    for (int j = 0; j < kPackPer; ++j) {
+        const long long t = base + j;
+        if (t >= tilenum) break;
+        int k = 0;
+        for (int w = 0; w < words; ++w) k += __popcll(bmp[(size_t)t * words + w]);
+        vptr[t] = k;
+        s += k;
+    }
+    int total = 0;
+    BR().reduce(s, total, st, rocprim::plus<int>());
+    if (threadIdx.x == 0) sums[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(kThreads) void pack_block_scan_kernel(int *__restrict__ sums, int nb)
+{
+    using BS = rocprim::block_scan<int, kThreads>;
+    __shared__ typename BS::storage_type st;
+    int carry = 0;
+    for (int base = 0; base < nb; base += kThreads) {
+        const int i = base + (int)threadIdx.x;
+        const int v = i < nb ? sums[i] : 0;
+        int ex = 0, agg = 0;
+        BS().exclusive_scan(v, ex, 0, agg, st, rocprim::plus<int>());
+        if (i < nb) sums[i] = carry + ex;
+        carry += agg;
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) sums[nb] = carry;
+}
+
+__global__ __launch_bounds__(kThreads) void pack_offsets_kernel(int *__restrict__ vptr, int tilenum,
+                                                                const int *__restrict__ sums)
+{
+    using BS = rocprim::block_scan<int, kThreads>;
+    __shared__ typename BS::storage_type st;
+    const long long base = (long long)blockIdx.x * kPackBlockTiles + (long long)threadIdx.x * kPackPer;
+    int c[kPackPer];
+    int s = 0;
+    for (int j = 0; j < kPackPer; ++j) {
+        const long long t = base + j;
+        c[j] = t < tilenum ? vptr[t] : 0;
+        s += c[j];
+    }
+    int ex = 0;
+    BS().exclusive_scan(s, ex, 0, st, rocprim::plus<int>());
+    int o = sums[blockIdx.x] + ex;
+    for (int j = 0; j < kPackPer; ++j) {
+        const long long t = base + j;
+        if (t < tilenum) vptr[t] = o;
+        o += c[j];
+    }
+}
+
+// vptr[tilenum] = total; zero the nz padding elements after the last value
+template <typename V>
+__global__ void pack_tail_kernel(int *__restrict__ vptr, int tilenum, const int *__restrict__ sums, int nb,
+                                 V *__restrict__ pval, long long cap, int nz)
+{
+    const int total = sums[nb];
+    if (threadIdx.x == 0) vptr[tilenum] = total;
+    if ((int)threadIdx.x < nz && (long long)total + threadIdx.x < cap) pval[(long long)total + threadIdx.x] = V(0);
 }
 
 struct Scratch {
@@ -336,7 +431,80 @@ int tile_create_device(tsp_dev_tiles *out, int rows, int colA, long long nnz, co
 
 }  // namespace
 
+namespace tsp {
+
+// Per-device address of `scratch`, looked up with the device current (each
+// GPU holds its own copy at its own address).
+constexpr int kScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static int *g_scratch_ptr[kScratchDevices];
+
+int scratch_init_current_device(int **ptr)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kScratchDevices) return TSP_EINVAL;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!p) return TSP_EINVAL;
+        g_scratch_ptr[dev] = (int *)p;
+    }
+    if (ptr) *ptr = g_scratch_ptr[dev];
+    return TSP_OK;
+}
+
+}  // namespace tsp
+
 extern "C" {
+
+int tsp_tiles_pack_device_noalloc(int tilenum, int bm, int bn, int prec, const void *d_val,
+                                  const unsigned long long *d_bitmap, void *d_pval, long long pval_capacity,
+                                  int *d_vptr, long long *nvals, void *stream)
+{
+    if (tilenum < 0 || !nvals || !d_vptr || pval_capacity < 0 || (bm != 64 && bm != 16 && bm != 8) || bn <= 0 ||
+        bn > 32)
+        return TSP_EINVAL;
+    if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
+    if (pval_capacity > 0 && !d_pval) return TSP_EINVAL;
+    if (tilenum > 0 && (!d_bitmap || !d_val)) return TSP_EINVAL;
+    if ((long long)tilenum > TSP_PACK_NOALLOC_MAX_TILES) return TSP_EINVAL;
+    int *sums = nullptr;
+    int st = tsp::scratch_init_current_device(&sums);
+    if (st) return st;
+    hipStream_t s = (hipStream_t)stream;
+    const int words = (bm * bn + 63) / 64;
+    const int nb = (int)(((long long)tilenum + kPackBlockTiles - 1) / kPackBlockTiles);
+    if (nb > 0) pack_count_kernel<<<nb, kThreads, 0, s>>>(d_bitmap, tilenum, words, d_vptr, sums);
+    pack_block_scan_kernel<<<1, kThreads, 0, s>>>(sums, nb);
+    if (nb > 0) pack_offsets_kernel<<<nb, kThreads, 0, s>>>(d_vptr, tilenum, sums);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    int total = 0;
+    if ((e = hipMemcpyAsync(&total, sums + nb, sizeof(int), hipMemcpyDeviceToHost, s)) != hipSuccess) return (int)e;
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return (int)e;
+    *nvals = total;
+    // the values plus 4 elements of zero padding (the kernels' packed loads
+    // may read past the last value) must fit
+    if ((long long)total + 4 > pval_capacity) return TSP_EINVAL;
+    if (prec == TSP_PREC_FP16) {
+        pack_tail_kernel<uint16_t><<<1, 64, 0, s>>>(d_vptr, tilenum, sums, nb, (uint16_t *)d_pval, pval_capacity, 4);
+        if (tilenum > 0)
+            pack_kernel<uint16_t><<<nblocks(tilenum), kThreads, 0, s>>>(
+                (const uint16_t *)d_val, d_bitmap, d_vptr, tilenum, words, bm * bn, (uint16_t *)d_pval, pval_capacity);
+    } else {
+        pack_tail_kernel<uint32_t><<<1, 64, 0, s>>>(d_vptr, tilenum, sums, nb, (uint32_t *)d_pval, pval_capacity, 4);
+        if (tilenum > 0)
+            pack_kernel<uint32_t><<<nblocks(tilenum), kThreads, 0, s>>>(
+                (const uint32_t *)d_val, d_bitmap, d_vptr, tilenum, words, bm * bn, (uint32_t *)d_pval, pval_capacity);
+    }
+    if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(s)) != hipSuccess) return (int)e;
+    return TSP_OK;
+}
+
 
 int tsp_tile_create_device(tsp_dev_tiles *out, int rows, int colA, long long nnz, const int *d_ptr,
                            const int *d_idx, const void *d_val, int BM, int BN, int prec, void *stream)
@@ -398,10 +566,10 @@ int tsp_tiles_pack_device(int tilenum, int bm, int bn, int prec, const void *d_v
     if (tilenum > 0) {
         if (prec == TSP_PREC_FP16)
             pack_kernel<uint16_t><<<nblocks(tilenum), kThreads, 0, s>>>(
-                (const uint16_t *)d_val, d_bitmap, vptr, tilenum, words, bm * bn, (uint16_t *)pv);
+                (const uint16_t *)d_val, d_bitmap, vptr, tilenum, words, bm * bn, (uint16_t *)pv, total);
         else
             pack_kernel<uint32_t><<<nblocks(tilenum), kThreads, 0, s>>>(
-                (const uint32_t *)d_val, d_bitmap, vptr, tilenum, words, bm * bn, (uint32_t *)pv);
+                (const uint32_t *)d_val, d_bitmap, vptr, tilenum, words, bm * bn, (uint32_t *)pv, total);
     }
     if ((e = hipGetLastError()) != hipSuccess || (e = hipStreamSynchronize(s)) != hipSuccess) {
         (void)hipFree(pv);
