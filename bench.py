@@ -363,7 +363,8 @@ def measure(tsp, hip, config, prec, colB, args, headline):
 
     # the dominant kernel's instantiation spmm_kernel<BM, W, PREC, S, PK>; the
     # profiled HBM traffic applies only to the same instantiation and hot rows
-    kname = (f"spmm_kernel<{dom}, {dk['chunk_width']}, {prec}, {dk['stages']}, "
+    # (plans launch tf32 on operands they rounded once: kernel precision code 2)
+    kname = (f"spmm_kernel<{dom}, {dk['chunk_width']}, {2 if prec == 1 else 0}, {dk['stages']}, "
              f"{'true' if dk['format'] == 'packed' else 'false'}>")
     traffic, traffic_note = None, "no profile of this workload in profiles/"
     prof = os.path.join(ROOT, "profiles", f"traffic_config{config}_{pname}_{colB}.json")

@@ -159,6 +159,13 @@ int tsp_gen_config(int config, int prec, int colB, unsigned long long seed, int 
 /* Only the structure of config (no values). */
 int tsp_gen_structure(int config, unsigned long long seed, int *rows, int *cols, long long *nnz,
                       int **rowptr, int **colidx);
+/* The configuration-5 RMAT generator at any scale: 2^scale vertices, `edges`
+ * directed edges with quadrant probabilities (a, b, c, d) = (.57, .19, .19,
+ * .05), symmetrised, duplicates removed, self-loops kept, columns ascending;
+ * values 1/deg(row) in prec's storage type.  Configuration 5 is scale 22,
+ * 2^26 edges, seed 20260005.  Free the arrays with tsp_free_host. */
+int tsp_gen_rmat(int scale, long long edges, unsigned long long seed, int prec, int *rows,
+                 long long *nnz, int **rowptr, int **colidx, void **val);
 /* Fill n values of prec from seed: dist 0 = U[-1,1), 1 = N(0,1). */
 int tsp_gen_values(int prec, int dist, unsigned long long seed, size_t n, void *out);
 /* padded width the kernels see: colB <= 32 ? 32 : roundup(colB, 64). */

@@ -172,6 +172,20 @@ int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const 
                            int c_rows, void *stream, int w, int stages, int tasks_per_wave, int order,
                            int placement);
 
+/* tsp_spmm_launch_placed with flags.  TSP_LAUNCH_OPERANDS_TF32 (tf32 only):
+ * the caller guarantees that every A value and every B value the launch
+ * reads is a tf32 value already (low 13 mantissa bits zero, or Inf/NaN),
+ * e.g. after tsp_round_tf32_device; the kernels then skip their
+ * per-operand rounding and give the same result as the rounding launch.
+ * The plan rounds its copies of A and B once when they enter it and
+ * launches this way.  No counterpart in the reference. */
+#define TSP_LAUNCH_OPERANDS_TF32 1
+int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
+                       const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,
+                       const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,
+                       int c_rows, void *stream, int w, int stages, int tasks_per_wave, int order,
+                       int placement, int flags);
+
 /* Per-class entry points with the reference dispatcher names
  * (src/tilespmm_cuda.h:1634, :1672, :1710) and argument order. */
 int tsp_switch_v64(int prec, int rowblkblock, int colB_p, const void *d_val,
@@ -192,6 +206,16 @@ int tsp_switch_v8(int prec, int rowblkblock, int colB_p, const void *d_val,
 int tsp_vendor_spmm(int prec, int m, int k, long long nnz, const int *rowptr, const int *colidx,
                     const void *val, int n, int ldb, const void *h_B, float *h_C, int warmup,
                     int repeat, double *pre_ms, double *ms);
+
+/* The kernels' tf32 operand rounding, run on the host over n fp32 bit
+ * patterns: nearest-even to 10 mantissa bits; Inf and NaN unchanged.  The
+ * reference gives raw fp32 bits to its tf32 tensor-core instructions
+ * (src/utils.h:233-246); this build rounds explicitly, and NaN still
+ * propagates. */
+int tsp_round_tf32_bits(const uint32_t *in, uint32_t *out, size_t n);
+/* The same rounding in place over n fp32 values in device memory,
+ * asynchronous on `stream`. */
+int tsp_round_tf32_device(void *d_x, size_t n, void *stream);
 
 /* A plain streaming copy kernel (dst = src, 16-byte vectors), used to
  * calibrate HBM byte counters and the achievable copy bandwidth. */

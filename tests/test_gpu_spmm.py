@@ -477,3 +477,157 @@ def test_hot_row_device_helpers(gpu):
     finally:
         for b in bufs.values():
             b.free()
+
+
+def test_tf32_raw_fp32_inputs_error_bound(gpu, orc):
+    """fp32 inputs that are NOT tf32 values.  The kernels round both operands
+    to tf32 (nearest-even, relative error <= 2^-11 each), so against the fp64
+    product of the UNROUNDED inputs every entry is within
+    (2 * 2^-11 + 2^-22 + fp32 accumulation) of sum |A||B|: bounded here by
+    1.0e-3, and checked to be above the exact-input tolerance (the rounding
+    really happens).  The reference instead hands raw fp32 bits to tf32
+    tensor cores (src/utils.h:233-246), which ignore the low 13 bits, so its
+    per-operand error reaches 2^-10.  Against the oracle on tf32-rounded
+    inputs the result stays within the 1e-4 tf32 tolerance."""
+    tsp = gpu
+    rng = np.random.default_rng(2024)
+    A = random_matrix(tsp, rng, 600, 500, 50, 1, heavy_rows=3)
+    A.val = (rng.uniform(-1, 1, A.nnz) * (1 + rng.random(A.nnz) * 2 ** -12)).astype(np.float32)
+    assert ((A.val.view(np.uint32) & 0x1FFF) != 0).mean() > 0.99
+    colB = 64
+    B, cbp = random_b(tsp, rng, A.cols, colB, 1)
+    B[:, :colB] = (B[:, :colB] * (1 + rng.random((A.cols, colB)) * 2 ** -12)).astype(np.float32)
+    Cg, _ = run_tiles(tsp, A, B, cbp, 2.0, 1.5, (16, 16, 16))
+    a = A.val.astype(np.float64)
+    b = B[:, :colB].astype(np.float64)
+    Craw = orc.spmm_f64(A.rows, A.rowptr, A.colidx, a, b, colB)
+    Cabs = orc.spmm_f64(A.rows, A.rowptr, A.colidx, np.abs(a), np.abs(b), colB)
+    err = np.abs(Cg[:, :colB] - Craw) / (Cabs + 1e-30)
+    say(f"tf32 on raw fp32 inputs: max normalised error {err.max():.3e}")
+    assert err.max() <= 1.0e-3
+    assert err.max() > 1e-4
+    Cref, Cabs_r = reference(orc, A, B, colB)
+    assert_close(Cg[:, :colB], Cref, Cabs_r, 1, "tf32 vs oracle on rounded inputs")
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+def test_nan_and_inf_propagate(gpu, prec):
+    """Non-finite operands propagate as through the reference's raw operands;
+    NaN payloads that a rounding bias would carry into the exponent or sign
+    (0x7f800001, 0x7fffffff) stay NaN in the tf32 path.
+    * A NaN in A reaches exactly its own row of C (every column).
+    * A NaN / +Inf in B row c, column j reaches C[r, j] of every row r whose
+      CSR row holds c (NaN / +Inf with positive operands) -- and, because the
+      tiles are dense zero-padded blocks (as the reference's are), also
+      C[r', j] of the other rows r' of those row-blocks as NaN (0 * Inf and
+      0 * NaN are NaN).  Every other entry stays finite."""
+    tsp = gpu
+    rng = np.random.default_rng(9)
+    rows, cols, colB = 256, 128, 64
+    lens = np.full(rows, 4)
+    rp = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    ci = np.concatenate([np.sort(rng.choice(cols, 4, replace=False)) for _ in range(rows)]).astype(np.int32)
+    v = rng.uniform(0.5, 1, rp[-1]).astype(np.float32)
+    bv = rng.uniform(0.5, 1, (cols, colB)).astype(np.float32)
+    if prec == 0:
+        val = v.astype(np.float16).view(np.uint16)
+        B = bv.astype(np.float16).view(np.uint16)
+        nan_a, nan_b, inf_b = np.uint16(0x7E01), np.uint16(0x7C01), np.uint16(0x7C00)
+    else:
+        val = v.copy()
+        B = bv.copy()
+        nan_a, nan_b, inf_b = np.uint32(0x7FFFFFFF), np.uint32(0x7F800001), np.uint32(0x7F800000)
+    vb = val.view(np.uint16 if prec == 0 else np.uint32)
+    Bb = B.view(np.uint16 if prec == 0 else np.uint32)
+    vb[rp[10] + 1] = nan_a                 # row 10
+    cnan, cinf = 77, 91
+    Bb[cnan, 5] = nan_b
+    Bb[cinf, 9] = inf_b
+    A = tsp.Csr(rows, cols, rp, ci, val, prec)
+    for th in ((8, 8, 8), (128, 128, 128)):
+        Cg, _ = run_tiles(tsp, A, B, colB, 2.0, 1.5, th)
+        C = Cg[:, :colB]
+        has = lambda c: np.array([c in ci[rp[r]:rp[r + 1]] for r in range(rows)])
+        other = np.ones(rows, bool)
+        other[10] = False
+        assert np.isnan(C[10]).all()
+        assert np.isnan(C[has(cnan) & other, 5]).all()
+        assert np.isposinf(C[has(cinf) & other, 9]).all()
+        # rows of C other than 10 are finite outside columns 5 and 9, and
+        # columns 5 / 9 hold no Inf / NaN of the wrong kind
+        rest = np.delete(np.arange(colB), [5, 9])
+        assert np.isfinite(C[other][:, rest]).all()
+        assert not np.isinf(C[other, 5]).any()
+        assert not np.isneginf(C[other, 9]).any()
+
+
+@pytest.mark.parametrize("bm", [64, 16, 8])
+def test_tf32_prerounded_launch_matches_rounding_launch(gpu, orc, bm):
+    """The plan rounds its copies of A and B to tf32 once and launches with
+    TSP_LAUNCH_OPERANDS_TF32 (no per-operand rounding in the kernel); the
+    reference-compatible launch (tsp_switch_v*) rounds in the kernel.  On raw
+    fp32 inputs, NaN included, both give the same C bit for bit (unsplit
+    schedule: no atomics), and tsp_round_tf32_device equals the host
+    rounding."""
+    tsp = gpu
+    hip, _ = tsp.load()
+    rng = np.random.default_rng(40 + bm)
+    A = random_matrix(tsp, rng, 3 * bm + 5, 400, 40, 1)
+    A.val = (rng.uniform(-1, 1, A.nnz) * (1 + rng.random(A.nnz) * 2 ** -12)).astype(np.float32)
+    A.val.view(np.uint32)[3] = 0x7FFFFFFF                                   # NaN whose rounding would carry
+    colB = 64
+    B, cbp = random_b(tsp, rng, A.cols, colB, 1)
+    B[:, :colB] = (B[:, :colB] * (1 + rng.random((A.cols, colB)) * 2 ** -12)).astype(np.float32)
+    sub = tsp.Csr(A.rows, A.cols, A.rowptr, A.colidx, A.val, 1)
+    sub.orig_row = np.arange(A.rows, dtype=np.int32)
+    t = tsp.tile_create(sub, A.cols, bm, 1)
+    arr = t.arrays()
+    rows, cs = tsp.pretreatment(t, 1 << 20)
+    assert not (rows & 0x80000000).any()
+    bufs = {}
+
+    def up(name, a):
+        p = C.c_void_p()
+        assert hip.tsp_malloc(C.byref(p), max(a.nbytes, 4)) == 0
+        assert hip.tsp_memcpy_h2d(p, a.ctypes.data_as(C.c_void_p), a.nbytes) == 0
+        bufs[name] = p
+        return p
+
+    def down(name, like):
+        out = np.zeros_like(like)
+        assert hip.tsp_memcpy_d2h(out.ctypes.data_as(C.c_void_p), bufs[name], out.nbytes) == 0
+        return out
+
+    switch = {64: hip.tsp_switch_v64, 16: hip.tsp_switch_v16, 8: hip.tsp_switch_v8}[bm]
+    try:
+        dense = np.ascontiguousarray(arr["dense"]).view(np.float32)
+        up("val", dense); up("col", arr["tile_colidx"]); up("rows", rows); up("cs", cs); up("B", B)
+        up("valr", dense); up("Br", B)
+        Cz = np.zeros((A.rows, cbp), dtype=np.float32)
+        up("C1", Cz); up("C2", Cz)
+        assert switch(1, len(rows), cbp, bufs["val"], bufs["rows"], bufs["cs"], bufs["B"], bufs["C1"], bufs["col"],
+                      A.rows, None) == 0
+        assert hip.tsp_round_tf32_device(bufs["valr"], dense.size, None) == 0
+        assert hip.tsp_round_tf32_device(bufs["Br"], B.size, None) == 0
+        assert hip.tsp_device_sync() == 0
+        host_r = np.zeros(dense.size, np.uint32)
+        assert hip.tsp_round_tf32_bits(dense.ctypes.data_as(C.c_void_p), host_r.ctypes.data_as(C.c_void_p),
+                                       dense.size) == 0
+        assert np.array_equal(down("valr", dense).view(np.uint32).reshape(-1), host_r)
+        assert hip.tsp_spmm_launch_ex(bm, 1, len(rows), cbp, bufs["valr"], None, None, bufs["rows"], bufs["cs"],
+                                      bufs["Br"], bufs["C2"], bufs["col"], A.rows, None, 0, 0, 0, 0, 0, 1) == 0
+        assert hip.tsp_device_sync() == 0
+        c1, c2 = down("C1", Cz), down("C2", Cz)
+        assert np.array_equal(c1.view(np.uint32), c2.view(np.uint32))
+        row3 = int(np.searchsorted(A.rowptr, 3, side="right") - 1)
+        assert np.isnan(c1[row3, :colB]).all()
+        ok = np.ones(A.rows, bool)
+        ok[row3] = False
+        Cref, Cabs = reference(orc, A, B, colB)
+        assert_close(c1[ok, :colB], Cref[ok], Cabs[ok], 1, f"bm {bm}")
+        # an unknown flag is refused before any launch
+        assert hip.tsp_spmm_launch_ex(bm, 1, len(rows), cbp, bufs["valr"], None, None, bufs["rows"], bufs["cs"],
+                                      bufs["Br"], bufs["C2"], bufs["col"], A.rows, None, 0, 0, 0, 0, 0, 2) != 0
+    finally:
+        for p in bufs.values():
+            hip.tsp_free(p)

@@ -108,7 +108,7 @@ def test_device_tiles_dc2(gpu, orc, dc2_path):
             check_vs_oracle(gpu, orc, m, n, rp, ci, prec, bm, store, bits, "dc2")
 
 
-@pytest.mark.parametrize("config,prec", [(2, 0), (3, 1), (4, 0), (3, 0), (5, 0)])
+@pytest.mark.parametrize("config,prec", [(2, 0), (3, 1), (4, 0), (3, 0), (5, 0), (5, 1)])
 def test_device_tiles_config_classes(gpu, config, prec):
     """Every class sub-CSR of a full synthetic config, split at the shipped
     policy's (gamma, delta): device tiles == host tiles (the host conversion

@@ -326,3 +326,33 @@ def test_gen_c4_blocksparse(tsp):
     nnz = int(rp[-1])
     # singletons that land inside one of the blocks (2% of the area) are dropped
     assert abs(nnz - (335544 * 256 + 429497 * 0.98)) < 1000
+
+
+def test_round_tf32_bits_special_values(tsp, orc):
+    """The kernels' tf32 operand rounding (tsp_round_tf32_bits, the same
+    function the device code calls) equals the oracle's nearest-even rounding
+    on finite values and passes Inf and every NaN through unchanged (a bias
+    added to a NaN would carry into the exponent or sign: 0x7f800001 -> Inf,
+    0x7fffffff -> -0)."""
+    import ctypes as C
+    hip = tsp.load()[0]
+    special = np.array([0x00000000, 0x80000000, 0x00000001, 0x00001000, 0x00003000, 0x00002fff, 0x3f801000,
+                        0x3f803000, 0x7f7fe000, 0x7f7fefff, 0x7f7ff000, 0x7f7fffff, 0xff7fffff, 0x7f800000,
+                        0xff800000, 0x7f800001, 0x7f801000, 0x7fc00000, 0x7fffe000, 0x7ffff000, 0x7fffffff,
+                        0xffffffff, 0xff800001, 0xffc00001], dtype=np.uint32)
+    rnd = np.random.default_rng(3).integers(0, 2 ** 32, 200000, dtype=np.uint64).astype(np.uint32)
+    x = np.concatenate([special, rnd])
+    out = np.zeros_like(x)
+    assert hip.tsp_round_tf32_bits(x.ctypes.data_as(C.c_void_p), out.ctypes.data_as(C.c_void_p), x.size) == 0
+    exp_all_ones = (x & 0x7F800000) == 0x7F800000
+    want = orc.round_tf32_array(x.view(np.float32)).view(np.uint32)
+    assert np.array_equal(out[~exp_all_ones], want[~exp_all_ones])
+    assert np.array_equal(out[exp_all_ones], x[exp_all_ones])          # Inf and NaN unchanged
+    f = out.view(np.float32)
+    assert np.isnan(f[np.isnan(x.view(np.float32))]).all()
+    # hand values: ties to even, the largest finite value rounds to Inf
+    hand = dict(zip(special.tolist(), out[: special.size].tolist()))
+    assert hand[0x00001000] == 0x00000000 and hand[0x00003000] == 0x00004000
+    assert hand[0x3f801000] == 0x3f800000 and hand[0x3f803000] == 0x3f804000
+    assert hand[0x7f7fffff] == 0x7f800000 and hand[0xff7fffff] == 0xff800000
+    assert hand[0x7f7fefff] == 0x7f7fe000 and hand[0x7f7ff000] == 0x7f800000

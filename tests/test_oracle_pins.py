@@ -428,3 +428,44 @@ def test_round_tf32_array_matches_scalar(orc):
     got = orc.round_tf32_array(x)
     want = np.array([orc.round_tf32(float(v)) for v in x], dtype=np.float32)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_optimal_th_colB32_block_packing(orc):
+    # colB 32: 8- and 16-row kernels pack four tasks per block, total_block =
+    # ceil(total_chunk / 4); 64-row tiles do not (src/csr2tile.h:592-597).
+    # One SM, one resident block: cap = 1, lambda_L2 = 4096/2^20; atom_pen =
+    # 0.01/32*32 = 0.01; two row-blocks of 20 tiles (Tmax 24).
+    #   TH  8: chunks 6, per 7, atoms 4   BM 8/16: 2 blocks -> 2*8 + 7 = 23.05
+    #                                      BM 64:   6 blocks -> 6*8 + 7 = 55.05
+    #   TH 16: chunks 4, per 10, atoms 2  BM 8/16: 1 -> 16 + 10 = 26.02; BM 64: 64 + 10 = 74.02
+    #   TH 24: chunks 2, per 20            BM 8/16: 1 -> 24 + 20 = 44;    BM 64: 48 + 20 = 68
+    p = params(sm_count=1, threads_per_sm=64)
+    tp = np.array([0, 20, 40], dtype=np.int32)
+    for bm in (8, 16):
+        n, top4 = orc.optimal_th(bm, 32, tp, p)
+        assert n == 3 and top4.tolist() == [8, 16, 24, 8], bm
+    n, top4 = orc.optimal_th(64, 32, tp, p)
+    assert n == 3 and top4.tolist() == [8, 24, 16, 8]
+    # colB 64 goes through the column-grid branch: same as the 64-row order
+    n, top4 = orc.optimal_th(16, 64, tp, p)
+    assert n == 3 and top4.tolist() == [8, 24, 16, 8]
+
+
+def test_optimal_th_long_tail_atomic_discount(orc):
+    # Nine row-blocks of 1 tile and one of 100: max 100 > 5 * mean 10.9, so the
+    # atomic weight is multiplied by 0.04 (src/csr2tile.h:549).  lambda_atom 2
+    # at colB 64: atom_pen = 2/32*64 = 4, discounted 0.16.  22000 resident
+    # blocks and 1-byte iterations make the throughput and L2 terms < 0.03, so
+    # the cost is max_chunk + atom_pen * (tasks - 1) of the long row-block:
+    #   TH:    8     16    24    32    40    56    104   (48, 64-96 repeat a task count)
+    #   per:   8     15    20    25    34    50    100
+    #   atoms: 12    6     4     3     2     1     0
+    # discounted: 9.92 15.96 20.64 25.48 34.32 50.16 100  -> 8, 16, 24, 32
+    # full 4:     56   39    36    37    42    54    100  -> 24, 32, 16, 40
+    p = params(sm_count=1000, iteration_bytes=1, lambda_atom=2.0)
+    tp = np.concatenate([[0], np.cumsum([1] * 9 + [100])]).astype(np.int32)
+    n, top4 = orc.optimal_th(16, 64, tp, p)
+    assert n == 7 and top4.tolist() == [8, 16, 24, 32]
+    # without the long tail (the 100-tile block alone) the full weight applies
+    n, top4 = orc.optimal_th(16, 64, np.array([0, 100], dtype=np.int32), p)
+    assert top4.tolist() == [24, 32, 16, 40]

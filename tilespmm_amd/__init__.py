@@ -163,12 +163,16 @@ HIP_SYMBOLS = {
                                          C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int]),
     "tsp_spmm_launch_placed": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P,
                                          C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "tsp_spmm_launch_ex": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P,
+                                     C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "tsp_switch_v64": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v16": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v8": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_vendor_spmm": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_longlong, _P, _P, _P, C.c_int,
                                   C.c_int, _P, _P, C.c_int, C.c_int, C.POINTER(C.c_double),
                                   C.POINTER(C.c_double)]),
+    "tsp_round_tf32_bits": (C.c_int, [_P, _P, C.c_size_t]),
+    "tsp_round_tf32_device": (C.c_int, [_P, C.c_size_t, _P]),
     "tsp_copy_kernel": (C.c_int, [_P, _P, C.c_size_t, _P]),
     "tsp_gather_kernel": (C.c_int, [_P, C.c_size_t, C.c_int, C.c_int, C.c_uint, _P, _P]),
     "tsp_colidx_count": (C.c_int, [_P, C.c_longlong, C.c_int, _P, C.c_int, _P, _P]),
@@ -209,6 +213,8 @@ HOST_SYMBOLS = {
                                  C.POINTER(C.c_void_p), _IP, C.POINTER(C.c_void_p)]),
     "tsp_gen_structure": (C.c_int, [C.c_int, C.c_ulonglong, _IP, _IP, C.POINTER(C.c_longlong),
                                     C.POINTER(_IP), C.POINTER(_IP)]),
+    "tsp_gen_rmat": (C.c_int, [C.c_int, C.c_longlong, C.c_ulonglong, C.c_int, _IP, C.POINTER(C.c_longlong),
+                               C.POINTER(_IP), C.POINTER(_IP), C.POINTER(C.c_void_p)]),
     "tsp_gen_values": (C.c_int, [C.c_int, C.c_int, C.c_ulonglong, C.c_size_t, _P]),
     "tsp_colB_padded": (C.c_int, [C.c_int]),
     "tsp_plan_create": (C.c_int, [C.POINTER(C.c_void_p), C.c_int, C.POINTER(Tile_matrix),
@@ -351,6 +357,17 @@ def gen_config(config: int, prec: int = -1, colB: int = -1, seed: int = 0):
             _take(v, nnz.value, dt), prec)
     B = _take(b, cols.value * cbp.value, dt).reshape(cols.value, cbp.value)
     return A, B, colB, cbp.value
+
+
+def gen_rmat(scale: int, edges: int, seed: int, prec: int):
+    """RMAT graph of the configuration-5 generator at any scale (Csr, values 1/deg)."""
+    _, host = load()
+    rows, nnz = C.c_int(), C.c_longlong()
+    rp, ci, v = _IP(), _IP(), C.c_void_p()
+    _check("tsp_gen_rmat", host.tsp_gen_rmat(scale, edges, seed, prec, C.byref(rows), C.byref(nnz), C.byref(rp),
+                                             C.byref(ci), C.byref(v)))
+    return Csr(rows.value, rows.value, _take(rp, rows.value + 1, np.int32), _take(ci, nnz.value, np.int32),
+               _take(v, nnz.value, _vdtype(prec)), prec)
 
 
 def gen_structure(config: int, seed: int = 0):

@@ -261,6 +261,17 @@ int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const 
                            int c_rows, void *stream, int w, int stages, int tasks_per_wave, int order,
                            int placement)
 {
+    return tsp_spmm_launch_ex(bm, prec, rowblkblock, colB_p, d_val, d_bitmap, d_vptr, d_rows, d_colstart, d_B, d_C,
+                              d_colidx, c_rows, stream, w, stages, tasks_per_wave, order, placement, 0);
+}
+
+int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
+                       const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,
+                       const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,
+                       int c_rows, void *stream, int w, int stages, int tasks_per_wave, int order,
+                       int placement, int flags)
+{
+    if (flags & ~TSP_LAUNCH_OPERANDS_TF32) return TSP_EINVAL;
     if (bm != 64 && bm != 16 && bm != 8) return TSP_EINVAL;
     if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
     if (colB_p != 32 && (colB_p <= 0 || colB_p % 64 != 0)) return TSP_EINVAL;
@@ -270,7 +281,8 @@ int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const 
     if (w > 0 && (colB_p % w != 0 || !tsp::valid_variant(bm, w, stages > 0 ? stages : 1))) return TSP_EINVAL;
     if (rowblkblock == 0) return TSP_OK;
     if (!d_val || !d_rows || !d_colstart || !d_B || !d_C || !d_colidx) return TSP_EINVAL;
-    return tsp::launch(bm, prec, rowblkblock, colB_p, d_val, d_bitmap, d_vptr, d_rows, d_colstart, d_B,
+    const int kprec = prec == TSP_PREC_TF32 && (flags & TSP_LAUNCH_OPERANDS_TF32) ? tsp::kPrecTf32Exact : prec;
+    return tsp::launch(bm, kprec, rowblkblock, colB_p, d_val, d_bitmap, d_vptr, d_rows, d_colstart, d_B,
                        d_C, d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave, order,
                        placement);
 }
@@ -312,6 +324,30 @@ int tsp_switch_v8(int prec, int rowblkblock, int colB_p, const void *d_val, cons
 {
     return tsp_spmm_launch(8, prec, rowblkblock, colB_p, d_val, d_rows, d_colstart, d_B, d_C,
                            d_colidx, c_rows, stream);
+}
+
+namespace tsp {
+__global__ __launch_bounds__(256) void round_tf32_kernel(uint32_t *__restrict__ x, size_t n)
+{
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) x[i] = round_tf32_bits(x[i]);
+}
+}  // namespace tsp
+
+int tsp_round_tf32_device(void *d_x, size_t n, void *stream)
+{
+    if (n && !d_x) return TSP_EINVAL;
+    if (n == 0) return TSP_OK;
+    const size_t b = (n + 255) / 256;
+    tsp::round_tf32_kernel<<<(unsigned)(b < 16384 ? b : 16384), 256, 0, (hipStream_t)stream>>>((uint32_t *)d_x, n);
+    return (int)hipGetLastError();
+}
+
+int tsp_round_tf32_bits(const uint32_t *in, uint32_t *out, size_t n)
+{
+    if (n && (!in || !out)) return TSP_EINVAL;
+    for (size_t i = 0; i < n; ++i) out[i] = tsp::round_tf32_bits(in[i]);
+    return TSP_OK;
 }
 
 int tsp_copy_kernel(void *dst, const void *src, size_t bytes, void *stream)

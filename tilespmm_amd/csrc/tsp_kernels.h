@@ -3,6 +3,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+#include <stdint.h>
 
 namespace tsp {
 
@@ -11,9 +12,25 @@ constexpr int kBlockThreads = 64 * kWavesPerBlock;
 
 // Tile width BN for a row-block height BM and precision (fp16: 64->32,
 // 16->16, 8->16; tf32: 64->16, 16->8, 8->8), as src/main.cu:267-275 fixes it.
+// Internal precision code of tf32 launches whose operands are tf32 values
+// already (the kernels then skip the per-operand rounding); tile shapes are
+// those of TSP_PREC_TF32.
+constexpr int kPrecTf32Exact = 2;
+
 constexpr __host__ __device__ int tile_bn(int bm, int prec)
 {
     return prec == 0 ? (bm == 64 ? 32 : 16) : (bm == 64 ? 16 : 8);
+}
+
+// fp32 bits rounded to tf32 (10 mantissa bits), nearest-even.  Inf and NaN
+// pass unchanged: adding the rounding bias to a NaN would carry its payload
+// into the exponent or the sign (0x7f800001 -> Inf, 0x7fffffff -> -0), while
+// the reference's tensor cores see the raw NaN and propagate it.  Shared by
+// the kernels and the host-callable tsp_round_tf32_bits.
+__host__ __device__ inline uint32_t round_tf32_bits(uint32_t x)
+{
+    const uint32_t r = (x + 0xfffu + ((x >> 13) & 1u)) & 0xffffe000u;
+    return (x & 0x7f800000u) == 0x7f800000u ? x : r;
 }
 
 // Placement of a launch's workgroups on the XCDs.  The hardware deals

@@ -61,11 +61,6 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint32_t round_tf32_bits(uint32_t x)
-{
-    return (x + 0xfffu + ((x >> 13) & 1u)) & 0xffffe000u;
-}
-
 // Wave-uniform read-only data (schedule, column indices) is read through the
 // constant address space so the loads become scalar (SMEM) loads into SGPRs:
 // they are counted by lgkmcnt and never make a wave wait on its in-flight
@@ -104,6 +99,11 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     int c_rows, int placement)
 {
     constexpr bool F16 = PREC == TSP_PREC_FP16;
+    // tf32 operands are rounded in registers, unless the launch guarantees
+    // they are tf32 values already (kPrecTf32Exact: the plan rounds its copies
+    // of A and B once when they enter it)
+    constexpr bool RND = PREC == TSP_PREC_TF32;
+    auto rnd = [](uint32_t x) { return RND ? round_tf32_bits(x) : x; };
     constexpr int BN = tile_bn(BM, PREC);
     constexpr int VV = F16 ? 8 : 4;          // values per 16-byte vector
     constexpr int VPR = W / VV;              // vectors per panel row
@@ -224,7 +224,7 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
             dst[0][1] = bits.y;
         } else {
 #pragma unroll
-            for (int j = 0; j < NVAL; ++j) dst[0][j] = round_tf32_bits(__float_as_uint(o[j]));
+            for (int j = 0; j < NVAL; ++j) dst[0][j] = rnd(__float_as_uint(o[j]));
         }
     };
     auto load_a = [&](int t, const PMeta &m, uint32_t (&dst)[RG][AW]) {
@@ -252,11 +252,11 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
                 const float *p = tile + r * BN + KS * lq;
                 if constexpr (KS == 2) {
                     const u2 x = *(const u2 *)p;
-                    dst[g][0] = round_tf32_bits(x.x); dst[g][1] = round_tf32_bits(x.y);
+                    dst[g][0] = rnd(x.x); dst[g][1] = rnd(x.y);
                 } else {
                     const u4 x = *(const u4 *)p;
-                    dst[g][0] = round_tf32_bits(x.x); dst[g][1] = round_tf32_bits(x.y);
-                    dst[g][2] = round_tf32_bits(x.z); dst[g][3] = round_tf32_bits(x.w);
+                    dst[g][0] = rnd(x.x); dst[g][1] = rnd(x.y);
+                    dst[g][2] = rnd(x.z); dst[g][3] = rnd(x.w);
                 }
             }
         }
@@ -397,9 +397,9 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             u4 x = src[i];
-            if constexpr (!F16) {
-                x.x = round_tf32_bits(x.x); x.y = round_tf32_bits(x.y);
-                x.z = round_tf32_bits(x.z); x.w = round_tf32_bits(x.w);
+            if constexpr (RND) {
+                x.x = rnd(x.x); x.y = rnd(x.y);
+                x.z = rnd(x.z); x.w = rnd(x.w);
             }
             VT *d = lds + prow[i] * LDSW + pcol[i];
             if constexpr (F16) {
@@ -542,14 +542,16 @@ const void *select_kernel(int bm, int prec, int w, int s, bool packed)
 {
 #define TSP_K(BMv, Wv, Sv)                                                                            \
     if (!packed && bm == BMv && w == Wv && s == Sv)                                                   \
-        return prec == TSP_PREC_FP16 ? (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, false>  \
-                                     : (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, false>;
+        return prec == TSP_PREC_FP16   ? (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, false> \
+               : prec == kPrecTf32Exact ? (const void *)&spmm_kernel<BMv, Wv, kPrecTf32Exact, Sv, false> \
+                                       : (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, false>;
     TSP_FOR_EACH_VARIANT(TSP_K)
 #undef TSP_K
 #define TSP_K(BMv, Wv, Sv)                                                                            \
     if (packed && bm == BMv && w == Wv && s == Sv)                                                    \
-        return prec == TSP_PREC_FP16 ? (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, true>   \
-                                     : (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, true>;
+        return prec == TSP_PREC_FP16   ? (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, true>  \
+               : prec == kPrecTf32Exact ? (const void *)&spmm_kernel<BMv, Wv, kPrecTf32Exact, Sv, true> \
+                                       : (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, true>;
     TSP_FOR_EACH_PACKED_VARIANT(TSP_K)
 #undef TSP_K
     return nullptr;
@@ -595,6 +597,10 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
     if (packed == PKv && bm == BMv && w == Wv && s == Sv) {                                     \
         if (prec == TSP_PREC_FP16)                                                              \
             spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, PKv><<<grid3, kBlockThreads, 0, st>>>(       \
+                ntasks, nchunks, tpw, cm, val, bmp, vptr, rows, colstart, B, C, colidx, colB_p, \
+                c_rows, placement);                                                             \
+        else if (prec == kPrecTf32Exact)                                                        \
+            spmm_kernel<BMv, Wv, kPrecTf32Exact, Sv, PKv><<<grid3, kBlockThreads, 0, st>>>(      \
                 ntasks, nchunks, tpw, cm, val, bmp, vptr, rows, colstart, B, C, colidx, colB_p, \
                 c_rows, placement);                                                             \
         else                                                                                    \

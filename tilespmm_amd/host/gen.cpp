@@ -386,6 +386,35 @@ extern "C" int tsp_gen_structure(int config, unsigned long long seed, int *rows,
     return TSP_OK;
 }
 
+extern "C" int tsp_gen_rmat(int scale, long long edges, unsigned long long seed, int prec, int *rows,
+                            long long *nnz, int **rowptr, int **colidx, void **val)
+{
+    if (scale < 1 || scale > 30 || edges < 0 || (prec != 0 && prec != 1) || !rows || !nnz || !rowptr || !colidx ||
+        !val)
+        return TSP_EINVAL;
+    Csr a;
+    gen_rmat(seed, scale, edges, a);
+    const size_t nz = a.idx.size();
+    *rows = a.rows;
+    *nnz = (long long)nz;
+    *rowptr = tsph::alloc_n<int>(a.ptr.size());
+    *colidx = tsph::alloc_n<int>(nz ? nz : 1);
+    *val = malloc(tsph::val_size(prec) * (nz ? nz : 1));
+    if (!*rowptr || !*colidx || !*val) return TSP_ENOMEM;
+    memcpy(*rowptr, a.ptr.data(), sizeof(int) * a.ptr.size());
+    if (nz) memcpy(*colidx, a.idx.data(), sizeof(int) * nz);
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < a.rows; ++r) {
+        const int deg = a.ptr[(size_t)r + 1] - a.ptr[(size_t)r];
+        for (int k = a.ptr[(size_t)r]; k < a.ptr[(size_t)r + 1]; ++k) {
+            const float x = 1.0f / (float)deg;
+            if (prec == TSP_PREC_FP16) ((uint16_t *)*val)[k] = tsph::f2h(x);
+            else ((float *)*val)[k] = tsph::round_tf32(x);
+        }
+    }
+    return TSP_OK;
+}
+
 extern "C" int tsp_gen_config(int config, int prec, int colB, unsigned long long seed, int *rows,
                               int *cols, long long *nnz, int **rowptr, int **colidx, void **val,
                               int *colB_p_out, void **B)

@@ -128,10 +128,21 @@ static long long packed_values(const Tile_matrix *m)
     return n;
 }
 
+// tf32 plans keep their copies of A and B as tf32 values: rounded once here
+// (nearest-even, Inf/NaN unchanged), so the kernels launch with
+// TSP_LAUNCH_OPERANDS_TF32 and skip the per-operand rounding.
+static int round_tf32_copy(const tsp_plan *p, void *d, size_t n)
+{
+    if (p->prec != TSP_PREC_TF32 || n == 0) return TSP_OK;
+    TSP_TRY(tsp_round_tf32_device(d, n, nullptr));
+    return tsp_device_sync();
+}
+
 static int upload_packed(tsp_plan *p, ClassDev &c)
 {
     if (c.d_pval) return TSP_OK;
     if (c.dev_built) {
+        // packed from the (already rounded) dense tiles
         long long n = 0;
         return tsp_tiles_pack_device(c.m->tilenum, c.m->bm, c.m->bn, p->prec, c.d_val,
                                      (const unsigned long long *)c.d_bmp, &n, &c.d_pval, &c.d_vptr, nullptr);
@@ -167,6 +178,7 @@ static int upload_packed(tsp_plan *p, ClassDev &c)
     }
     TSP_TRY(tsp_malloc(&c.d_pval, pv.size()));
     TSP_TRY(tsp_memcpy_h2d(c.d_pval, pv.data(), pv.size()));
+    TSP_TRY(round_tf32_copy(p, c.d_pval, pv.size() / vs));
     TSP_TRY(tsp_malloc((void **)&c.d_bmp, sizeof(uint64_t) * (size_t)nt * wd));
     TSP_TRY(tsp_memcpy_h2d(c.d_bmp, m->tile_bitmap, sizeof(uint64_t) * (size_t)nt * wd));
     TSP_TRY(tsp_malloc((void **)&c.d_vptr, sizeof(int) * ((size_t)nt + 1)));
@@ -179,7 +191,8 @@ static int upload_dense(tsp_plan *p, ClassDev &c)
     if (c.d_val) return TSP_OK;
     const size_t vs = tsph::val_size(p->prec);
     TSP_TRY(tsp_malloc(&c.d_val, vs * c.m->dnssize));
-    return tsp_memcpy_h2d(c.d_val, c.m->Blockdense_Val, vs * c.m->dnssize);
+    TSP_TRY(tsp_memcpy_h2d(c.d_val, c.m->Blockdense_Val, vs * c.m->dnssize));
+    return round_tf32_copy(p, c.d_val, c.m->dnssize);
 }
 
 // Launch one class on `stream` (its own stream unless given another).
@@ -187,10 +200,10 @@ static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
 {
     if (!c.active() || c.ntasks == 0) return TSP_OK;
     const bool pk = c.fmt == 2;
-    return tsp_spmm_launch_placed(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val,
-                                  pk ? c.d_bmp : nullptr, pk ? c.d_vptr : nullptr, c.d_rows, c.d_colstart,
-                                  p->d_B, p->d_C, c.d_colidx, p->rowA, stream ? stream : c.stream, c.var_w,
-                                  c.var_s, c.var_tpw, c.var_order, c.place);
+    return tsp_spmm_launch_ex(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val, pk ? c.d_bmp : nullptr,
+                              pk ? c.d_vptr : nullptr, c.d_rows, c.d_colstart, p->d_B, p->d_C, c.d_colidx, p->rowA,
+                              stream ? stream : c.stream, c.var_w, c.var_s, c.var_tpw, c.var_order, c.place,
+                              p->prec == TSP_PREC_TF32 ? TSP_LAUNCH_OPERANDS_TF32 : 0);
 }
 
 extern "C" int tsp_plan_set_format(tsp_plan *p, int bm, int fmt)
@@ -316,6 +329,7 @@ static int plan_begin(std::unique_ptr<tsp_plan> &p, int device_id, int rowA, int
     if (p->hot_cap > 0) TSP_TRY(tsp_malloc((void **)&p->d_hot, sizeof(int) * (size_t)p->hot_cap));
     TSP_TRY(tsp_malloc((void **)&p->d_C, cbytes));
     if (h_B) TSP_TRY(tsp_memcpy_h2d(p->d_B, h_B, bbytes));
+    TSP_TRY(round_tf32_copy(p.get(), p->d_B, (size_t)colA * colB_p));
     return tsp_memset(p->d_C, 0, cbytes);
 }
 
@@ -432,6 +446,7 @@ static int class_from_csr(tsp_plan *p, ClassDev &c, const tsp_sub_csr *s)
     tsp_free(dt.d_tile_ptr);
     tsp_free(dt.d_tile_nnz);
     if (st) return st;
+    TSP_TRY(round_tf32_copy(p, c.d_val, m.dnssize));
     if (c.bm != 64 && m.tilenum > 0) {
         long long nvals = 0;
         TSP_TRY(tsp_tiles_pack_device(m.tilenum, BM, BN, p->prec, nullptr, dt.d_bitmap, &nvals, nullptr, nullptr,
