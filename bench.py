@@ -263,7 +263,7 @@ def pins_of(plan, th, cls):
         t.append(c["tasks_per_wave"] if c else 0)
         w.append(c["chunk_width"] if c else 0)
         s.append(c["stages"] if c else 0)
-        p.append({"contiguous": 1, "interleaved": 2}[c["placement"]] if c else 0)
+        p.append({"contiguous": 1, "interleaved": 2, "chunk-xcd": 3}[c["placement"]] if c else 0)
     j = lambda v: ",".join(str(x) for x in v)
     return (f"--no-tune --th {j(th)} --format {j(f)} --order {j(o)} --tpw {j(t)} --width {j(w)} "
             f"--stages {j(s)} --place {j(p)} --hot-bytes {plan.get_hot_rows()[1]}")
@@ -352,7 +352,7 @@ def measure(tsp, hip, config, prec, colB, args, headline):
                    "format": {1: "dense", 2: "packed"}.get(plan.get_format(bm), "?"),
                    "order": {0: "side-by-side", 1: "side-by-side", 2: "chunk-major"}[v[3]],
                    "tasks_per_wave": max(1, v[2]), "stages": max(1, v[1]), "chunk_width": w,
-                   "placement": {0: "contiguous", 1: "interleaved"}.get(plan.get_placement(bm), "?"),
+                   "placement": {0: "contiguous", 1: "interleaved", 2: "chunk-xcd"}.get(plan.get_placement(bm), "?"),
                    "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9,
                    "gathered_lines": lines, "glines_per_s": lines / (cms * 1e-3) / 1e9}
     dom = max(cls, key=lambda k: cls[k]["ms"])
@@ -483,7 +483,8 @@ def main():
     ap.add_argument("--stages", type=ints3, default=None,
                     help="pin the pipeline depth per class 64,16,8 (1-4; 0 keep)")
     ap.add_argument("--place", type=ints3, default=None,
-                    help="pin the XCD placement per class 64,16,8 (1 contiguous, 2 interleaved, 0 keep)")
+                    help="pin the XCD placement per class 64,16,8 (1 contiguous, 2 interleaved, 3 one column "
+                         "chunk per XCD group, 0 keep)")
     ap.add_argument("--hot-bytes", type=int, default=None,
                     help="pin the hot B row budget in bytes after tuning (0: no hot rows)")
     ap.add_argument("--no-cpu", action="store_true")

@@ -166,6 +166,11 @@ int tsp_spmm_launch_packed(int bm, int prec, int rowblkblock, int colB_p, const 
  * the reference (NVIDIA GPUs have one L2). */
 #define TSP_PLACE_CONTIGUOUS 0
 #define TSP_PLACE_INTERLEAVED 1
+/* TSP_PLACE_CHUNK_XCD (2, 4 or 8 column chunks of w columns): each group of
+ * 8 / chunks XCDs serves one chunk, with runs of 4 workgroups dealt in turn
+ * inside the group, so an XCD's L2 holds the B segments of one chunk only
+ * (the chunk order argument is then ignored). */
+#define TSP_PLACE_CHUNK_XCD 2
 int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
                            const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,
                            const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,

@@ -115,8 +115,8 @@ def test_random_all_classes(gpu, orc, prec, colB):
 @pytest.mark.parametrize("prec", [0, 1])
 def test_every_kernel_variant(gpu, orc, prec):
     """Every (chunk width, pipeline depth, tasks per wave) variant of every
-    class, with both XCD placements, gives the oracle's result, split tasks
-    included."""
+    class, with every XCD placement its chunk count allows, gives the
+    oracle's result, split tasks included."""
     tsp = gpu
     rng = np.random.default_rng(50 + prec)
     A = random_matrix(tsp, rng, 611, 509, 45, prec, heavy_rows=4)
@@ -135,7 +135,7 @@ def test_every_kernel_variant(gpu, orc, prec):
                 for w in ((32, 64) if bm == 64 else (32, 64, 128)):
                     for s in (1, 2, 3, 4):
                         for tpw, order in ((1, 1), (3, 2), (0, 0)):
-                            for place in (0, 1):
+                            for place in ((0, 1, 2) if cbp // w in (2, 4, 8) else (0, 1)):
                                 tag = (f"prec={prec} bm={bm} fmt={fmt} w={w} s={s} tpw={tpw} order={order} "
                                        f"place={place}")
                                 say("variant " + tag)
@@ -631,3 +631,35 @@ def test_tf32_prerounded_launch_matches_rounding_launch(gpu, orc, bm):
     finally:
         for p in bufs.values():
             hip.tsp_free(p)
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+def test_chunk_xcd_placement_chunk_counts(gpu, orc, prec):
+    """One column chunk per XCD group with 2, 4 and 8 chunks (colB 64, 128,
+    256 at 32-column chunks) for every class, split tasks included; a chunk
+    count that does not divide the 8 XCDs (colB 192 at 64 columns: 3) is
+    refused."""
+    tsp = gpu
+    rng = np.random.default_rng(70 + prec)
+    A = random_matrix(tsp, rng, 900, 700, 40, prec, heavy_rows=4)
+    for colB in (64, 128, 256, 192):
+        B, cbp = random_b(tsp, rng, A.cols, colB, prec)
+        Cref, Cabs = reference(orc, A, B, colB)
+        subs = tsp.matrix_split(A, 2.0, 1.5)
+        tiles = [tsp.tile_create(s, A.cols, b, prec) for s, b in zip(subs, (64, 16, 8))]
+        plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
+        try:
+            plan.set_th(8, 8, 8)
+            w = 64 if colB == 192 else 32
+            for bm in (64, 16, 8):
+                plan.set_variant(bm, w, 1, 1, 1)
+                plan.set_placement(bm, 2)
+            say(f"chunk-xcd prec={prec} colB={colB} w={w} chunks={cbp // w}")
+            if cbp // w in (2, 4, 8):
+                plan.run(zero_c=True)
+                assert_close(plan.download_c()[:, :colB], Cref, Cabs, prec, f"colB {colB}")
+            else:
+                with pytest.raises(tsp.TspError):
+                    plan.run(zero_c=True)
+        finally:
+            plan.close()

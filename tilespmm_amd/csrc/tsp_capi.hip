@@ -277,7 +277,8 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
     if (colB_p != 32 && (colB_p <= 0 || colB_p % 64 != 0)) return TSP_EINVAL;
     if (rowblkblock < 0 || c_rows < 0) return TSP_EINVAL;
     if (d_bitmap && (bm == 64 || !d_vptr)) return TSP_EINVAL;
-    if (placement != TSP_PLACE_CONTIGUOUS && placement != TSP_PLACE_INTERLEAVED) return TSP_EINVAL;
+    if (placement != TSP_PLACE_CONTIGUOUS && placement != TSP_PLACE_INTERLEAVED && placement != TSP_PLACE_CHUNK_XCD)
+        return TSP_EINVAL;
     if (w > 0 && (colB_p % w != 0 || !tsp::valid_variant(bm, w, stages > 0 ? stages : 1))) return TSP_EINVAL;
     if (rowblkblock == 0) return TSP_OK;
     if (!d_val || !d_rows || !d_colstart || !d_B || !d_C || !d_colidx) return TSP_EINVAL;

@@ -40,10 +40,15 @@ __host__ __device__ inline uint32_t round_tf32_bits(uint32_t x)
 // an L2); kPlaceInterleaved deals runs of kXcdRun consecutive logical blocks
 // to the XCDs in turn, which keeps skewed matrices (hub rows at one end)
 // balanced across the XCDs.
+// kPlaceChunkXcd gives each group of 8 / nchunks XCDs one column chunk (for
+// 2, 4 or 8 chunks), dealt in runs of kXcdRun inside the group: every XCD's
+// L2 then holds B segments of one chunk only, so it covers nchunks times as
+// many B rows.
 constexpr int kXcds = 8;
 constexpr int kXcdRun = 4;
 constexpr int kPlaceContiguous = 0;
 constexpr int kPlaceInterleaved = 1;
+constexpr int kPlaceChunkXcd = 2;
 
 // Kernel variant = (chunk width W, pipeline stages S, tasks per wave).
 int default_chunk_width(int bm, int colB_p);

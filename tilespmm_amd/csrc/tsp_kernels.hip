@@ -129,15 +129,28 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
 
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform per wave
-    const int lb = place_block(blockIdx.x, gridDim.x, placement);
-    const long long gw = (long long)lb * kWavesPerBlock + wid;
     const long long nranges = ((long long)ntasks + tasks_per_wave - 1) / tasks_per_wave;
-    if (gw >= nranges * nchunks) return;
-    // chunk_major: all task ranges of chunk 0, then chunk 1, ... (the live
-    // B working set of a phase is one chunk's columns); otherwise the chunks
-    // of one range are neighbours (the A tiles are reused from L2).
-    const int range = chunk_major ? (int)(gw % nranges) : (int)(gw / nchunks);
-    const int chunk = chunk_major ? (int)(gw / nranges) : (int)(gw - (long long)range * nchunks);
+    int range, chunk;
+    if (placement == kPlaceChunkXcd) {
+        // XCD x (workgroup b runs on XCD b % 8) serves chunk x % nchunks; the
+        // group's 8 / nchunks XCDs take runs of kXcdRun workgroups in turn
+        const int x = blockIdx.x % kXcds, k = blockIdx.x / kXcds, nx = kXcds / nchunks;
+        const long long j = ((long long)(k / kXcdRun) * nx + x / nchunks) * kXcdRun + k % kXcdRun;
+        const long long r = j * kWavesPerBlock + wid;
+        if (r >= nranges) return;
+        range = (int)r;
+        chunk = x % nchunks;
+    } else {
+        const int lb = place_block(blockIdx.x, gridDim.x, placement);
+        const long long gw = (long long)lb * kWavesPerBlock + wid;
+        if (gw >= nranges * nchunks) return;
+        // chunk_major: all task ranges of chunk 0, then chunk 1, ... (the
+        // live B working set of a phase is one chunk's columns); otherwise
+        // the chunks of one range are neighbours (the A tiles are reused
+        // from L2).
+        range = chunk_major ? (int)(gw % nranges) : (int)(gw / nchunks);
+        chunk = chunk_major ? (int)(gw / nranges) : (int)(gw - (long long)range * nchunks);
+    }
     const int k0 = range * tasks_per_wave;
     const int k1 = min(ntasks, k0 + tasks_per_wave);
     const int tb = uload(colstart, k0), te = uload(colstart, k1);
@@ -178,15 +191,21 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
             m.vbase = uload(vptr, t);
         }
     };
-    auto load_a_packed = [&](const PMeta &m, uint32_t (&dst)[RG][AW]) {
+    // Packed A in two halves, so a wave never waits for a load it has just
+    // issued: issue_a_packed (S tiles ahead) computes the lane's position in
+    // the packed stream from the scalar bitmap words, loads its NVAL
+    // consecutive values raw and keeps its NVAL occupancy bits; finish_a_packed
+    // (just before the tile's MFMAs) expands them into operand registers.
+    constexpr int NVAL = F16 ? 4 : KS;           // packed: operand values per lane
+    auto issue_a_packed = [&](const PMeta &m, VT (&raw)[NVAL], uint32_t &nib) {
         static_assert(!PK || BM <= 16, "packed tiles are 8- or 16-row");
         constexpr int WD = PWD;                  // bitmap words per tile
-        constexpr int NVAL = F16 ? 4 : KS;       // operand values per lane
         const uint64_t *bw = m.bw;
         const int vbase = m.vbase;
         if (BM == 8 && ln >= 8) {
 #pragma unroll
-            for (int w = 0; w < AW; ++w) dst[0][w] = 0u;
+            for (int j = 0; j < NVAL; ++j) raw[j] = (VT)0;
+            nib = 0u;
             return;
         }
         // first bit of this lane's slots; NVAL-bit groups never straddle words
@@ -200,13 +219,15 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
             pre += __popcll(bw[w] & m);
             if (p >= lo && p < lo + 64) word = bw[w];
         }
-        const unsigned nib = (unsigned)(word >> (p & 63)) & ((1u << NVAL) - 1u);
+        nib = (unsigned)(word >> (p & 63)) & ((1u << NVAL) - 1u);
         // the lane's values are consecutive in the packed stream (the value
         // array is padded, so reading NVAL of them is always in bounds)
         const VT *pv = val + vbase + pre;
-        VT v[NVAL], o[NVAL];
 #pragma unroll
-        for (int j = 0; j < NVAL; ++j) v[j] = pv[j];
+        for (int j = 0; j < NVAL; ++j) raw[j] = pv[j];
+    };
+    auto finish_a_packed = [&](const VT (&v)[NVAL], uint32_t nib, uint32_t (&dst)[RG][AW]) {
+        VT o[NVAL];
         int idx = 0;
 #pragma unroll
         for (int j = 0; j < NVAL; ++j) {
@@ -227,11 +248,7 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
             for (int j = 0; j < NVAL; ++j) dst[0][j] = rnd(__float_as_uint(o[j]));
         }
     };
-    auto load_a = [&](int t, const PMeta &m, uint32_t (&dst)[RG][AW]) {
-        if constexpr (PK) {
-            load_a_packed(m, dst);
-            return;
-        }
+    auto load_a = [&](int t, uint32_t (&dst)[RG][AW]) {
         const VT *tile = val + (size_t)t * (BM * BN);
 #pragma unroll
         for (int g = 0; g < RG; ++g) {
@@ -417,10 +434,16 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     // tile periods to arrive before its B addresses are formed (the indices
     // stream from HBM; one period is not enough to hide that latency).
     u4 bv[S][NV];
-    uint32_t ar[S][RG][AW];
+    uint32_t ar[S][RG][AW];          // dense A: operand words
+    VT araw[S][NVAL];                 // packed A: raw values and occupancy bits
+    uint32_t anib[S];
     CSV cs[S];
     PMeta pm[S];
     int cid[NV];
+    auto issue_a = [&](int t, int s) {
+        if constexpr (PK) issue_a_packed(pm[s], araw[s], anib[s]);
+        else load_a(t, ar[s]);
+    };
 #pragma unroll
     for (int s = 0; s < S; ++s)
         if (tb + s < te) {
@@ -432,7 +455,7 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
         if (tb + s < te) {
             select_cid(cs[s], cid);
             load_b(cid, bv[s]);
-            load_a(tb + s, pm[s], ar[s]);
+            issue_a(tb + s, s);
         }
 #pragma unroll
     for (int s = 0; s < S; ++s)
@@ -461,14 +484,18 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
                 }
                 stage_b(bv[s]);
                 uint32_t acur[RG][AW];
+                if constexpr (PK) {
+                    finish_a_packed(araw[s], anib[s], acur);
+                } else {
 #pragma unroll
-                for (int g = 0; g < RG; ++g)
+                    for (int g = 0; g < RG; ++g)
 #pragma unroll
-                    for (int w = 0; w < AW; ++w) acur[g][w] = ar[s][g][w];
+                        for (int w = 0; w < AW; ++w) acur[g][w] = ar[s][g][w];
+                }
                 if (t + S < te) {
                     select_cid(cs[s], cid);
                     load_b(cid, bv[s]);
-                    load_a(t + S, pm[s], ar[s]);
+                    issue_a(t + S, s);
                     if (t + 2 * S < te) {
                         load_cs(t + 2 * S, cs[s]);
                         load_meta(t + 2 * S, pm[s]);
@@ -578,18 +605,26 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
 {
     const bool packed = bmp != nullptr;
     if (packed && (bm == 64 || !vptr)) return TSP_EINVAL;
-    if (placement != kPlaceContiguous && placement != kPlaceInterleaved) return TSP_EINVAL;
+    if (placement != kPlaceContiguous && placement != kPlaceInterleaved && placement != kPlaceChunkXcd)
+        return TSP_EINVAL;
     int nchunks = 0, cm = 0;
     if (!resolve_variant(bm, prec, colB_p, w, s, nchunks, tpw, order, cm)) return TSP_EINVAL;
+    if (placement == kPlaceChunkXcd && (nchunks < 2 || kXcds % nchunks != 0)) return TSP_EINVAL;
     const long long ranges = ((long long)ntasks + tpw - 1) / tpw;
     const long long waves = ranges * nchunks;
     long long blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
     if (blocks <= 0) return 0;
-    // interleaved: whole runs on every XCD (workgroups past the last
-    // logical block find no task range and exit)
     if (placement == kPlaceInterleaved) {
+        // whole runs on every XCD (workgroups past the last logical block
+        // find no task range and exit)
         const long long run = (long long)kXcds * kXcdRun;
         blocks = (blocks + run - 1) / run * run;
+    } else if (placement == kPlaceChunkXcd) {
+        // per XCD: enough whole runs for its share of one chunk's ranges
+        const long long per_chunk = (ranges + kWavesPerBlock - 1) / kWavesPerBlock;
+        const long long nx = kXcds / nchunks;
+        const long long per_xcd = (per_chunk + nx * kXcdRun - 1) / (nx * kXcdRun) * kXcdRun;
+        blocks = per_xcd * kXcds;
     }
     if (blocks > 0x7fffffffLL) return TSP_EINVAL;
     const dim3 grid3((unsigned)blocks);

@@ -248,7 +248,9 @@ extern "C" int tsp_plan_set_variant(tsp_plan *p, int bm, int w, int stages, int 
 
 extern "C" int tsp_plan_set_placement(tsp_plan *p, int bm, int placement)
 {
-    if (!p || (placement != TSP_PLACE_CONTIGUOUS && placement != TSP_PLACE_INTERLEAVED)) return TSP_EINVAL;
+    if (!p || (placement != TSP_PLACE_CONTIGUOUS && placement != TSP_PLACE_INTERLEAVED &&
+               placement != TSP_PLACE_CHUNK_XCD))
+        return TSP_EINVAL;
     for (ClassDev &c : p->cls)
         if (c.bm == bm) {
             c.place = placement;
@@ -726,14 +728,17 @@ static int tune_time_class(tsp_plan *p, int bm, double *ms)
 //      L2; chunk-major shrinks the live B working set per phase) x tasks per
 //      wave (1, or 4 when row-blocks are split: consecutive tasks of a split
 //      row-block then merge into one flush instead of several atomic ones);
-//   2. the two best of step 1 under both XCD placements (contiguous eighths
+//   2. the two best of step 1 under each XCD placement (contiguous eighths
 //      keep neighbouring row-blocks, which share B rows, on one L2; runs dealt
-//      round-robin balance matrices whose heavy row-blocks sit together);
+//      round-robin balance matrices whose heavy row-blocks sit together; with
+//      2, 4 or 8 column chunks, one chunk per XCD group shrinks each L2's B
+//      working set);
 //   3. every chunk width (32, 64, 128 columns; 32 or 64 for 64-row tiles),
-//      each with both chunk orders, under both placements: wider chunks mean
+//      each with both chunk orders, under each placement: wider chunks mean
 //      fewer waves and longer B row segments, narrower ones a smaller B
 //      working set per wave and more waves (tf32 RMAT gains 11% at 32 when
-//      interleaved).  Step 2's choice stays unless another is 1% faster.
+//      interleaved).  Step 2's choice stays unless another is 1% faster;
+//   4. the pipeline depth (1-3 tiles in flight per wave).
 // A class whose variant was pinned with tsp_plan_set_variant is left alone.
 static int tune_class(tsp_plan *p, ClassDev &c)
 {
@@ -776,11 +781,19 @@ static int tune_class(tsp_plan *p, ClassDev &c)
             fprintf(stderr, "tune bm=%d th=%d format=%d order=%d tasks/wave=%d: %.5f ms\n", c.bm, c.th, cand[j].fmt,
                     cand[j].order, cand[j].tpw, cand_ms[j]);
 
+    // placements a launch with `nch` column chunks can use
+    const auto places = [](int nch) {
+        std::vector<int> v{TSP_PLACE_CONTIGUOUS, TSP_PLACE_INTERLEAVED};
+        if (nch == 2 || nch == 4 || nch == 8) v.push_back(TSP_PLACE_CHUNK_XCD);
+        return v;
+    };
+    const char *place_name[3] = {"contiguous", "interleaved", "chunk-xcd"};
     std::vector<Opt> pl;
     for (size_t j = 0; j < std::min<size_t>(2, rank.size()); ++j)
-        for (int place = TSP_PLACE_CONTIGUOUS; place <= TSP_PLACE_INTERLEAVED; ++place) {
+        for (int place : places(p->colB_p / k.cols_per_task)) {
             Opt o = cand[rank[j]];
             o.place = place;
+            if (place == TSP_PLACE_CHUNK_XCD && o.order == 2) continue;   // order has no effect there
             pl.push_back(o);
         }
     std::vector<double> pl_ms;
@@ -791,7 +804,7 @@ static int tune_class(tsp_plan *p, ClassDev &c)
     if (log)
         for (size_t j = 0; j < pl.size(); ++j)
             fprintf(stderr, "tune bm=%d format=%d order=%d tasks/wave=%d placement=%s: %.5f ms%s\n", c.bm, pl[j].fmt,
-                    pl[j].order, pl[j].tpw, pl[j].place ? "interleaved" : "contiguous", pl_ms[j],
+                    pl[j].order, pl[j].tpw, place_name[pl[j].place], pl_ms[j],
                     j == best ? "  <- kept" : "");
     TSP_TRY(tsp_plan_set_format(p, c.bm, pl[best].fmt));
     c.var_order = pl[best].order;
@@ -806,11 +819,17 @@ static int tune_class(tsp_plan *p, ClassDev &c)
         int w, order, place;
     };
     std::vector<WOpt> wo;
-    for (int place = TSP_PLACE_CONTIGUOUS; place <= TSP_PLACE_INTERLEAVED; ++place) {
-        wo.push_back({0, c.var_order, place});
+    for (int place = TSP_PLACE_CONTIGUOUS; place <= TSP_PLACE_CHUNK_XCD; ++place) {
+        const std::vector<int> dp = places(p->colB_p / k.cols_per_task);
+        if (std::find(dp.begin(), dp.end(), place) != dp.end())
+            wo.push_back({0, place == TSP_PLACE_CHUNK_XCD ? 1 : c.var_order, place});
         for (int w : {32, 64, 128}) {
             if (w == k.cols_per_task || p->colB_p % w != 0 || (c.bm == 64 && w == 128)) continue;
-            if (p->colB_p / w >= 2) {
+            const std::vector<int> wp = places(p->colB_p / w);
+            if (std::find(wp.begin(), wp.end(), place) == wp.end()) continue;
+            if (place == TSP_PLACE_CHUNK_XCD) {
+                wo.push_back({w, 1, place});
+            } else if (p->colB_p / w >= 2) {
                 wo.push_back({w, 1, place});
                 wo.push_back({w, 2, place});
             } else {
@@ -845,8 +864,29 @@ static int tune_class(tsp_plan *p, ClassDev &c)
             for (size_t j = 0; j < wo.size(); ++j)
                 fprintf(stderr, "tune bm=%d chunk width %d order=%d placement=%s: %.5f ms%s\n", c.bm,
                         wo[j].w ? wo[j].w : k.cols_per_task, wo[j].order,
-                        wo[j].place ? "interleaved" : "contiguous", wms[j], j == bw ? "  <- kept" : "");
+                        place_name[wo[j].place], wms[j], j == bw ? "  <- kept" : "");
     }
+
+    // 4. pipeline depth: 2 or 3 tiles in flight per wave against 1, the rest
+    //    as kept; a deeper pipeline holds more B gathers in flight per wave but
+    //    costs registers (occupancy), so it is kept only when 1% faster
+    const int w_kept = c.var_w ? c.var_w : k.cols_per_task;
+    double sms[4] = {1e30, 1e30, 1e30, 1e30};
+    for (int round = 0; round < 2; ++round)
+        for (int st = 1; st <= 3; ++st) {
+            c.var_w = w_kept;
+            c.var_s = st;
+            double t = 0;
+            TSP_TRY(tune_time_class(p, c.bm, &t));
+            sms[st] = std::min(sms[st], t);
+        }
+    int sb = 1;
+    for (int st = 2; st <= 3; ++st)
+        if (sms[st] < 0.99 * sms[sb]) sb = st;
+    c.var_s = sb;
+    if (log)
+        for (int st = 1; st <= 3; ++st)
+            fprintf(stderr, "tune bm=%d stages %d: %.5f ms%s\n", c.bm, st, sms[st], st == sb ? "  <- kept" : "");
     return TSP_OK;
 }
 
@@ -860,25 +900,31 @@ static int tune_time_step(tsp_plan *p, double min_ms, double *ms)
     return tsp_plan_time(p, reps, ms);
 }
 
-// Hot B rows: whole steps timed without hot rows and with kHotTuneBytes of
-// them, best of two interleaved rounds of at least 20 ms each; the hot rows
-// are kept when they are at least 2% faster.  On the skewed MI355X cases the
-// step time is flat from 8 to 64 MB of hot rows (RMAT scale 22: within 0.4%
-// tf32 and 1% fp16) and 1-3% slower at 4 MB, so one budget in the middle of
-// that plateau is timed instead of a noisy search over several.  Run before
-// the threshold and class tuning (with the model's thresholds and default
-// variants) and again after it.  TSP_HOT_BYTES=<bytes> pins the budget.
+// Hot B rows during tuning.  The thresholds and class variants are tuned
+// with kHotTuneBytes of hot rows whenever any column is gathered at least
+// TSP_HOT_MIN_GATHERS times; then whole steps are timed without hot rows and
+// with them (best of two interleaved rounds of at least 20 ms each) and the
+// hot rows stay when they are at least 2% faster.  On the skewed MI355X cases
+// the step time is flat from 8 to 64 MB of hot rows (RMAT scale 22: within
+// 0.4% tf32 and 1% fp16) and 1-3% slower at 4 MB, so one budget in the middle
+// of that plateau is timed instead of a noisy search over several.  Deciding
+// before the variants are tuned is not enough: with the default variants the
+// hot rows may miss the 2% bar, and variants tuned without them then hide
+// their gain (RMAT fp16 colB 128 ran 4.8 instead of 3.9 ms that way).
+// TSP_HOT_BYTES=<bytes> pins the budget instead.
 static constexpr long long kHotTuneBytes = 16LL << 20;
 
-static int tune_hot_rows(tsp_plan *p, int tune)
+static int hot_candidates(tsp_plan *p, long long *ncand)
 {
+    *ncand = 0;
     if (p->hot_cap == 0) return TSP_OK;
-    if (const char *env = getenv("TSP_HOT_BYTES")) return tsp_plan_set_hot_rows(p, atoll(env));
-    if (!tune) return TSP_OK;
     TSP_TRY(count_gathers(p));
-    long long ncand = 0;
-    for (unsigned g : p->col_gathers) ncand += g >= TSP_HOT_MIN_GATHERS;
-    if (ncand == 0) return TSP_OK;
+    for (unsigned g : p->col_gathers) *ncand += g >= TSP_HOT_MIN_GATHERS;
+    return TSP_OK;
+}
+
+static int decide_hot_rows(tsp_plan *p, bool *kept)
+{
     const long long budgets[2] = {0, kHotTuneBytes};
     double best[2] = {1e30, 1e30};
     for (int round = 0; round < 2; ++round)
@@ -888,11 +934,12 @@ static int tune_hot_rows(tsp_plan *p, int tune)
             TSP_TRY(tune_time_step(p, 20.0, &ms));
             best[j] = std::min(best[j], ms);
         }
-    const int keep = best[1] <= 0.98 * best[0] ? 1 : 0;
+    *kept = best[1] <= 0.98 * best[0];
     if (getenv("TSP_TUNE_LOG"))
         for (int j = 0; j < 2; ++j)
-            fprintf(stderr, "tune hot rows %lld MB: %.5f ms%s\n", budgets[j] >> 20, best[j], j == keep ? "  <- kept" : "");
-    return tsp_plan_set_hot_rows(p, budgets[keep]);
+            fprintf(stderr, "tune hot rows %lld MB: %.5f ms%s\n", budgets[j] >> 20, best[j],
+                    (j == 1) == *kept ? "  <- kept" : "");
+    return tsp_plan_set_hot_rows(p, budgets[*kept ? 1 : 0]);
 }
 
 extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model_ms, double *tune_ms)
@@ -918,7 +965,17 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
     int best[3] = {opts[0][0], opts[1][0], opts[2][0]};
     TSP_TRY(tsp_plan_set_th(p, best[0], best[1], best[2]));
     double t2 = now_ms(), t3 = t2;
-    TSP_TRY(tune_hot_rows(p, tune));
+    bool hot_tuning = false;
+    if (const char *pin = getenv("TSP_HOT_BYTES")) {
+        TSP_TRY(tsp_plan_set_hot_rows(p, atoll(pin)));
+    } else if (tune) {
+        long long ncand = 0;
+        TSP_TRY(hot_candidates(p, &ncand));
+        if (ncand > 0) {
+            TSP_TRY(tsp_plan_set_hot_rows(p, kHotTuneBytes));
+            hot_tuning = true;
+        }
+    }
     const size_t combos = opts[0].size() * opts[1].size() * opts[2].size();
     if (tune && combos > 1) {
         double best_ms = 1e30;
@@ -939,9 +996,16 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
     }
     if (tune) {
         for (ClassDev &c : p->cls) TSP_TRY(tune_class(p, c));
-        // the class variants change how much the hot rows save: time the
-        // budgets again with the tuned variants
-        TSP_TRY(tune_hot_rows(p, tune));
+        bool kept = false;
+        if (hot_tuning) TSP_TRY(decide_hot_rows(p, &kept));
+        if (hot_tuning && !kept) {
+            // the variants were tuned for the hot rows: tune them again without
+            for (ClassDev &c : p->cls) {
+                c.var_w = c.var_s = c.var_tpw = c.var_order = 0;
+                c.place = TSP_PLACE_CONTIGUOUS;
+                TSP_TRY(tune_class(p, c));
+            }
+        }
         t3 = now_ms();
     }
     if (tune_ms) *tune_ms = t3 - t2;
