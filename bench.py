@@ -370,12 +370,17 @@ def measure(tsp, hip, config, prec, colB, args, headline):
     prof = os.path.join(ROOT, "profiles", f"traffic_config{config}_{pname}_{colB}.json")
     if os.path.exists(prof):
         with open(prof) as fh:
-            tp = json.load(fh).get(f"bm{dom}", {})
-        if tp.get("kernel", "").endswith(kname) and tp.get("hot_rows", 0) == hot_n:
-            traffic, traffic_note = tp.get("hbm_bytes_per_launch"), os.path.relpath(prof, ROOT)
+            pj = json.load(fh)
+        # the tuned instantiation may be the profile's main entry or one of
+        # the alternatives profiled beside it
+        entries = [pj.get(f"bm{dom}", {})] + [e for e in pj.get("alternatives", []) if e.get("bm") == dom]
+        hit = [e for e in entries if e.get("kernel", "").endswith(kname) and e.get("hot_rows", 0) == hot_n]
+        if hit:
+            traffic, traffic_note = hit[0].get("hbm_bytes_per_launch"), os.path.relpath(prof, ROOT)
         else:
-            traffic_note = (f"{os.path.relpath(prof, ROOT)} profiles {tp.get('kernel', '?')} with "
-                            f"{tp.get('hot_rows', 0)} hot rows, not the tuned {kname} with {hot_n}")
+            traffic_note = (f"{os.path.relpath(prof, ROOT)} profiles "
+                            f"{', '.join(e.get('kernel', '?') + ' with ' + str(e.get('hot_rows', 0)) + ' hot rows' for e in entries)}"
+                            f", not the tuned {kname} with {hot_n}")
     roof = {"bound": "hbm", "achieved": round(dk["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
             "traffic_over_alg": round(traffic / dk["alg_bytes"], 3) if traffic else None,
