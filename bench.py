@@ -313,6 +313,8 @@ def measure(tsp, hip, config, prec, colB, args, headline):
         del B
     log(f"split gamma={g} delta={d} ({split_ms:.0f} ms); tilenum {tilenum}")
 
+    if args.tune_cold:
+        plan.set_tune_mode(True)
     th, model_ms, tune_ms = plan.tune(not args.no_tune)
     th = apply_pins(plan, args) or th
     hot_n, hot_b = plan.get_hot_rows()
@@ -390,6 +392,7 @@ def measure(tsp, hip, config, prec, colB, args, headline):
             "step_alg_bytes": step_bytes}
 
     rec = {"workload": f"{NAMES[config]}, {pname}, colB {colB}", "config_id": config, "dtype": pname,
+           "tune_mode": "cold" if args.tune_cold else "back-to-back",
            "rows": A.rows, "nnz": A.nnz, "colB": colB, "colB_padded": cbp, "gamma": g, "delta": d,
            "th": list(th), "tilenum": tilenum, "hot_rows": hot_n, "hot_bytes": hot_b,
            "ms_per_step": ms, "tflops": tflops, "steps": args.steps, "window_ms": ms * args.steps,
@@ -492,6 +495,8 @@ def main():
                          "chunk per XCD group, 0 keep)")
     ap.add_argument("--hot-bytes", type=int, default=None,
                     help="pin the hot B row budget in bytes after tuning (0: no hot rows)")
+    ap.add_argument("--tune-cold", action="store_true",
+                    help="tune for single steps from a cold cache (TSP_TUNE_COLD) instead of back-to-back steps")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-vendor", action="store_true")
     ap.add_argument("--class-reps", type=int, default=200,
@@ -546,6 +551,7 @@ def main():
         for k in ("th", "format", "order", "tpw", "width", "stages", "place", "hot_bytes", "gamma", "delta"):
             setattr(targ, k, None)
         targ.no_tune = False
+        targ.tune_cold = False
         t, _, _, tplan = measure(tsp, hip, cfg, 0, 128, targ, headline=False)
         tplan.close()
         targets[TARGETS.get(cfg, f"C{cfg}")] = {
@@ -578,6 +584,7 @@ def main():
         "classes": {f"bm{k}": {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in rec["classes"].items()},
         "cold_cache": rec.get("cold_cache"),
+        "tune_mode": rec["tune_mode"],
         "vendor": rec.get("vendor"),
         "pre_ms": rec["pre_ms"],
         "replay": rec["replay"],

@@ -222,6 +222,18 @@ int tsp_plan_get_placement(tsp_plan *plan, int bm);
  * faster.  get: the current slot count and bytes.  No counterpart in the
  * reference. */
 #define TSP_HOT_MAX_BYTES (64LL << 20)
+/* What tsp_plan_tune optimises.  TSP_TUNE_BACK_TO_BACK (the default): steps
+ * run back to back, as the reference times its 1000 repetitions, so data
+ * that fits in L2 or the 256 MB MALL carries over between steps.
+ * TSP_TUNE_COLD: single steps from a cold cache (each measurement follows a
+ * copy that evicts L2 and the MALL), for callers that run the product once
+ * between other work; setting it allocates 1 GB of eviction buffer, which
+ * TSP_TUNE_BACK_TO_BACK or tsp_plan_destroy frees.  No counterpart in the
+ * reference. */
+#define TSP_TUNE_BACK_TO_BACK 0
+#define TSP_TUNE_COLD 1
+int tsp_plan_set_tune_mode(tsp_plan *plan, int mode);
+int tsp_plan_get_tune_mode(tsp_plan *plan);
 #define TSP_HOT_MIN_GATHERS 4
 int tsp_plan_set_hot_rows(tsp_plan *plan, long long budget_bytes);
 int tsp_plan_get_hot_rows(tsp_plan *plan, int *nhot, long long *bytes);
@@ -231,10 +243,11 @@ int tsp_plan_get_hot_rows(tsp_plan *plan, int *nhot, long long *bytes);
 int tsp_plan_run(tsp_plan *plan, int zero_c);
 /* Warm-up before timing, replacing warmup_gpu (src/csr2tile.h:798-823):
  * steps in batches of 20, then 50, reading the GFX clock
- * (tsp_gpu_clock_mhz) after each batch, until two successive readings agree
- * within 2% and are at least 95% of the maximum clock, or three successive
- * readings agree within 2% (MI355X power management can settle a
- * memory-bound load below 95% of the maximum); at most max_iters steps.
+ * (tsp_gpu_clock_mhz) while each batch runs, until -- after at least 20 ms
+ * of steps -- two successive readings agree within 2% and are at least 95%
+ * of the maximum clock, or three successive readings agree within 2%
+ * (MI355X power management can settle a memory-bound load below 95% of the
+ * maximum); at most max_iters steps.
  * Without a readable clock it runs min(max_iters, 100) steps, the
  * reference's fallback.  *iters_run / *clock_mhz (may be NULL): steps run and
  * the last clock reading. */

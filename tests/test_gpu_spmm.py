@@ -663,3 +663,31 @@ def test_chunk_xcd_placement_chunk_counts(gpu, orc, prec):
                     plan.run(zero_c=True)
         finally:
             plan.close()
+
+
+def test_cold_tune_mode(gpu, orc):
+    """TSP_TUNE_COLD: the tuning times single launches after evicting L2 and
+    the MALL; the tuned plan still gives the oracle's result, and the mode
+    can be switched back (freeing the eviction buffer)."""
+    tsp = gpu
+    rng = np.random.default_rng(12)
+    A = random_matrix(tsp, rng, 2000, 1500, 30, 0, heavy_rows=3)
+    colB = 128
+    B, cbp = random_b(tsp, rng, A.cols, colB, 0)
+    Cref, Cabs = reference(orc, A, B, colB)
+    subs = tsp.matrix_split(A, 2.0, 1.5)
+    tiles = [tsp.tile_create(s, A.cols, b, 0) for s, b in zip(subs, (64, 16, 8))]
+    plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, 0, B)
+    try:
+        assert plan.get_tune_mode() == 0
+        plan.set_tune_mode(True)
+        assert plan.get_tune_mode() == 1
+        plan.tune(True)
+        plan.run(zero_c=True)
+        assert_close(plan.download_c()[:, :colB], Cref, Cabs, 0, "cold-tuned plan")
+        plan.set_tune_mode(False)
+        assert plan.get_tune_mode() == 0
+        plan.run(zero_c=True)
+        assert_close(plan.download_c()[:, :colB], Cref, Cabs, 0, "after switching back")
+    finally:
+        plan.close()

@@ -232,6 +232,8 @@ HOST_SYMBOLS = {
     "tsp_plan_set_placement": (C.c_int, [_P, C.c_int, C.c_int]),
     "tsp_plan_get_placement": (C.c_int, [_P, C.c_int]),
     "tsp_plan_set_hot_rows": (C.c_int, [_P, C.c_longlong]),
+    "tsp_plan_set_tune_mode": (C.c_int, [_P, C.c_int]),
+    "tsp_plan_get_tune_mode": (C.c_int, [_P]),
     "tsp_plan_get_hot_rows": (C.c_int, [_P, _IP, C.POINTER(C.c_longlong)]),
     "tsp_plan_run": (C.c_int, [_P, C.c_int]),
     "tsp_plan_warmup": (C.c_int, [_P, C.c_int]),
@@ -662,6 +664,13 @@ class Plan:
 
     def get_placement(self, bm: int) -> int:
         return load()[1].tsp_plan_get_placement(self.p, bm)
+
+    def set_tune_mode(self, cold: bool):
+        """Tune for single steps from a cold cache (True) or back-to-back steps."""
+        _check("tsp_plan_set_tune_mode", load()[1].tsp_plan_set_tune_mode(self.p, 1 if cold else 0))
+
+    def get_tune_mode(self) -> int:
+        return load()[1].tsp_plan_get_tune_mode(self.p)
 
     def set_hot_rows(self, budget_bytes: int):
         """Copy the most-gathered B rows (at most budget_bytes) into spare rows

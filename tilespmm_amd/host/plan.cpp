@@ -68,6 +68,8 @@ struct tsp_plan {
     int nhot = 0;                 // hot slots in use: row colA + s copies B row d_hot[s]
     int *d_hot = nullptr;
     std::vector<unsigned> col_gathers;   // gathers per column over every class (canonical indices)
+    int tune_mode = TSP_TUNE_BACK_TO_BACK;
+    void *d_flush = nullptr;      // cold tuning: 2 x kFlushBytes of other memory, copied to evict the caches
     float *d_C = nullptr;
     ClassDev cls[3];
     void *main = nullptr;
@@ -298,6 +300,7 @@ extern "C" int tsp_plan_destroy(tsp_plan *p)
     }
     tsp_free(p->d_B);
     tsp_free(p->d_hot);
+    tsp_free(p->d_flush);
     tsp_free(p->d_C);
     tsp_event_destroy(p->ev0);
     tsp_event_destroy(p->ev1);
@@ -676,6 +679,12 @@ extern "C" int tsp_plan_time_class(tsp_plan *p, int bm, int reps, double *ms)
 }
 
 // warmup_gpu (src/csr2tile.h:798-823) with the clock read through AMD SMI.
+// The clock is read right after a batch is enqueued, while its steps run (a
+// reading after the batch has drained sees the idle clock), and stability is
+// accepted only after at least kWarmupMinMs of steps, so batches of a few
+// microseconds-long steps cannot stop the warm-up while the clock still ramps.
+static constexpr double kWarmupMinMs = 20.0;
+
 extern "C" int tsp_plan_warmup_clock(tsp_plan *p, int max_iters, int *iters_run, unsigned *clock_mhz)
 {
     if (!p || max_iters < 0) return TSP_EINVAL;
@@ -686,13 +695,18 @@ extern "C" int tsp_plan_warmup_clock(tsp_plan *p, int max_iters, int *iters_run,
     const auto agree = [](unsigned a, unsigned b) { return a && b && std::fabs((double)a / b - 1.0) <= 0.02; };
     unsigned prev = 0, prev2 = 0;
     int total = 0;
+    const double t0 = now_ms();
     while (total < limit) {
         const int count = std::min(total == 0 ? 20 : 50, limit - total);
         for (int i = 0; i < count; ++i) TSP_TRY(tsp_plan_run(p, 0));
+        if (clocked) TSP_TRY(tsp_gpu_clock_mhz(p->dev, &cur, nullptr));
         TSP_TRY(tsp_stream_sync(p->main));
         total += count;
-        if (!clocked) continue;
-        TSP_TRY(tsp_gpu_clock_mhz(p->dev, &cur, nullptr));
+        if (!clocked || now_ms() - t0 < kWarmupMinMs) {
+            prev2 = prev;
+            prev = cur;
+            continue;
+        }
         const bool high = maxc == 0 || (cur >= 0.95 * maxc && prev >= 0.95 * maxc);
         if (agree(cur, prev) && (high || agree(prev, prev2))) break;
         prev2 = prev;
@@ -708,11 +722,58 @@ extern "C" int tsp_plan_warmup(tsp_plan *p, int max_iters)
     return tsp_plan_warmup_clock(p, max_iters, nullptr, nullptr);
 }
 
+// Cold-cache tuning (TSP_TUNE_COLD): every measurement is the median of
+// single launches (or steps), each after a copy over 2 x 512 MB of other
+// memory, which evicts L2 (8 x 4 MB) and the 256 MB MALL.
+static constexpr size_t kFlushBytes = 512ull << 20;
+static constexpr int kColdReps = 7;
+
+static int evict_caches(tsp_plan *p)
+{
+    TSP_TRY(tsp_copy_kernel((char *)p->d_flush + kFlushBytes, p->d_flush, kFlushBytes, p->main));
+    return tsp_stream_sync(p->main);
+}
+
+static double median(std::vector<double> v)
+{
+    std::sort(v.begin(), v.end());
+    return v[v.size() / 2];
+}
+
+static int cold_time(tsp_plan *p, int bm, double *ms)
+{
+    std::vector<double> t;
+    for (int r = 0; r < kColdReps; ++r) {
+        TSP_TRY(evict_caches(p));
+        double x = 0;
+        TSP_TRY(bm ? tsp_plan_time_class(p, bm, 1, &x) : tsp_plan_time(p, 1, &x));
+        t.push_back(x);
+    }
+    *ms = median(t);
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_set_tune_mode(tsp_plan *p, int mode)
+{
+    if (!p || (mode != TSP_TUNE_BACK_TO_BACK && mode != TSP_TUNE_COLD)) return TSP_EINVAL;
+    if (mode == TSP_TUNE_COLD && !p->d_flush) TSP_TRY(tsp_malloc(&p->d_flush, 2 * kFlushBytes));
+    if (mode == TSP_TUNE_BACK_TO_BACK && p->d_flush) {
+        TSP_TRY(tsp_device_sync());
+        TSP_TRY(tsp_free(p->d_flush));
+        p->d_flush = nullptr;
+    }
+    p->tune_mode = mode;
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_get_tune_mode(tsp_plan *p) { return p ? p->tune_mode : -1; }
+
 // One tuning measurement of a class: a warm-up launch, then enough launches
 // to span about 2 ms (at least 3, at most 200), so that short kernels are not
 // decided by timer noise and long ones cost little.
 static int tune_time_class(tsp_plan *p, int bm, double *ms)
 {
+    if (p->tune_mode == TSP_TUNE_COLD) return cold_time(p, bm, ms);
     double warm = 0;
     TSP_TRY(tsp_plan_time_class(p, bm, 1, &warm));
     const int reps = (int)std::min(200.0, std::max(3.0, 2.0 / std::max(warm, 1e-4)));
@@ -894,6 +955,7 @@ static int tune_class(tsp_plan *p, ClassDev &c)
 // span about min_ms (at least 3, at most 1000).
 static int tune_time_step(tsp_plan *p, double min_ms, double *ms)
 {
+    if (p->tune_mode == TSP_TUNE_COLD) return cold_time(p, 0, ms);
     double warm = 0;
     TSP_TRY(tsp_plan_time(p, 1, &warm));
     const int reps = (int)std::min(1000.0, std::max(3.0, min_ms / std::max(warm, 1e-4)));
@@ -983,9 +1045,13 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
             for (int b : opts[1])
                 for (int c : opts[2]) {
                     TSP_TRY(tsp_plan_set_th(p, a, b, c));
-                    for (int w = 0; w < 5; ++w) TSP_TRY(tsp_plan_run(p, 0));
                     double ms = 0;
-                    TSP_TRY(tsp_plan_time(p, 10, &ms));
+                    if (p->tune_mode == TSP_TUNE_COLD) {
+                        TSP_TRY(cold_time(p, 0, &ms));
+                    } else {
+                        for (int w = 0; w < 5; ++w) TSP_TRY(tsp_plan_run(p, 0));
+                        TSP_TRY(tsp_plan_time(p, 10, &ms));
+                    }
                     if (ms < best_ms) {
                         best_ms = ms;
                         best[0] = a; best[1] = b; best[2] = c;
