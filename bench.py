@@ -172,7 +172,7 @@ def sweep(plan, tilenum, cbp, args):
         plan.set_variant(bm)
         res["default"] = plan.time_class(bm, args.class_reps)
         for w in widths:
-            for s in (1, 2, 3, 4):
+            for s in (1, 2, 3):
                 for tpw in (1, 4):
                     for order in ((1, 2) if cbp > w else (1,)):
                         plan.set_variant(bm, w, s, tpw, order)
@@ -248,6 +248,9 @@ def apply_pins(plan, args):
     for bm, pl in zip((64, 16, 8), args.place or ()):
         if pl:
             plan.set_placement(bm, pl - 1)
+    for bm, li in zip((64, 16, 8), args.lane_idx or ()):
+        if li:
+            plan.set_lane_indices(bm, li - 1)
     if args.hot_bytes is not None:
         plan.set_hot_rows(args.hot_bytes)
     return th
@@ -255,7 +258,7 @@ def apply_pins(plan, args):
 
 def pins_of(plan, th, cls):
     """The bench flags that replay this plan's tuned configuration."""
-    f, o, t, w, s, p = [], [], [], [], [], []
+    f, o, t, w, s, p, li = [], [], [], [], [], [], []
     for bm in (64, 16, 8):
         c = cls.get(bm)
         f.append({"dense": 1, "packed": 2}[c["format"]] if c else 0)
@@ -264,9 +267,10 @@ def pins_of(plan, th, cls):
         w.append(c["chunk_width"] if c else 0)
         s.append(c["stages"] if c else 0)
         p.append({"contiguous": 1, "interleaved": 2, "chunk-xcd": 3}[c["placement"]] if c else 0)
+        li.append(c["lane_indices"] + 1 if c else 0)
     j = lambda v: ",".join(str(x) for x in v)
     return (f"--no-tune --th {j(th)} --format {j(f)} --order {j(o)} --tpw {j(t)} --width {j(w)} "
-            f"--stages {j(s)} --place {j(p)} --hot-bytes {plan.get_hot_rows()[1]}")
+            f"--stages {j(s)} --place {j(p)} --lane-idx {j(li)} --hot-bytes {plan.get_hot_rows()[1]}")
 
 
 def measure(tsp, hip, config, prec, colB, args, headline):
@@ -354,6 +358,7 @@ def measure(tsp, hip, config, prec, colB, args, headline):
                    "format": {1: "dense", 2: "packed"}.get(plan.get_format(bm), "?"),
                    "order": {0: "side-by-side", 1: "side-by-side", 2: "chunk-major"}[v[3]],
                    "tasks_per_wave": max(1, v[2]), "stages": max(1, v[1]), "chunk_width": w,
+                   "lane_indices": max(0, plan.get_lane_indices(bm)),
                    "placement": {0: "contiguous", 1: "interleaved", 2: "chunk-xcd"}.get(plan.get_placement(bm), "?"),
                    "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9,
                    "gathered_lines": lines, "glines_per_s": lines / (cms * 1e-3) / 1e9}
@@ -367,7 +372,7 @@ def measure(tsp, hip, config, prec, colB, args, headline):
     # profiled HBM traffic applies only to the same instantiation and hot rows
     # (plans launch tf32 on operands they rounded once: kernel precision code 2)
     kname = (f"spmm_kernel<{dom}, {dk['chunk_width']}, {2 if prec == 1 else 0}, {dk['stages']}, "
-             f"{'true' if dk['format'] == 'packed' else 'false'}>")
+             f"{'true' if dk['format'] == 'packed' else 'false'}, {'true' if dk['lane_indices'] else 'false'}>")
     traffic, traffic_note = None, "no profile of this workload in profiles/"
     prof = os.path.join(ROOT, "profiles", f"traffic_config{config}_{pname}_{colB}.json")
     if os.path.exists(prof):
@@ -489,10 +494,12 @@ def main():
     ap.add_argument("--width", type=ints3, default=None,
                     help="pin the chunk width per class 64,16,8 (32, 64, 128; 0 keep)")
     ap.add_argument("--stages", type=ints3, default=None,
-                    help="pin the pipeline depth per class 64,16,8 (1-4; 0 keep)")
+                    help="pin the pipeline depth per class 64,16,8 (1-3; 0 keep)")
     ap.add_argument("--place", type=ints3, default=None,
                     help="pin the XCD placement per class 64,16,8 (1 contiguous, 2 interleaved, 3 one column "
                          "chunk per XCD group, 0 keep)")
+    ap.add_argument("--lane-idx", type=ints3, default=None,
+                    help="pin lane-loaded column indices per class 64,16,8 (1 off, 2 on, 0 keep)")
     ap.add_argument("--hot-bytes", type=int, default=None,
                     help="pin the hot B row budget in bytes after tuning (0: no hot rows)")
     ap.add_argument("--tune-cold", action="store_true",
@@ -548,7 +555,8 @@ def main():
     targets = {}
     for cfg in [int(x) for x in args.targets.split(",") if x.strip()]:
         targ = argparse.Namespace(**vars(args))
-        for k in ("th", "format", "order", "tpw", "width", "stages", "place", "hot_bytes", "gamma", "delta"):
+        for k in ("th", "format", "order", "tpw", "width", "stages", "place", "lane_idx", "hot_bytes", "gamma",
+                  "delta"):
             setattr(targ, k, None)
         targ.no_tune = False
         targ.tune_cold = False

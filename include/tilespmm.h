@@ -210,6 +210,11 @@ int tsp_plan_get_variant(tsp_plan *plan, int bm, int *w, int *stages, int *tasks
 /* Workgroup placement of one class on the XCDs (TSP_PLACE_CONTIGUOUS or
  * TSP_PLACE_INTERLEAVED, see tsp_spmm_launch_placed); tsp_plan_tune times
  * both.  get returns -1 on a bad argument. */
+/* Lane-loaded column indices (TSP_LAUNCH_LANE_INDICES) for a class on the
+ * packed format: 1 on, 0 off (64-row classes: off only); tsp_plan_tune picks.
+ * get returns -1 on a bad argument. */
+int tsp_plan_set_lane_indices(tsp_plan *plan, int bm, int on);
+int tsp_plan_get_lane_indices(tsp_plan *plan, int bm);
 int tsp_plan_set_placement(tsp_plan *plan, int bm, int placement);
 int tsp_plan_get_placement(tsp_plan *plan, int bm);
 /* Hot B rows (see tsp_hot_rows_gather): copy the most-gathered B rows, at

@@ -125,7 +125,7 @@ int tsp_spmm_launch(int bm, int prec, int rowblkblock, int colB_p,
 
 /* Same launch with an explicit kernel variant, for tuning drivers: chunk
  * width w (output columns per wave: 32, 64 or 128; 64-row tiles 32 or 64),
- * software-pipeline depth stages (1-4 tiles in flight per wave) and
+ * software-pipeline depth stages (1-3 tiles in flight per wave) and
  * tasks_per_wave (consecutive tasks one wave streams) and the order of the
  * column chunks (1: the chunks of one task range run side by side, 2:
  * chunk-major, every range of chunk 0 first).  Values <= 0 pick the defaults
@@ -185,6 +185,13 @@ int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const 
  * The plan rounds its copies of A and B once when they enter it and
  * launches this way.  No counterpart in the reference. */
 #define TSP_LAUNCH_OPERANDS_TF32 1
+/* TSP_LAUNCH_LANE_INDICES (packed A format only): each lane reads the
+ * column indices of its B rows with one vector load instead of the scalar
+ * loads plus a per-lane select chain; same result, fewer VALU instructions
+ * per tile, one more vector memory instruction.  The plan's tuning picks
+ * per class (faster on the gather-bound RMAT and power-law fp16 classes,
+ * slower on banded and block-sparse ones). */
+#define TSP_LAUNCH_LANE_INDICES 2
 int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
                        const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,
                        const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,

@@ -114,9 +114,10 @@ def test_random_all_classes(gpu, orc, prec, colB):
 
 @pytest.mark.parametrize("prec", [0, 1])
 def test_every_kernel_variant(gpu, orc, prec):
-    """Every (chunk width, pipeline depth, tasks per wave) variant of every
-    class, with every XCD placement its chunk count allows, gives the
-    oracle's result, split tasks included."""
+    """Every (chunk width, pipeline depth, tasks per wave, scalar or
+    lane-loaded column indices on the packed format) variant of every class,
+    with every XCD placement its chunk count allows, gives the oracle's
+    result, split tasks included."""
     tsp = gpu
     rng = np.random.default_rng(50 + prec)
     A = random_matrix(tsp, rng, 611, 509, 45, prec, heavy_rows=4)
@@ -133,13 +134,15 @@ def test_every_kernel_variant(gpu, orc, prec):
                 plan.set_format(bm, fmt)
                 assert plan.get_format(bm) == fmt
                 for w in ((32, 64) if bm == 64 else (32, 64, 128)):
-                    for s in (1, 2, 3, 4):
+                    for s, li in [(s, li) for s in (1, 2, 3) for li in ((0, 1) if fmt == 2 else (0,))]:
                         for tpw, order in ((1, 1), (3, 2), (0, 0)):
                             for place in ((0, 1, 2) if cbp // w in (2, 4, 8) else (0, 1)):
-                                tag = (f"prec={prec} bm={bm} fmt={fmt} w={w} s={s} tpw={tpw} order={order} "
-                                       f"place={place}")
+                                tag = (f"prec={prec} bm={bm} fmt={fmt} w={w} s={s} lane_idx={li} tpw={tpw} "
+                                       f"order={order} place={place}")
                                 say("variant " + tag)
                                 plan.set_variant(bm, w, s, tpw, order)
+                                plan.set_lane_indices(bm, li)
+                                assert plan.get_lane_indices(bm) == li
                                 plan.set_placement(bm, place)
                                 assert plan.get_placement(bm) == place
                                 plan.run(zero_c=True)

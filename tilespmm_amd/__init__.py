@@ -230,6 +230,8 @@ HOST_SYMBOLS = {
     "tsp_plan_get_format": (C.c_int, [_P, C.c_int]),
     "tsp_plan_get_variant": (C.c_int, [_P, C.c_int, _IP, _IP, _IP, _IP]),
     "tsp_plan_set_placement": (C.c_int, [_P, C.c_int, C.c_int]),
+    "tsp_plan_set_lane_indices": (C.c_int, [_P, C.c_int, C.c_int]),
+    "tsp_plan_get_lane_indices": (C.c_int, [_P, C.c_int]),
     "tsp_plan_get_placement": (C.c_int, [_P, C.c_int]),
     "tsp_plan_set_hot_rows": (C.c_int, [_P, C.c_longlong]),
     "tsp_plan_set_tune_mode": (C.c_int, [_P, C.c_int]),
@@ -657,6 +659,13 @@ class Plan:
         v = [C.c_int() for _ in range(4)]
         _check("tsp_plan_get_variant", load()[1].tsp_plan_get_variant(self.p, bm, *[C.byref(x) for x in v]))
         return tuple(x.value for x in v)
+
+    def set_lane_indices(self, bm: int, on: bool):
+        """Packed format: lane-loaded column indices (True) or scalar ones."""
+        _check("tsp_plan_set_lane_indices", load()[1].tsp_plan_set_lane_indices(self.p, bm, int(on)))
+
+    def get_lane_indices(self, bm: int) -> int:
+        return load()[1].tsp_plan_get_lane_indices(self.p, bm)
 
     def set_placement(self, bm: int, placement: int):
         """XCD placement: 0 = contiguous eighths, 1 = runs dealt round-robin."""

@@ -271,7 +271,8 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
                        int c_rows, void *stream, int w, int stages, int tasks_per_wave, int order,
                        int placement, int flags)
 {
-    if (flags & ~TSP_LAUNCH_OPERANDS_TF32) return TSP_EINVAL;
+    if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES)) return TSP_EINVAL;
+    if ((flags & TSP_LAUNCH_LANE_INDICES) && !d_bitmap) return TSP_EINVAL;
     if (bm != 64 && bm != 16 && bm != 8) return TSP_EINVAL;
     if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
     if (colB_p != 32 && (colB_p <= 0 || colB_p % 64 != 0)) return TSP_EINVAL;
@@ -285,7 +286,7 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
     const int kprec = prec == TSP_PREC_TF32 && (flags & TSP_LAUNCH_OPERANDS_TF32) ? tsp::kPrecTf32Exact : prec;
     return tsp::launch(bm, kprec, rowblkblock, colB_p, d_val, d_bitmap, d_vptr, d_rows, d_colstart, d_B,
                        d_C, d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave, order,
-                       placement);
+                       placement, (flags & TSP_LAUNCH_LANE_INDICES) != 0);
 }
 
 int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,

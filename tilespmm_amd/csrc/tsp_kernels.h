@@ -54,14 +54,14 @@ constexpr int kPlaceChunkXcd = 2;
 int default_chunk_width(int bm, int colB_p);
 int default_stages(int bm, int prec, int w);
 bool valid_variant(int bm, int w, int s);
-const void *select_kernel(int bm, int prec, int w, int s, bool packed);
+const void *select_kernel(int bm, int prec, int w, int s, bool packed, bool lane_idx = false);
 // w, s, tpw <= 0 select the defaults; order 0 = default, 1 = chunks of one
 // task range adjacent, 2 = chunk-major.  bmp != nullptr selects the
 // bitmap-packed A format (val = packed values, vptr = per-tile offsets).
 int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint64_t *bmp,
            const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
            const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order,
-           int placement = kPlaceContiguous);
+           int placement = kPlaceContiguous, bool lane_idx = false);
 int launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
 constexpr int kGatherBlocks = 8192;      // gather probe grid: 8192 x 256 threads
 int launch_gather(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed, void *sink,

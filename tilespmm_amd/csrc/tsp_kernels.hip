@@ -90,7 +90,7 @@ __device__ __forceinline__ int place_block(int b, int nb, int placement)
 // of its set bits, in bit order, at `val_` + vptr[tile].  Each lane expands its
 // slice of the tile into MFMA operand registers.  Without PK, `val_` holds
 // dense canonical tiles and `bmp` / `vptr` are unused.
-template <int BM, int W, int PREC, int S, bool PK>
+template <int BM, int W, int PREC, int S, bool PK, bool LI>
 __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     int ntasks, int nchunks, int tasks_per_wave, int chunk_major, const void *__restrict__ val_,
     const uint64_t *__restrict__ bmp, const int *__restrict__ vptr,
@@ -167,11 +167,16 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
     const int ln = lane & 15;        // MFMA row (A) / column (B, D) index
     const int lq = lane >> 4;        // MFMA lane group
 
+    // Panel rows of the lane's NV B loads.  Scalar column indices (LI
+    // false): load i covers rows i*RPI .. i*RPI+RPI-1, row i*RPI + lane/VPR
+    // for this lane.  Lane-loaded indices (LI): the lane's rows are the NV
+    // consecutive rows (lane/VPR)*NV + i, whose column indices are
+    // consecutive in the tile's index list (one vector load).
     int prow[NV], pcol[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int v = lane + 64 * i;
-        prow[i] = v / VPR;
+        prow[i] = LI ? (lane / VPR) * NV + i : v / VPR;
         pcol[i] = (v % VPR) * VV;
     }
 
@@ -278,20 +283,32 @@ __global__ __launch_bounds__(kBlockThreads) void spmm_kernel(
             }
         }
     };
-    // Column indices are wave-uniform: read them with scalar loads (counted
-    // by lgkmcnt, so waiting for them never waits for the vector loads of
-    // the B/A ring), then each lane picks the index of its panel row.
+    // Column indices.  Scalar (LI false): the tile's BN indices are
+    // wave-uniform; they are read with scalar loads (counted by lgkmcnt, so
+    // waiting for them never waits for the vector loads of the B/A ring),
+    // then each lane picks the index of each of its panel rows with a select
+    // chain (RPI - 1 selects per load).  Lane-loaded (LI): each lane reads
+    // its NV consecutive indices with one vector load and needs no selects,
+    // at the cost of a vector memory instruction per tile.  Either way the
+    // indices of tile t+S are read S tiles before the B gathers that use them.
     constexpr int RPI = 64 / VPR;                // panel rows one vector instruction covers
     const int lrow = lane / VPR;
-    using CSV = int __attribute__((ext_vector_type(BN)));
-    auto load_cs = [&](int t, CSV &cs) { cs = *(cptr<CSV>)(colidx + (size_t)t * BN); };
+    using CSV = int __attribute__((ext_vector_type(LI ? NV : BN)));
+    auto load_cs = [&](int t, CSV &cs) {
+        if constexpr (LI) cs = *(const CSV *)(colidx + (size_t)t * BN + lrow * NV);
+        else cs = *(cptr<CSV>)(colidx + (size_t)t * BN);
+    };
     auto select_cid = [&](const CSV &cs, int (&dst)[NV]) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            int v = cs[i * RPI];
+            if constexpr (LI) {
+                dst[i] = cs[i];
+            } else {
+                int v = cs[i * RPI];
 #pragma unroll
-            for (int r = 1; r < RPI; ++r) v = lrow == r ? cs[i * RPI + r] : v;
-            dst[i] = v;
+                for (int r = 1; r < RPI; ++r) v = lrow == r ? cs[i * RPI + r] : v;
+                dst[i] = v;
+            }
         }
     };
     auto load_b = [&](const int (&cid)[NV], u4 (&dst)[NV]) {
@@ -542,44 +559,45 @@ int default_stages(int bm, int prec, int w)
 
 bool valid_variant(int bm, int w, int s)
 {
-    if (s < 1 || s > 4) return false;
+    if (s < 1 || s > 3) return false;
     if (bm == 64) return w == 32 || w == 64;
     return w == 32 || w == 64 || w == 128;
 }
 
 #define TSP_FOR_EACH_VARIANT(X)                                                                \
-    X(64, 32, 1) X(64, 32, 2) X(64, 32, 3) X(64, 32, 4)                                        \
-    X(64, 64, 1) X(64, 64, 2) X(64, 64, 3) X(64, 64, 4)                                        \
-    X(16, 32, 1) X(16, 32, 2) X(16, 32, 3) X(16, 32, 4)                                        \
-    X(16, 64, 1) X(16, 64, 2) X(16, 64, 3) X(16, 64, 4)                                        \
-    X(16, 128, 1) X(16, 128, 2) X(16, 128, 3) X(16, 128, 4)                                    \
-    X(8, 32, 1) X(8, 32, 2) X(8, 32, 3) X(8, 32, 4)                                            \
-    X(8, 64, 1) X(8, 64, 2) X(8, 64, 3) X(8, 64, 4)                                            \
-    X(8, 128, 1) X(8, 128, 2) X(8, 128, 3) X(8, 128, 4)
+    X(64, 32, 1) X(64, 32, 2) X(64, 32, 3)                                                     \
+    X(64, 64, 1) X(64, 64, 2) X(64, 64, 3)                                                     \
+    X(16, 32, 1) X(16, 32, 2) X(16, 32, 3)                                                     \
+    X(16, 64, 1) X(16, 64, 2) X(16, 64, 3)                                                     \
+    X(16, 128, 1) X(16, 128, 2) X(16, 128, 3)                                                  \
+    X(8, 32, 1) X(8, 32, 2) X(8, 32, 3)                                                        \
+    X(8, 64, 1) X(8, 64, 2) X(8, 64, 3)                                                        \
+    X(8, 128, 1) X(8, 128, 2) X(8, 128, 3)
 
 #define TSP_FOR_EACH_PACKED_VARIANT(X)                                                         \
-    X(16, 32, 1) X(16, 32, 2) X(16, 32, 3) X(16, 32, 4)                                        \
-    X(16, 64, 1) X(16, 64, 2) X(16, 64, 3) X(16, 64, 4)                                        \
-    X(16, 128, 1) X(16, 128, 2) X(16, 128, 3) X(16, 128, 4)                                    \
-    X(8, 32, 1) X(8, 32, 2) X(8, 32, 3) X(8, 32, 4)                                            \
-    X(8, 64, 1) X(8, 64, 2) X(8, 64, 3) X(8, 64, 4)                                            \
-    X(8, 128, 1) X(8, 128, 2) X(8, 128, 3) X(8, 128, 4)
+    X(16, 32, 1) X(16, 32, 2) X(16, 32, 3)                                                     \
+    X(16, 64, 1) X(16, 64, 2) X(16, 64, 3)                                                     \
+    X(16, 128, 1) X(16, 128, 2) X(16, 128, 3)                                                  \
+    X(8, 32, 1) X(8, 32, 2) X(8, 32, 3)                                                        \
+    X(8, 64, 1) X(8, 64, 2) X(8, 64, 3)                                                        \
+    X(8, 128, 1) X(8, 128, 2) X(8, 128, 3)
 
-const void *select_kernel(int bm, int prec, int w, int s, bool packed)
+const void *select_kernel(int bm, int prec, int w, int s, bool packed, bool lane_idx)
 {
-#define TSP_K(BMv, Wv, Sv)                                                                            \
-    if (!packed && bm == BMv && w == Wv && s == Sv)                                                   \
-        return prec == TSP_PREC_FP16   ? (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, false> \
-               : prec == kPrecTf32Exact ? (const void *)&spmm_kernel<BMv, Wv, kPrecTf32Exact, Sv, false> \
-                                       : (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, false>;
-    TSP_FOR_EACH_VARIANT(TSP_K)
-#undef TSP_K
-#define TSP_K(BMv, Wv, Sv)                                                                            \
-    if (packed && bm == BMv && w == Wv && s == Sv)                                                    \
-        return prec == TSP_PREC_FP16   ? (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, true>  \
-               : prec == kPrecTf32Exact ? (const void *)&spmm_kernel<BMv, Wv, kPrecTf32Exact, Sv, true> \
-                                       : (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, true>;
-    TSP_FOR_EACH_PACKED_VARIANT(TSP_K)
+#define TSP_K(BMv, Wv, Sv, PKv, LIv)                                                                    \
+    if (packed == PKv && lane_idx == LIv && bm == BMv && w == Wv && s == Sv)                            \
+        return prec == TSP_PREC_FP16   ? (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, PKv, LIv>  \
+               : prec == kPrecTf32Exact ? (const void *)&spmm_kernel<BMv, Wv, kPrecTf32Exact, Sv, PKv, LIv> \
+                                       : (const void *)&spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, PKv, LIv>;
+#define TSP_KD(BMv, Wv, Sv) TSP_K(BMv, Wv, Sv, false, false)
+#define TSP_KP(BMv, Wv, Sv) TSP_K(BMv, Wv, Sv, true, false)
+#define TSP_KL(BMv, Wv, Sv) TSP_K(BMv, Wv, Sv, true, true)
+    TSP_FOR_EACH_VARIANT(TSP_KD)
+    TSP_FOR_EACH_PACKED_VARIANT(TSP_KP)
+    TSP_FOR_EACH_PACKED_VARIANT(TSP_KL)
+#undef TSP_KD
+#undef TSP_KP
+#undef TSP_KL
 #undef TSP_K
     return nullptr;
 }
@@ -601,10 +619,11 @@ static bool resolve_variant(int bm, int prec, int colB_p, int &w, int &s, int &n
 int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint64_t *bmp,
            const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
            const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order,
-           int placement)
+           int placement, bool lane_idx)
 {
     const bool packed = bmp != nullptr;
     if (packed && (bm == 64 || !vptr)) return TSP_EINVAL;
+    if (lane_idx && !packed) return TSP_EINVAL;          // lane-loaded indices: packed kernels only
     if (placement != kPlaceContiguous && placement != kPlaceInterleaved && placement != kPlaceChunkXcd)
         return TSP_EINVAL;
     int nchunks = 0, cm = 0;
@@ -628,28 +647,31 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
     }
     if (blocks > 0x7fffffffLL) return TSP_EINVAL;
     const dim3 grid3((unsigned)blocks);
-#define TSP_L(BMv, Wv, Sv, PKv)                                                                 \
-    if (packed == PKv && bm == BMv && w == Wv && s == Sv) {                                     \
+#define TSP_L(BMv, Wv, Sv, PKv, LIv)                                                            \
+    if (packed == PKv && lane_idx == LIv && bm == BMv && w == Wv && s == Sv) {                  \
         if (prec == TSP_PREC_FP16)                                                              \
-            spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, PKv><<<grid3, kBlockThreads, 0, st>>>(       \
+            spmm_kernel<BMv, Wv, TSP_PREC_FP16, Sv, PKv, LIv><<<grid3, kBlockThreads, 0, st>>>(  \
                 ntasks, nchunks, tpw, cm, val, bmp, vptr, rows, colstart, B, C, colidx, colB_p, \
                 c_rows, placement);                                                             \
         else if (prec == kPrecTf32Exact)                                                        \
-            spmm_kernel<BMv, Wv, kPrecTf32Exact, Sv, PKv><<<grid3, kBlockThreads, 0, st>>>(      \
+            spmm_kernel<BMv, Wv, kPrecTf32Exact, Sv, PKv, LIv><<<grid3, kBlockThreads, 0, st>>>( \
                 ntasks, nchunks, tpw, cm, val, bmp, vptr, rows, colstart, B, C, colidx, colB_p, \
                 c_rows, placement);                                                             \
         else                                                                                    \
-            spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, PKv><<<grid3, kBlockThreads, 0, st>>>(       \
+            spmm_kernel<BMv, Wv, TSP_PREC_TF32, Sv, PKv, LIv><<<grid3, kBlockThreads, 0, st>>>(  \
                 ntasks, nchunks, tpw, cm, val, bmp, vptr, rows, colstart, B, C, colidx, colB_p, \
                 c_rows, placement);                                                             \
         return (int)hipGetLastError();                                                          \
     }
-#define TSP_LD(BMv, Wv, Sv) TSP_L(BMv, Wv, Sv, false)
-#define TSP_LP(BMv, Wv, Sv) TSP_L(BMv, Wv, Sv, true)
+#define TSP_LD(BMv, Wv, Sv) TSP_L(BMv, Wv, Sv, false, false)
+#define TSP_LP(BMv, Wv, Sv) TSP_L(BMv, Wv, Sv, true, false)
+#define TSP_LL(BMv, Wv, Sv) TSP_L(BMv, Wv, Sv, true, true)
     TSP_FOR_EACH_VARIANT(TSP_LD)
     TSP_FOR_EACH_PACKED_VARIANT(TSP_LP)
+    TSP_FOR_EACH_PACKED_VARIANT(TSP_LL)
 #undef TSP_LD
 #undef TSP_LP
+#undef TSP_LL
 #undef TSP_L
     return TSP_EINVAL;
 }

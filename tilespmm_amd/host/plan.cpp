@@ -34,6 +34,7 @@ struct ClassDev {
     int th = 0;
     int ntasks = 0;
     int var_w = 0, var_s = 0, var_tpw = 0, var_order = 0;   // kernel variant, 0 = library default
+    int var_li = 0;               // packed format: lane-loaded column indices (TSP_LAUNCH_LANE_INDICES)
     int fmt = 1;                  // A format on the device: 1 dense tiles, 2 bitmap-packed
     bool pack_ok = false;         // packed format is worth trying (fewer bytes)
     void *d_pval = nullptr;       // packed values (+4 elements of padding)
@@ -205,7 +206,8 @@ static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
     return tsp_spmm_launch_ex(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val, pk ? c.d_bmp : nullptr,
                               pk ? c.d_vptr : nullptr, c.d_rows, c.d_colstart, p->d_B, p->d_C, c.d_colidx, p->rowA,
                               stream ? stream : c.stream, c.var_w, c.var_s, c.var_tpw, c.var_order, c.place,
-                              p->prec == TSP_PREC_TF32 ? TSP_LAUNCH_OPERANDS_TF32 : 0);
+                              (p->prec == TSP_PREC_TF32 ? TSP_LAUNCH_OPERANDS_TF32 : 0) |
+                                  (pk && c.var_li ? TSP_LAUNCH_LANE_INDICES : 0));
 }
 
 extern "C" int tsp_plan_set_format(tsp_plan *p, int bm, int fmt)
@@ -246,6 +248,26 @@ extern "C" int tsp_plan_set_variant(tsp_plan *p, int bm, int w, int stages, int 
             return TSP_OK;
         }
     return TSP_EINVAL;
+}
+
+extern "C" int tsp_plan_set_lane_indices(tsp_plan *p, int bm, int on)
+{
+    if (!p || (on != 0 && on != 1)) return TSP_EINVAL;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) {
+            if (on && bm == 64) return TSP_EINVAL;
+            c.var_li = on;
+            return TSP_OK;
+        }
+    return TSP_EINVAL;
+}
+
+extern "C" int tsp_plan_get_lane_indices(tsp_plan *p, int bm)
+{
+    if (!p) return -1;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) return c.var_li;
+    return -1;
 }
 
 extern "C" int tsp_plan_set_placement(tsp_plan *p, int bm, int placement)
@@ -928,26 +950,41 @@ static int tune_class(tsp_plan *p, ClassDev &c)
                         place_name[wo[j].place], wms[j], j == bw ? "  <- kept" : "");
     }
 
-    // 4. pipeline depth: 2 or 3 tiles in flight per wave against 1, the rest
-    //    as kept; a deeper pipeline holds more B gathers in flight per wave but
-    //    costs registers (occupancy), so it is kept only when 1% faster
+    // 4. pipeline depth (1-3 tiles in flight per wave) x, on the packed
+    //    format, scalar or lane-loaded column indices; the rest as kept.  A
+    //    deeper pipeline holds more B gathers in flight per wave but costs
+    //    registers (occupancy); lane-loaded indices save the select chain
+    //    for a vector load.  Depth 1 with scalar indices stays unless another
+    //    option is 1% faster.
     const int w_kept = c.var_w ? c.var_w : k.cols_per_task;
-    double sms[4] = {1e30, 1e30, 1e30, 1e30};
+    const int nli = c.fmt == 2 ? 2 : 1;
+    double sms[2][4];
+    for (auto &r : sms)
+        for (double &x : r) x = 1e30;
     for (int round = 0; round < 2; ++round)
-        for (int st = 1; st <= 3; ++st) {
-            c.var_w = w_kept;
-            c.var_s = st;
-            double t = 0;
-            TSP_TRY(tune_time_class(p, c.bm, &t));
-            sms[st] = std::min(sms[st], t);
-        }
-    int sb = 1;
-    for (int st = 2; st <= 3; ++st)
-        if (sms[st] < 0.99 * sms[sb]) sb = st;
-    c.var_s = sb;
-    if (log)
+        for (int li = 0; li < nli; ++li)
+            for (int st = 1; st <= 3; ++st) {
+                c.var_w = w_kept;
+                c.var_s = st;
+                c.var_li = li;
+                double t = 0;
+                TSP_TRY(tune_time_class(p, c.bm, &t));
+                sms[li][st] = std::min(sms[li][st], t);
+            }
+    int sb = 1, lb = 0;
+    for (int li = 0; li < nli; ++li)
         for (int st = 1; st <= 3; ++st)
-            fprintf(stderr, "tune bm=%d stages %d: %.5f ms%s\n", c.bm, st, sms[st], st == sb ? "  <- kept" : "");
+            if (sms[li][st] < 0.99 * sms[lb][sb]) {
+                sb = st;
+                lb = li;
+            }
+    c.var_s = sb;
+    c.var_li = lb;
+    if (log)
+        for (int li = 0; li < nli; ++li)
+            for (int st = 1; st <= 3; ++st)
+                fprintf(stderr, "tune bm=%d stages %d %s indices: %.5f ms%s\n", c.bm, st, li ? "lane" : "scalar",
+                        sms[li][st], st == sb && li == lb ? "  <- kept" : "");
     return TSP_OK;
 }
 
@@ -1067,7 +1104,7 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
         if (hot_tuning && !kept) {
             // the variants were tuned for the hot rows: tune them again without
             for (ClassDev &c : p->cls) {
-                c.var_w = c.var_s = c.var_tpw = c.var_order = 0;
+                c.var_w = c.var_s = c.var_tpw = c.var_order = c.var_li = 0;
                 c.place = TSP_PLACE_CONTIGUOUS;
                 TSP_TRY(tune_class(p, c));
             }
