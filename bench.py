@@ -251,6 +251,10 @@ def apply_pins(plan, args):
     for bm, li in zip((64, 16, 8), args.lane_idx or ()):
         if li:
             plan.set_lane_indices(bm, li - 1)
+    lags = args.panel_lag or (2, 2, 2)
+    for bm, pr, lg in zip((64, 16, 8), args.panels or (), lags):
+        if pr:
+            plan.set_panels(bm, pr, lg)
     if args.hot_bytes is not None:
         plan.set_hot_rows(args.hot_bytes)
     return th
@@ -258,7 +262,7 @@ def apply_pins(plan, args):
 
 def pins_of(plan, th, cls):
     """The bench flags that replay this plan's tuned configuration."""
-    f, o, t, w, s, p, li = [], [], [], [], [], [], []
+    f, o, t, w, s, p, li, pr, lg = [], [], [], [], [], [], [], [], []
     for bm in (64, 16, 8):
         c = cls.get(bm)
         f.append({"dense": 1, "packed": 2}[c["format"]] if c else 0)
@@ -268,9 +272,12 @@ def pins_of(plan, th, cls):
         s.append(c["stages"] if c else 0)
         p.append({"contiguous": 1, "interleaved": 2, "chunk-xcd": 3}[c["placement"]] if c else 0)
         li.append(c["lane_indices"] + 1 if c else 0)
+        pr.append(c["panel_rows"] if c else 0)
+        lg.append(c["panel_lag"] if c else 0)
     j = lambda v: ",".join(str(x) for x in v)
     return (f"--no-tune --th {j(th)} --format {j(f)} --order {j(o)} --tpw {j(t)} --width {j(w)} "
-            f"--stages {j(s)} --place {j(p)} --lane-idx {j(li)} --hot-bytes {plan.get_hot_rows()[1]}")
+            f"--stages {j(s)} --place {j(p)} --lane-idx {j(li)} --panels {j(pr)} --panel-lag {j(lg)} "
+            f"--hot-bytes {plan.get_hot_rows()[1]}")
 
 
 def measure(tsp, hip, config, prec, colB, args, headline):
@@ -360,6 +367,7 @@ def measure(tsp, hip, config, prec, colB, args, headline):
                    "tasks_per_wave": max(1, v[2]), "stages": max(1, v[1]), "chunk_width": w,
                    "lane_indices": max(0, plan.get_lane_indices(bm)),
                    "placement": {0: "contiguous", 1: "interleaved", 2: "chunk-xcd"}.get(plan.get_placement(bm), "?"),
+                   "panel_rows": plan.get_panels(bm)[0], "panel_lag": plan.get_panels(bm)[1],
                    "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9,
                    "gathered_lines": lines, "glines_per_s": lines / (cms * 1e-3) / 1e9}
     dom = max(cls, key=lambda k: cls[k]["ms"])
@@ -368,11 +376,13 @@ def measure(tsp, hip, config, prec, colB, args, headline):
     step_bytes = alg_bytes(A.rows, A.nnz, s, k_all, colB, s)
     step_gbs = step_bytes / (ms * 1e-3) / 1e9
 
-    # the dominant kernel's instantiation spmm_kernel<BM, W, PREC, S, PK>; the
-    # profiled HBM traffic applies only to the same instantiation and hot rows
-    # (plans launch tf32 on operands they rounded once: kernel precision code 2)
+    # the dominant kernel's instantiation spmm_kernel<BM, W, PREC, S, PK, LI, SY>;
+    # the profiled HBM traffic applies only to the same instantiation and hot
+    # rows (plans launch tf32 on operands they rounded once: kernel precision
+    # code 2)
+    tf = lambda b: "true" if b else "false"
     kname = (f"spmm_kernel<{dom}, {dk['chunk_width']}, {2 if prec == 1 else 0}, {dk['stages']}, "
-             f"{'true' if dk['format'] == 'packed' else 'false'}, {'true' if dk['lane_indices'] else 'false'}>")
+             f"{tf(dk['format'] == 'packed')}, {tf(dk['lane_indices'])}, {tf(dk['panel_rows'])}>")
     traffic, traffic_note = None, "no profile of this workload in profiles/"
     prof = os.path.join(ROOT, "profiles", f"traffic_config{config}_{pname}_{colB}.json")
     if os.path.exists(prof):
@@ -500,6 +510,10 @@ def main():
                          "chunk per XCD group, 0 keep)")
     ap.add_argument("--lane-idx", type=ints3, default=None,
                     help="pin lane-loaded column indices per class 64,16,8 (1 off, 2 on, 0 keep)")
+    ap.add_argument("--panels", type=ints3, default=None,
+                    help="pin the panel-synchronised sweep per class: B rows per panel (0 = off)")
+    ap.add_argument("--panel-lag", type=ints3, default=None,
+                    help="lead in panels a wave may have on the slowest (with --panels; default 2)")
     ap.add_argument("--hot-bytes", type=int, default=None,
                     help="pin the hot B row budget in bytes after tuning (0: no hot rows)")
     ap.add_argument("--tune-cold", action="store_true",
@@ -555,7 +569,8 @@ def main():
     targets = {}
     for cfg in [int(x) for x in args.targets.split(",") if x.strip()]:
         targ = argparse.Namespace(**vars(args))
-        for k in ("th", "format", "order", "tpw", "width", "stages", "place", "lane_idx", "hot_bytes", "gamma",
+        for k in ("th", "format", "order", "tpw", "width", "stages", "place", "lane_idx", "panels", "panel_lag", "hot_bytes",
+                  "gamma",
                   "delta"):
             setattr(targ, k, None)
         targ.no_tune = False

@@ -217,6 +217,14 @@ int tsp_plan_set_lane_indices(tsp_plan *plan, int bm, int on);
 int tsp_plan_get_lane_indices(tsp_plan *plan, int bm);
 int tsp_plan_set_placement(tsp_plan *plan, int bm, int placement);
 int tsp_plan_get_placement(tsp_plan *plan, int bm);
+/* Panel-synchronised sweep (tsp_spmm_launch_panels) for one class on the
+ * dense format: B rows per panel (a power of two, at least 64; 0 = off) and
+ * the lead in panels a wave may have on the slowest wave of its XCD (at
+ * least 1).  The plan allocates the class's 4 MB of counters on first use;
+ * tsp_plan_tune tries it for classes whose work fills the device a few
+ * times at most.  No counterpart in the reference. */
+int tsp_plan_set_panels(tsp_plan *plan, int bm, int panel_rows, int lag);
+int tsp_plan_get_panels(tsp_plan *plan, int bm, int *panel_rows, int *lag);
 /* Hot B rows (see tsp_hot_rows_gather): copy the most-gathered B rows, at
  * most budget_bytes of them (and at most TSP_HOT_MAX_BYTES), into spare rows
  * of the plan's B and point every class's tile columns at the copies; every

@@ -198,6 +198,30 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
                        int c_rows, void *stream, int w, int stages, int tasks_per_wave, int order,
                        int placement, int flags);
 
+/* Panel-synchronised sweep: tsp_spmm_launch_ex whose waves step through
+ * the B rows in panels of panel_rows rows (a power of two, at least 64;
+ * b_rows = rows of B the column indices can name).  The grid holds at most
+ * the workgroups that fit on the device at once, each wave running one task
+ * range per generation.  Within a generation, a wave about to load from
+ * panel q first waits (at most 20 us) until every wave of its XCD that has
+ * started has reached panel q - panel_lag, so the waves of one XCD gather
+ * from a window of about panel_lag + 1 panels, which that XCD's L2 holds.
+ * With one task per wave the tiles of a task come in ascending column
+ * order.  The result is the same as tsp_spmm_launch_ex's with the same
+ * arguments; only the timing changes.  d_sync: sync_ints ints of device
+ * memory for the wave counters, which each launch zeroes on the stream
+ * before it runs.  A launch needs generations x 8 x (panels + 1) x 512 of
+ * them; TSP_EINVAL if sync_ints is smaller, for TSP_PLACE_CHUNK_XCD, for a
+ * bad panel_rows or for panel_lag < 1.  Launches that share d_sync must not
+ * overlap.  No counterpart in the reference (its grid is one block per
+ * task). */
+int tsp_spmm_launch_panels(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
+                           const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,
+                           const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,
+                           int c_rows, void *stream, int w, int stages, int tasks_per_wave, int order,
+                           int placement, int flags, int b_rows, int panel_rows, int panel_lag, int *d_sync,
+                           long long sync_ints);
+
 /* Per-class entry points with the reference dispatcher names
  * (src/tilespmm_cuda.h:1634, :1672, :1710) and argument order. */
 int tsp_switch_v64(int prec, int rowblkblock, int colB_p, const void *d_val,

@@ -75,6 +75,20 @@ def test_error_strings_and_arg_checks(tsp):
     assert placed(16, None, None, 0) == 1001 and placed(16, None, None, 1) == 1001   # null buffers
     dummy = C.c_void_p(1)
     assert placed(64, dummy, dummy, 0) == 1001 and placed(8, dummy, None, 0) == 1001
+    # panel-synchronised sweep: contiguous or interleaved placement, panels a
+    # power of two of at least 64 rows, B rows and a counter buffer given;
+    # these refusals come before any device call
+    panels = lambda place, b_rows, panel_rows, sync, ints, ntasks=1, lag=2: hip.tsp_spmm_launch_panels(
+        16, 0, ntasks, 128, dummy, None, None, dummy, dummy, dummy, dummy, dummy, 0, None, 0, 0, 0, 0, place, 0,
+        b_rows, panel_rows, lag, sync, ints)
+    assert panels(2, 1000, 256, dummy, 1024) == 1001                # chunk per XCD group
+    for pr in (0, 32, 96, 1000):
+        assert panels(0, 1000, pr, dummy, 1024) == 1001             # bad panel size
+    assert panels(0, 0, 256, dummy, 1024) == 1001                   # no B rows
+    assert panels(0, 1000, 256, None, 1024) == 1001                 # no counters
+    assert panels(0, 1000, 256, dummy, 0) == 1001
+    assert panels(0, 1000, 256, dummy, 1024, lag=0) == 1001          # a lead of at least one panel
+    assert panels(1, 1000, 256, dummy, 1024, ntasks=0) == 0          # nothing to do
 
 
 def test_cli_usage_and_errors(tmp_path):

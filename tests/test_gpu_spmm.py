@@ -153,6 +153,56 @@ def test_every_kernel_variant(gpu, orc, prec):
 
 
 @pytest.mark.parametrize("prec", [0, 1])
+def test_panel_sweep_and_wide_chunks(gpu, orc, prec):
+    """The panel-synchronised sweep (tsp_plan_set_panels, dense format) and
+    the 256-column chunks: every class, chunk width, depth, order, placement
+    and panel size gives the oracle's result; without split tasks the result
+    is bit-identical to the unsynchronised launch of the same variant (the
+    sweep only changes when a wave loads), and repeated launches (the
+    counters clear themselves) repeat it.  The 8-row class holds enough
+    row-blocks for several generations of the capped grid."""
+    tsp = gpu
+    rng = np.random.default_rng(70 + prec)
+    A = random_matrix(tsp, rng, 20000, 6000, 24, prec, heavy_rows=6)
+    colB = 256
+    B, cbp = random_b(tsp, rng, A.cols, colB, prec)
+    rows = np.unique(np.concatenate([rng.choice(A.rows, 3000, replace=False),
+                                     np.argsort(np.diff(A.rowptr))[-20:]]))
+    Cref, Cabs = reference(orc, A, B, colB, rows)
+    for g, d, bm in [(0.0, 1.5, 64), (5.0, 0.0, 16), (5.0, 3.0, 8)]:
+        subs = tsp.matrix_split(A, g, d)
+        tiles = [tsp.tile_create(s, A.cols, b, prec) for s, b in zip(subs, (64, 16, 8))]
+        plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
+        try:
+            plan.set_format(bm, 1)
+            for th in ((4096, 4096, 4096), (8, 8, 8)):
+                plan.set_th(*th)
+                full = th[0] == 4096
+                for w in ((64,) if bm == 64 else (64, 128, 256) if full else (128,)):
+                    for s, order, place in ((1, 1, 0), (2, 2, 1), (1, 2, 1)) if full else ((1, 2, 1),):
+                        plan.set_variant(bm, w, s, 1, order)
+                        plan.set_placement(bm, place)
+                        plan.set_panels(bm, 0, 1)
+                        plan.run(zero_c=True)
+                        C0 = plan.download_c()
+                        tag = f"prec={prec} bm={bm} th={th[0]} w={w} s={s} order={order} place={place}"
+                        assert_close(C0[rows, :colB], Cref, Cabs, prec, tag + " unsynchronised")
+                        for pr, lag in ((256, 1), (4096, 2), (512, 4)) if full else ((512, 2),):
+                            say(f"panels {tag} panel_rows={pr} lag={lag}")
+                            plan.set_panels(bm, pr, lag)
+                            assert plan.get_panels(bm) == (pr, lag)
+                            for rep in range(2):
+                                plan.run(zero_c=True)
+                                Cg = plan.download_c()
+                                assert_close(Cg[rows, :colB], Cref, Cabs, prec, f"{tag} panels={pr} rep={rep}")
+                                if full:
+                                    assert np.array_equal(Cg, C0), f"{tag} panels={pr} rep={rep} differs"
+            plan.set_panels(bm, 0, 1)
+        finally:
+            plan.close()
+
+
+@pytest.mark.parametrize("prec", [0, 1])
 @pytest.mark.parametrize("colB", [32, 128])
 def test_cli_integer_stream_dc2_exact(gpu, orc, dc2_path, prec, colB):
     """The reference CLI's inputs on its shipped matrix: exact integers."""

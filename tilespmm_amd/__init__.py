@@ -165,6 +165,9 @@ HIP_SYMBOLS = {
                                          C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "tsp_spmm_launch_ex": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P,
                                      C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "tsp_spmm_launch_panels": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P,
+                                         C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                                         C.c_int, C.c_int, C.c_int, _P, C.c_longlong]),
     "tsp_switch_v64": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v16": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v8": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
@@ -233,6 +236,8 @@ HOST_SYMBOLS = {
     "tsp_plan_set_lane_indices": (C.c_int, [_P, C.c_int, C.c_int]),
     "tsp_plan_get_lane_indices": (C.c_int, [_P, C.c_int]),
     "tsp_plan_get_placement": (C.c_int, [_P, C.c_int]),
+    "tsp_plan_set_panels": (C.c_int, [_P, C.c_int, C.c_int, C.c_int]),
+    "tsp_plan_get_panels": (C.c_int, [_P, C.c_int, _IP, _IP]),
     "tsp_plan_set_hot_rows": (C.c_int, [_P, C.c_longlong]),
     "tsp_plan_set_tune_mode": (C.c_int, [_P, C.c_int]),
     "tsp_plan_get_tune_mode": (C.c_int, [_P]),
@@ -673,6 +678,17 @@ class Plan:
 
     def get_placement(self, bm: int) -> int:
         return load()[1].tsp_plan_get_placement(self.p, bm)
+
+    def set_panels(self, bm: int, panel_rows: int, lag: int = 2):
+        """Panel-synchronised sweep with panel_rows B rows per panel and a
+        lead of at most `lag` panels (dense format; panel_rows 0 = off)."""
+        _check("tsp_plan_set_panels", load()[1].tsp_plan_set_panels(self.p, bm, int(panel_rows), int(lag)))
+
+    def get_panels(self, bm: int):
+        """(panel rows, lag) of the class's panel sweep (0 rows = off)."""
+        r, g = C.c_int(), C.c_int()
+        _check("tsp_plan_get_panels", load()[1].tsp_plan_get_panels(self.p, bm, C.byref(r), C.byref(g)))
+        return r.value, g.value
 
     def set_tune_mode(self, cold: bool):
         """Tune for single steps from a cold cache (True) or back-to-back steps."""

@@ -289,6 +289,32 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
                        placement, (flags & TSP_LAUNCH_LANE_INDICES) != 0);
 }
 
+int tsp_spmm_launch_panels(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
+                           const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,
+                           const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,
+                           int c_rows, void *stream, int w, int stages, int tasks_per_wave, int order,
+                           int placement, int flags, int b_rows, int panel_rows, int panel_lag, int *d_sync,
+                           long long sync_ints)
+{
+    if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES)) return TSP_EINVAL;
+    if ((flags & TSP_LAUNCH_LANE_INDICES) && !d_bitmap) return TSP_EINVAL;
+    if (bm != 64 && bm != 16 && bm != 8) return TSP_EINVAL;
+    if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
+    if (colB_p != 32 && (colB_p <= 0 || colB_p % 64 != 0)) return TSP_EINVAL;
+    if (rowblkblock < 0 || c_rows < 0 || b_rows <= 0 || sync_ints <= 0) return TSP_EINVAL;
+    if (d_bitmap && (bm == 64 || !d_vptr)) return TSP_EINVAL;
+    if (placement != TSP_PLACE_CONTIGUOUS && placement != TSP_PLACE_INTERLEAVED) return TSP_EINVAL;
+    if (panel_rows < 64 || (panel_rows & (panel_rows - 1)) || panel_lag < 1) return TSP_EINVAL;
+    if (w > 0 && (colB_p % w != 0 || !tsp::valid_variant(bm, w, stages > 0 ? stages : 1))) return TSP_EINVAL;
+    if (rowblkblock == 0) return TSP_OK;
+    if (!d_val || !d_rows || !d_colstart || !d_B || !d_C || !d_colidx || !d_sync) return TSP_EINVAL;
+    const int kprec = prec == TSP_PREC_TF32 && (flags & TSP_LAUNCH_OPERANDS_TF32) ? tsp::kPrecTf32Exact : prec;
+    return tsp::launch(bm, kprec, rowblkblock, colB_p, d_val, d_bitmap, d_vptr, d_rows, d_colstart, d_B,
+                       d_C, d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave, order,
+                       placement, (flags & TSP_LAUNCH_LANE_INDICES) != 0, b_rows, panel_rows, panel_lag, d_sync,
+                       sync_ints);
+}
+
 int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
                             const unsigned *d_rows, const int *d_colstart, const void *d_B,
                             float *d_C, const int *d_colidx, int c_rows, void *stream, int w,

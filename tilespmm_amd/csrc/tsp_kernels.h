@@ -50,18 +50,51 @@ constexpr int kPlaceContiguous = 0;
 constexpr int kPlaceInterleaved = 1;
 constexpr int kPlaceChunkXcd = 2;
 
+// Panel-synchronised sweep (optional).  The B rows are cut into panels of
+// 2^pshift rows; the waves that one XCD runs in one generation of the grid
+// step through the panels together, so the B rows they gather stay in that
+// XCD's L2.  Per (generation g, XCD x) the counters hold the waves
+// registered for g (a wave registers when its work item of g starts) and
+// one count per panel, each striped over kSyncStripes cache lines.  A wave announces a panel when it issues the loads of
+// its first tile at or past it, and before it loads from panel q it waits
+// until as many waves have announced panel q - lag as have registered, for at
+// most `spin` wall-clock ticks: the wait only shapes the timing, never the
+// result.  The grid holds at most the waves that fit on the device at once;
+// each wave runs one work item per generation (ngen generations).  The
+// launch zeroes the counters first.  cnt == nullptr: no synchronisation, one
+// generation over a grid of every work item.
+constexpr int kSyncStripes = 16;   // words per count, one per 128-byte line
+constexpr int kSyncLine = 32;      // ints per 128-byte line
+struct SyncArgs {
+    int *cnt;        // [ngen][kXcds][npanels + 1][kSyncStripes][kSyncLine]
+    int pshift;
+    int npanels;
+    int ngen;
+    int lag;         // a wave loads from panel q once all have reached q - lag
+    long long spin;  // longest wait per panel, wall-clock ticks
+};
+
 // Kernel variant = (chunk width W, pipeline stages S, tasks per wave).
 int default_chunk_width(int bm, int colB_p);
 int default_stages(int bm, int prec, int w);
 bool valid_variant(int bm, int w, int s);
-const void *select_kernel(int bm, int prec, int w, int s, bool packed, bool lane_idx = false);
+const void *select_kernel(int bm, int prec, int w, int s, bool packed, bool lane_idx = false, bool sync = false);
+// The instantiations of one row-block class (tsp_spmm_bm{64,16,8}.hip);
+// nullptr for a variant that is not built.  prec: TSP_PREC_FP16,
+// TSP_PREC_TF32 or kPrecTf32Exact.
+const void *select_kernel_bm64(int prec, int w, int s, bool packed, bool lane_idx, bool sync);
+const void *select_kernel_bm16(int prec, int w, int s, bool packed, bool lane_idx, bool sync);
+const void *select_kernel_bm8(int prec, int w, int s, bool packed, bool lane_idx, bool sync);
 // w, s, tpw <= 0 select the defaults; order 0 = default, 1 = chunks of one
 // task range adjacent, 2 = chunk-major.  bmp != nullptr selects the
 // bitmap-packed A format (val = packed values, vptr = per-tile offsets).
+// b_rows, panel_rows, panel_lag, sync, sync_ints: the panel-synchronised
+// sweep (sync != nullptr; see SyncArgs) with a buffer of sync_ints counters.
 int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint64_t *bmp,
            const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
            const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order,
-           int placement = kPlaceContiguous, bool lane_idx = false);
+           int placement = kPlaceContiguous, bool lane_idx = false, int b_rows = 0, int panel_rows = 0,
+           int panel_lag = 1, int *sync = nullptr, long long sync_ints = 0);
 int launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
 constexpr int kGatherBlocks = 8192;      // gather probe grid: 8192 x 256 threads
 int launch_gather(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed, void *sink,

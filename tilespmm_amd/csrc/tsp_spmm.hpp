@@ -1,0 +1,620 @@
+// tsp_spmm.hpp -- MI355X (gfx950, CDNA4) tile SpMM kernel template.
+//
+// One kernel template serves the three row-block classes (BM = 64, 16, 8) of
+// both precisions.  It computes, for every task of the schedule,
+//     C[start .. start+BM)[cols] (= or atomically +=)
+//         sum over the task's tiles of  A_tile(BM x BN) * B[colidx[tile]][cols]
+// which is what the reference's stir_spmm_cuda_kernel_v{8,16,64}[_tf32][_32]
+// compute (src/tilespmm_cuda.h:12-1632).  The design is CDNA4-first, not a
+// translation:
+//   * a wave64 owns a contiguous RANGE of tasks for one column chunk of W
+//     columns.  The tiles of consecutive tasks are contiguous in memory, so
+//     the wave streams them through one software pipeline that never drains
+//     at task boundaries; at a boundary it only flushes its accumulators to C
+//     and clears them.  Consecutive tasks of one split row-block keep
+//     accumulating.  A split task is flushed with fp32 atomics whose lanes
+//     cover whole rows (the slab is transposed through LDS first), unless
+//     the wave ran every task of its row-block; then, like an unsplit task,
+//     with plain vector stores.  A 256-thread block runs four independent
+//     waves: there is no block barrier;
+//   * S tiles are in flight per wave: the B row panel (BN rows x W columns,
+//     16-byte vector loads) and the A fragment of tile t+S are loaded while
+//     tile t is computed, and the column indices of tile t+2S (they feed the
+//     B addresses) S steps earlier still;
+//   * the B panel is staged in a wave-private LDS slice (one wave's LDS
+//     operations execute in issue order, so one buffer is safe).  MFMA
+//     column n of 16-column block c is chunk column n*CB + c (CB = W/16
+//     blocks), so a lane reads CB adjacent values of a B row with one LDS
+//     read and owns CB adjacent output columns (one vector store per row);
+//   * A tiles are canonical row-major BM x BN blocks read straight into MFMA
+//     operand registers (8 or 16 bytes per lane);
+//   * fp16: v_mfma_f32_16x16x16_f16 (BN = 16) and v_mfma_f32_16x16x32_f16
+//     (BN = 32), fp32 accumulate; 8-row tiles occupy rows 0-7 of the 16-row
+//     MFMA block;
+//   * tf32: operands are rounded to tf32 (nearest-even, 10 mantissa bits) in
+//     registers and multiplied with v_mfma_f32_16x16x4_f32 -- a tf32 product
+//     is exact in fp32, so this is tf32 arithmetic with fp32 accumulate
+//     (CDNA4 has no xf32 MFMA);
+//   * workgroups are placed on the 8 XCDs (each with its own L2) either as
+//     8 contiguous ranges of task ranges (neighbouring row-blocks share B
+//     rows) or as runs of 4 workgroups dealt to the XCDs in turn (skewed
+//     matrices stay balanced); the plan's runtime tuning picks per class.
+//
+// The MFMA K index of (lane group q = lane/16, operand element j) is a free
+// permutation as long as A and B use the same one; this file uses
+//   fp16: k = 4q + j (j < 4), k = 16 + 4q + (j - 4) (j >= 4)
+//   tf32: k = (BN/4) q + s for MFMA step s
+// so that A fragments are contiguous in the row-major tile and the four lane
+// groups read LDS rows that fall in disjoint bank ranges.
+//
+// The template is instantiated per row-block class in tsp_spmm_bm{64,16,8}.hip
+// (so the instantiations compile in parallel); tsp_kernels.hip selects and
+// launches them.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <type_traits>
+
+#include "../../include/tilespmm_hip.h"
+#include "tsp_kernels.h"
+
+namespace tsp {
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+
+// Wave-uniform read-only data (schedule, column indices) is read through the
+// constant address space so the loads become scalar (SMEM) loads into SGPRs:
+// they are counted by lgkmcnt and never make a wave wait on its in-flight
+// vector loads.
+template <typename T>
+using cptr = const __attribute__((address_space(4))) T *;
+
+template <typename T>
+__device__ __forceinline__ T uload(const T *p, size_t i)
+{
+    return ((cptr<T>)p)[i];
+}
+
+// Workgroup b of nb -> logical block.  Contiguous: each XCD receives one
+// contiguous range of logical blocks.  Interleaved: runs of kXcdRun logical
+// blocks go to the XCDs in turn (nb is then a multiple of kXcds * kXcdRun).
+__device__ __forceinline__ int place_block(int b, int nb, int placement)
+{
+    const int x = b % kXcds, k = b / kXcds;
+    if (placement == kPlaceInterleaved) return ((k / kXcdRun) * kXcds + x) * kXcdRun + k % kXcdRun;
+    const int q = nb / kXcds, r = nb % kXcds;
+    return x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
+}
+
+// PK selects the bitmap-packed A format (8- and 16-row classes): per tile a
+// row-major occupancy bitmap (BM*BN bits, bit r*BN+c) in `bmp`, and the values
+// of its set bits, in bit order, at `val_` + vptr[tile].  Each lane expands its
+// slice of the tile into MFMA operand registers.  Without PK, `val_` holds
+// dense canonical tiles and `bmp` / `vptr` are unused.
+// Waves per SIMD the register allocation must leave room for: the 64-row
+// kernel with 64-column chunks (unsynchronised) fits 3 waves in 168
+// registers, a couple short of what the compiler picks unprompted;
+// elsewhere the compiler's own choice.
+template <int BM, int W, int S, bool SY>
+constexpr int kMinWaves = BM == 64 && W == 64 && S == 1 && !SY ? 3 : 1;
+
+// SY: the panel-synchronised sweep (SyncArgs) is compiled in; without it the
+// kernel runs one generation and the sync arguments are ignored.
+template <int BM, int W, int PREC, int S, bool PK, bool LI, bool SY>
+__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(kMinWaves<BM, W, S, SY>))) void spmm_kernel(
+    int ntasks, int nchunks, int tasks_per_wave, int chunk_major, const void *__restrict__ val_,
+    const uint64_t *__restrict__ bmp, const int *__restrict__ vptr,
+    const unsigned *__restrict__ rows, const int *__restrict__ colstart,
+    const void *__restrict__ B_, float *__restrict__ C, const int *__restrict__ colidx, int ld,
+    int c_rows, int placement, SyncArgs sy)
+{
+    constexpr bool F16 = PREC == TSP_PREC_FP16;
+    // tf32 operands are rounded in registers, unless the launch guarantees
+    // they are tf32 values already (kPrecTf32Exact: the plan rounds its copies
+    // of A and B once when they enter it)
+    constexpr bool RND = PREC == TSP_PREC_TF32;
+    auto rnd = [](uint32_t x) { return RND ? round_tf32_bits(x) : x; };
+    constexpr int BN = tile_bn(BM, PREC);
+    constexpr int VV = F16 ? 8 : 4;          // values per 16-byte vector
+    constexpr int VPR = W / VV;              // vectors per panel row
+    constexpr int NV = BN * VPR / 64;        // vectors per lane per tile
+    static_assert(NV >= 1 && (BN * VPR) % 64 == 0, "panel does not tile the wave");
+    // LDS row stride: a multiple of the CB-value vectors the MFMA operand
+    // reads use (up to 32 bytes), padded so consecutive rows shift banks
+    constexpr int LDSW = W + 8;
+    constexpr int RG = BM >= 16 ? BM / 16 : 1;   // 16-row MFMA row groups
+    constexpr int CB = W / 16;                   // 16-column MFMA blocks
+    constexpr int KS = F16 ? 1 : BN / 4;         // tf32 MFMA steps per tile
+    constexpr int AW = F16 ? (BN == 32 ? 4 : 2) : KS;   // A words per row group
+    using VT = typename std::conditional<F16, _Float16, float>::type;
+    using RV = VT __attribute__((ext_vector_type(CB)));     // CB values of one B row
+    constexpr int PWD = PK ? BM * BN / 64 : 1;               // packed: bitmap words per tile
+    struct PMeta {
+        uint64_t bw[PWD];
+        int vbase;
+    };
+    using FV = float __attribute__((ext_vector_type(CB)));  // CB output columns
+
+    __shared__ __attribute__((aligned(32))) VT lds_all[kWavesPerBlock][BN * LDSW];
+
+    const int lane = threadIdx.x & 63;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform per wave
+    const long long nranges = ((long long)ntasks + tasks_per_wave - 1) / tasks_per_wave;
+    const bool sync = SY && sy.cnt != nullptr;
+    const int xcd = blockIdx.x % kXcds;
+    // Counters of generation g on this XCD: the waves registered for it, then
+    // one announcement count per panel.  Each count is striped over
+    // kSyncStripes words in separate 128-byte lines (wave w of the XCD adds
+    // to stripe w % kSyncStripes): one word taking an atomic from each of
+    // the XCD's hundreds of waves would serialise in the L2 atomic unit for
+    // longer than the waits it gates.  Only this XCD's waves touch them, so
+    // the adds are L2 atomics, and a poll reads the stripes from L2 with one
+    // device-scope vector load (it skips the CU's L1, whose copy would be
+    // stale) and sums them.
+    const int stripe = ((blockIdx.x / kXcds) * kWavesPerBlock + wid) % kSyncStripes;
+    auto cell = [&](int g, int i, int st) {
+        return sy.cnt + ((((size_t)g * kXcds + xcd) * (sy.npanels + 1) + i) * kSyncStripes + st) * kSyncLine;
+    };
+    auto bump = [&](int g, int i) {
+        __hip_atomic_fetch_add(cell(g, i, stripe), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    };
+    auto total = [&](int g, int i) {
+        int v = 0;
+        if (lane < kSyncStripes) v = __hip_atomic_load(cell(g, i, lane), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int o = kSyncStripes / 2; o >= 1; o >>= 1) v += __shfl_xor(v, o, kSyncStripes);
+        return __builtin_amdgcn_readfirstlane(v);
+    };
+    // Panel announcements from..to of generation g (lane 0 only).
+    auto announce = [&](int g, int from, int to) {
+        if (lane == 0)
+            for (int i = from; i <= to; ++i) bump(g, 1 + i);
+    };
+
+    // One work item: the task range `range` on column chunk `chunk`.
+    auto run = [&](int g, int range, int chunk) {
+        int lp = -1;                     // last panel this wave announced (sync)
+        const int k0 = range * tasks_per_wave;
+        const int k1 = min(ntasks, k0 + tasks_per_wave);
+        const int tb = uload(colstart, k0), te = uload(colstart, k1);
+        if (tb >= te) return;                        // every task of the range is empty
+        // a wave waits only for the waves that registered before it looks, so
+        // a wave that is not resident (yet) holds nobody back
+        if (sync && lane == 0) bump(g, 0);
+        int k = k0;
+        int kend = uload(colstart, k0 + 1);
+        while (kend <= tb) kend = uload(colstart, ++k + 1);  // skip leading empty tasks
+        int gfirst = k;                  // first task of the accumulation group
+        const int col0 = chunk * W;
+        // Before the B loads of a tile whose first column is fc: announce its
+        // panel q and wait (bounded) until every registered wave of this XCD
+        // has reached panel q - lag.  The tiles of one task run in ascending
+        // column order, so with one task per wave a wave's panels only grow
+        // (later tasks of a longer range are simply not held back).
+        auto gate = [&](int fc) {
+            if (!sync) return;
+            const int q = min(fc >> sy.pshift, sy.npanels - 1);
+            if (q <= lp) return;
+            announce(g, lp + 1, q);
+            lp = q;
+            if (q < sy.lag) return;
+            const long long t0 = wall_clock64();
+            while (total(g, 1 + q - sy.lag) < total(g, 0) && wall_clock64() - t0 < sy.spin)
+                __builtin_amdgcn_s_sleep(2);
+        };
+
+        VT *lds = lds_all[wid];
+        const VT *val = (const VT *)val_;
+        const char *Bb = (const char *)B_;
+        const int ln = lane & 15;        // MFMA row (A) / column (B, D) index
+        const int lq = lane >> 4;        // MFMA lane group
+
+        // Panel rows of the lane's NV B loads.  Scalar column indices (LI
+        // false): load i covers rows i*RPI .. i*RPI+RPI-1, row i*RPI + lane/VPR
+        // for this lane.  Lane-loaded indices (LI): the lane's rows are the NV
+        // consecutive rows (lane/VPR)*NV + i, whose column indices are
+        // consecutive in the tile's index list (one vector load).
+        int prow[NV], pcol[NV];
+    #pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int v = lane + 64 * i;
+            prow[i] = LI ? (lane / VPR) * NV + i : v / VPR;
+            pcol[i] = (v % VPR) * VV;
+        }
+
+        f4 acc[RG][CB];
+    #pragma unroll
+        for (int g = 0; g < RG; ++g)
+    #pragma unroll
+            for (int c = 0; c < CB; ++c) acc[g][c] = f4{0.f, 0.f, 0.f, 0.f};
+
+        // Packed-format metadata of one tile (bitmap words, value offset): wave-
+        // uniform scalar loads, prefetched S tiles ahead like the column indices
+        // because the value addresses depend on them.
+        auto load_meta = [&](int t, PMeta &m) {
+            if constexpr (PK) {
+    #pragma unroll
+                for (int w = 0; w < PWD; ++w) m.bw[w] = uload(bmp, (size_t)t * PWD + w);
+                m.vbase = uload(vptr, t);
+            }
+        };
+        // Packed A in two halves, so a wave never waits for a load it has just
+        // issued: issue_a_packed (S tiles ahead) computes the lane's position in
+        // the packed stream from the scalar bitmap words, loads its NVAL
+        // consecutive values raw and keeps its NVAL occupancy bits; finish_a_packed
+        // (just before the tile's MFMAs) expands them into operand registers.
+        constexpr int NVAL = F16 ? 4 : KS;           // packed: operand values per lane
+        auto issue_a_packed = [&](const PMeta &m, VT (&raw)[NVAL], uint32_t &nib) {
+            static_assert(!PK || BM <= 16, "packed tiles are 8- or 16-row");
+            constexpr int WD = PWD;                  // bitmap words per tile
+            const uint64_t *bw = m.bw;
+            const int vbase = m.vbase;
+            if (BM == 8 && ln >= 8) {
+    #pragma unroll
+                for (int j = 0; j < NVAL; ++j) raw[j] = (VT)0;
+                nib = 0u;
+                return;
+            }
+            // first bit of this lane's slots; NVAL-bit groups never straddle words
+            const int p = ln * BN + NVAL * lq;
+            int pre = 0;
+            uint64_t word = bw[0];
+    #pragma unroll
+            for (int w = 0; w < WD; ++w) {
+                const int lo = 64 * w;
+                const uint64_t m = p >= lo + 64 ? ~0ull : (p <= lo ? 0ull : ((1ull << (p - lo)) - 1ull));
+                pre += __popcll(bw[w] & m);
+                if (p >= lo && p < lo + 64) word = bw[w];
+            }
+            nib = (unsigned)(word >> (p & 63)) & ((1u << NVAL) - 1u);
+            // the lane's values are consecutive in the packed stream (the value
+            // array is padded, so reading NVAL of them is always in bounds)
+            const VT *pv = val + vbase + pre;
+    #pragma unroll
+            for (int j = 0; j < NVAL; ++j) raw[j] = pv[j];
+        };
+        auto finish_a_packed = [&](const VT (&v)[NVAL], uint32_t nib, uint32_t (&dst)[RG][AW]) {
+            VT o[NVAL];
+            int idx = 0;
+    #pragma unroll
+            for (int j = 0; j < NVAL; ++j) {
+                const bool b = (nib >> j) & 1u;
+                VT x = v[0];
+    #pragma unroll
+                for (int q = 1; q < NVAL; ++q) x = idx == q ? v[q] : x;
+                o[j] = b ? x : (VT)0;
+                idx += b ? 1 : 0;
+            }
+            if constexpr (F16) {
+                const h4 hv = h4{o[0], o[1], o[2], o[3]};
+                const u2 bits = __builtin_bit_cast(u2, hv);
+                dst[0][0] = bits.x;
+                dst[0][1] = bits.y;
+            } else {
+    #pragma unroll
+                for (int j = 0; j < NVAL; ++j) dst[0][j] = rnd(__float_as_uint(o[j]));
+            }
+        };
+        auto load_a = [&](int t, uint32_t (&dst)[RG][AW]) {
+            const VT *tile = val + (size_t)t * (BM * BN);
+    #pragma unroll
+            for (int g = 0; g < RG; ++g) {
+                const int r = 16 * g + ln;
+                if (BM == 8 && ln >= 8) {
+    #pragma unroll
+                    for (int w = 0; w < AW; ++w) dst[g][w] = 0u;
+                    continue;
+                }
+                if constexpr (F16) {
+                    const u2 lo = *(const u2 *)(tile + r * BN + 4 * lq);
+                    dst[g][0] = lo.x; dst[g][1] = lo.y;
+                    if constexpr (BN == 32) {
+                        const u2 hi = *(const u2 *)(tile + r * BN + 16 + 4 * lq);
+                        dst[g][2] = hi.x; dst[g][3] = hi.y;
+                    }
+                } else {
+                    const float *p = tile + r * BN + KS * lq;
+                    if constexpr (KS == 2) {
+                        const u2 x = *(const u2 *)p;
+                        dst[g][0] = rnd(x.x); dst[g][1] = rnd(x.y);
+                    } else {
+                        const u4 x = *(const u4 *)p;
+                        dst[g][0] = rnd(x.x); dst[g][1] = rnd(x.y);
+                        dst[g][2] = rnd(x.z); dst[g][3] = rnd(x.w);
+                    }
+                }
+            }
+        };
+        // Column indices.  Scalar (LI false): the tile's BN indices are
+        // wave-uniform; they are read with scalar loads (counted by lgkmcnt, so
+        // waiting for them never waits for the vector loads of the B/A ring),
+        // then each lane picks the index of each of its panel rows with a select
+        // chain (RPI - 1 selects per load).  Lane-loaded (LI): each lane reads
+        // its NV consecutive indices with one vector load and needs no selects,
+        // at the cost of a vector memory instruction per tile.  Either way the
+        // indices of tile t+S are read S tiles before the B gathers that use them.
+        constexpr int RPI = 64 / VPR;                // panel rows one vector instruction covers
+        const int lrow = lane / VPR;
+        using CSV = int __attribute__((ext_vector_type(LI ? NV : BN)));
+        auto load_cs = [&](int t, CSV &cs) {
+            if constexpr (LI) cs = *(const CSV *)(colidx + (size_t)t * BN + lrow * NV);
+            else cs = *(cptr<CSV>)(colidx + (size_t)t * BN);
+        };
+        auto select_cid = [&](const CSV &cs, int (&dst)[NV]) {
+    #pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                if constexpr (LI) {
+                    dst[i] = cs[i];
+                } else {
+                    int v = cs[i * RPI];
+    #pragma unroll
+                    for (int r = 1; r < RPI; ++r) v = lrow == r ? cs[i * RPI + r] : v;
+                    dst[i] = v;
+                }
+            }
+        };
+        auto load_b = [&](const int (&cid)[NV], u4 (&dst)[NV]) {
+    #pragma unroll
+            for (int i = 0; i < NV; ++i)
+                dst[i] = *(const u4 *)(Bb + ((size_t)cid[i] * ld + col0 + pcol[i]) * sizeof(VT));
+        };
+        // Flush the accumulators of tasks first..last, which this wave ran back
+        // to back and which share one row-block.  A split task (bit 31) is added
+        // atomically, as the reference does, whatever the order of the schedule.
+        // Only a group of several tasks of one split row-block may store: when
+        // the tasks just before and after the group belong to other row-blocks,
+        // this wave ran every task of it (a split row-block's tasks are
+        // consecutive, as tile_pretreatment emits them).
+        auto flush = [&](int first, int last) {
+            const unsigned rw = uload(rows, last);
+            const int row0 = (int)(rw & 0x7fffffffu);
+            bool split = (rw & 0x80000000u) != 0;
+            if (split && first < last) {
+                const bool from_start = first == 0 || (int)(uload(rows, first - 1) & 0x7fffffffu) != row0;
+                const bool to_end = last + 1 >= ntasks || (int)(uload(rows, last + 1) & 0x7fffffffu) != row0;
+                split = !(from_start && to_end);
+            }
+            if (!split) {
+                // MFMA column n of block c is output column n*CB + c: the lane
+                // owns CB adjacent columns of each of its rows (one vector store)
+    #pragma unroll
+                for (int g = 0; g < RG; ++g) {
+                    if (BM == 8 && lq >= 2) break;
+    #pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int r = row0 + 16 * g + 4 * lq + j;
+                        if (r >= c_rows) continue;
+                        FV v;
+    #pragma unroll
+                        for (int c = 0; c < CB; ++c) v[c] = acc[g][c][j];
+                        __builtin_nontemporal_store(v, (FV *)(C + (size_t)r * ld + col0 + ln * CB));
+                    }
+                }
+            } else {
+                // fp32 atomics are issued per lane: transpose each 8-row slab
+                // through the wave's (now idle) B panel in LDS so that every
+                // atomic instruction covers whole rows of consecutive columns
+                static_assert(BN * LDSW * sizeof(VT) >= 8 * W * sizeof(float), "panel too small for a slab");
+                float *tr = (float *)lds;
+    #pragma unroll
+                for (int h = 0; h < BM / 8; ++h) {
+                    if ((lq >> 1) == (h & 1)) {
+    #pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            FV v;
+    #pragma unroll
+                            for (int c = 0; c < CB; ++c) v[c] = acc[h >> 1][c][j];
+                            *(FV *)(tr + (4 * (lq & 1) + j) * W + ln * CB) = v;
+                        }
+                    }
+                    __builtin_amdgcn_wave_barrier();
+    #pragma unroll
+                    for (int i = 0; i < 8 * W / 64; ++i) {
+                        const int idx = lane + 64 * i;
+                        const int rr = idx / W, col = idx % W;
+                        const int r = row0 + 8 * h + rr;
+                        const float x = tr[rr * W + col];
+                        if (r < c_rows) unsafeAtomicAdd(C + (size_t)r * ld + col0 + col, x);
+                    }
+                    __builtin_amdgcn_wave_barrier();
+                }
+            }
+    #pragma unroll
+            for (int g = 0; g < RG; ++g)
+    #pragma unroll
+                for (int c = 0; c < CB; ++c) acc[g][c] = f4{0.f, 0.f, 0.f, 0.f};
+        };
+        // B operand of MFMA block c at lane (n = ln, group lq): column n*CB + c
+        // of the chunk, so one LDS read of CB adjacent values per B row serves
+        // all CB blocks.
+        auto compute = [&](const uint32_t (&a)[RG][AW]) {
+            const VT *lb = lds + ln * CB;
+            if constexpr (F16) {
+                constexpr int KR = BN == 16 ? 4 : 8;     // B rows of one lane
+                RV rv[KR];
+    #pragma unroll
+                for (int j = 0; j < 4; ++j) rv[j] = *(const RV *)(lb + (4 * lq + j) * LDSW);
+                if constexpr (BN == 32) {
+    #pragma unroll
+                    for (int j = 0; j < 4; ++j) rv[4 + j] = *(const RV *)(lb + (16 + 4 * lq + j) * LDSW);
+                }
+    #pragma unroll
+                for (int c = 0; c < CB; ++c) {
+                    if constexpr (BN == 16) {
+                        const h4 b = h4{rv[0][c], rv[1][c], rv[2][c], rv[3][c]};
+    #pragma unroll
+                        for (int g = 0; g < RG; ++g) {
+                            const h4 av = __builtin_bit_cast(h4, u2{a[g][0], a[g][1]});
+                            acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, b, acc[g][c], 0, 0, 0);
+                        }
+                    } else {
+                        const h8 b = h8{rv[0][c], rv[1][c], rv[2][c], rv[3][c], rv[4][c], rv[5][c], rv[6][c], rv[7][c]};
+    #pragma unroll
+                        for (int g = 0; g < RG; ++g) {
+                            const h8 av = __builtin_bit_cast(h8, u4{a[g][0], a[g][1], a[g][2], a[g][3]});
+                            acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[g][c], 0, 0, 0);
+                        }
+                    }
+                }
+            } else {
+    #pragma unroll
+                for (int s = 0; s < KS; ++s) {
+                    const RV rv = *(const RV *)(lb + (KS * lq + s) * LDSW);
+    #pragma unroll
+                    for (int c = 0; c < CB; ++c)
+    #pragma unroll
+                        for (int g = 0; g < RG; ++g)
+                            acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[g][s]), rv[c],
+                                                                              acc[g][c], 0, 0, 0);
+                }
+            }
+        };
+        auto stage_b = [&](const u4 (&src)[NV]) {
+    #pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                u4 x = src[i];
+                if constexpr (RND) {
+                    x.x = rnd(x.x); x.y = rnd(x.y);
+                    x.z = rnd(x.z); x.w = rnd(x.w);
+                }
+                VT *d = lds + prow[i] * LDSW + pcol[i];
+                if constexpr (F16) {
+                    *(u2 *)d = u2{x.x, x.y};
+                    *(u2 *)(d + 4) = u2{x.z, x.w};
+                } else {
+                    *(u4 *)d = x;
+                }
+            }
+        };
+
+        // Prologue: B panels and A fragments of the first S tiles in flight, and
+        // a ring of S column-index sets in SGPRs: slot s holds the indices of
+        // tile t+S when tile t = s (mod S) is computed, so each scalar load has S
+        // tile periods to arrive before its B addresses are formed (the indices
+        // stream from HBM; one period is not enough to hide that latency).
+        u4 bv[S][NV];
+        uint32_t ar[S][RG][AW];          // dense A: operand words
+        VT araw[S][NVAL];                 // packed A: raw values and occupancy bits
+        uint32_t anib[S];
+        CSV cs[S];
+        PMeta pm[S];
+        int cid[NV];
+        auto issue_a = [&](int t, int s) {
+            if constexpr (PK) issue_a_packed(pm[s], araw[s], anib[s]);
+            else load_a(t, ar[s]);
+        };
+    #pragma unroll
+        for (int s = 0; s < S; ++s)
+            if (tb + s < te) {
+                load_cs(tb + s, cs[s]);
+                load_meta(tb + s, pm[s]);
+            }
+    #pragma unroll
+        for (int s = 0; s < S; ++s)
+            if (tb + s < te) {
+                gate(__builtin_amdgcn_readfirstlane(cs[s][0]));
+                select_cid(cs[s], cid);
+                load_b(cid, bv[s]);
+                issue_a(tb + s, s);
+            }
+    #pragma unroll
+        for (int s = 0; s < S; ++s)
+            if (tb + S + s < te) {
+                load_cs(tb + S + s, cs[s]);
+                load_meta(tb + S + s, pm[s]);
+            }
+
+        for (int t0 = tb; t0 < te; t0 += S) {
+    #pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const int t = t0 + s;
+                if (t < te) {
+                    if (t >= kend) {                 // task k is complete
+                        int kn = k;
+                        do kend = uload(colstart, ++kn + 1);
+                        while (kend <= t);           // skip empty tasks
+                        // the next task continues the same row-block: keep
+                        // accumulating instead of flushing partial sums
+                        const bool same = (uload(rows, kn) & 0x7fffffffu) == (uload(rows, k) & 0x7fffffffu);
+                        if (!same) {
+                            flush(gfirst, k);
+                            gfirst = kn;
+                        }
+                        k = kn;
+                    }
+                    stage_b(bv[s]);
+                    uint32_t acur[RG][AW];
+                    if constexpr (PK) {
+                        finish_a_packed(araw[s], anib[s], acur);
+                    } else {
+    #pragma unroll
+                        for (int g = 0; g < RG; ++g)
+    #pragma unroll
+                            for (int w = 0; w < AW; ++w) acur[g][w] = ar[s][g][w];
+                    }
+                    if (t + S < te) {
+                        gate(__builtin_amdgcn_readfirstlane(cs[s][0]));
+                        select_cid(cs[s], cid);
+                        load_b(cid, bv[s]);
+                        issue_a(t + S, s);
+                        if (t + 2 * S < te) {
+                            load_cs(t + 2 * S, cs[s]);
+                            load_meta(t + 2 * S, pm[s]);
+                        }
+                    }
+                    compute(acur);
+                }
+            }
+        }
+        flush(gfirst, k);
+        if (sync && lp < sy.npanels - 1) announce(g, lp + 1, sy.npanels - 1);
+    };
+
+    // Work item of this wave in each generation (one generation unless the
+    // sweep is synchronised).
+    for (int g = 0; g < (SY ? sy.ngen : 1); ++g) {
+        long long r = -1;
+        int chunk = 0;
+        if (placement == kPlaceChunkXcd) {
+            // XCD x (workgroup b runs on XCD b % 8) serves chunk x % nchunks;
+            // the group's 8 / nchunks XCDs take runs of kXcdRun workgroups in
+            // turn (never synchronised)
+            const int x = blockIdx.x % kXcds, kk = blockIdx.x / kXcds, nx = kXcds / nchunks;
+            const long long j = ((long long)(kk / kXcdRun) * nx + x / nchunks) * kXcdRun + kk % kXcdRun;
+            const long long rr = j * kWavesPerBlock + wid;
+            if (rr < nranges) {
+                r = rr;
+                chunk = x % nchunks;
+            }
+        } else {
+            const int lb = place_block(blockIdx.x, gridDim.x, placement);
+            const long long gw = ((long long)g * gridDim.x + lb) * kWavesPerBlock + wid;
+            if (gw < nranges * nchunks) {
+                // chunk_major: all task ranges of chunk 0, then chunk 1, ...
+                // (the live B working set of a phase is one chunk's columns);
+                // otherwise the chunks of one range are neighbours (the A
+                // tiles are reused from L2).
+                r = chunk_major ? gw % nranges : gw / nchunks;
+                chunk = chunk_major ? (int)(gw / nranges) : (int)(gw - r * nchunks);
+            }
+        }
+        if (r >= 0) run(g, (int)r, chunk);
+    }
+}
+
+// Host-side address of one instantiation for a launch precision
+// (TSP_PREC_FP16, TSP_PREC_TF32 or kPrecTf32Exact); taking it instantiates
+// the kernel.
+template <int BM, int W, int S, bool PK, bool LI, bool SY>
+const void *pick_kernel(int prec)
+{
+    if (prec == TSP_PREC_FP16) return (const void *)&spmm_kernel<BM, W, TSP_PREC_FP16, S, PK, LI, SY>;
+    if (prec == kPrecTf32Exact) return (const void *)&spmm_kernel<BM, W, kPrecTf32Exact, S, PK, LI, SY>;
+    return (const void *)&spmm_kernel<BM, W, TSP_PREC_TF32, S, PK, LI, SY>;
+}
+
+}  // namespace tsp

@@ -45,8 +45,16 @@ struct ClassDev {
     Tile_matrix own{};            // tile_ptr, orig_tile_row_idx, schedule; no value arrays
     std::map<int, std::pair<std::vector<unsigned>, std::vector<int>>> cache;
     int place = TSP_PLACE_CONTIGUOUS;   // workgroup placement on the XCDs
+    int panel = 0;                // panel-synchronised sweep: B rows per panel (0 = off)
+    int panel_lag = 1;            // ... and how many panels a wave may lead the slowest by
+    int *d_sync = nullptr;        // its wave counters (kSyncInts; each launch zeroes the part it uses)
     bool active() const { return m && m->tilenum > 0; }
 };
+
+// Counters of a class's panel-synchronised sweep: generations x 8 XCDs x
+// (panels + 1) x 16 striped 128-byte lines must fit (4 MB per class that
+// uses it).
+constexpr long long kSyncInts = 1LL << 20;
 
 double now_ms()
 {
@@ -203,11 +211,48 @@ static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
 {
     if (!c.active() || c.ntasks == 0) return TSP_OK;
     const bool pk = c.fmt == 2;
+    const int flags = (p->prec == TSP_PREC_TF32 ? TSP_LAUNCH_OPERANDS_TF32 : 0) |
+                      (pk && c.var_li ? TSP_LAUNCH_LANE_INDICES : 0);
+    if (c.panel > 0)
+        return tsp_spmm_launch_panels(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val,
+                                      pk ? c.d_bmp : nullptr, pk ? c.d_vptr : nullptr, c.d_rows, c.d_colstart,
+                                      p->d_B, p->d_C, c.d_colidx, p->rowA, stream ? stream : c.stream, c.var_w,
+                                      c.var_s, c.var_tpw, c.var_order, c.place, flags, p->colA + p->nhot,
+                                      c.panel, c.panel_lag, c.d_sync, kSyncInts);
     return tsp_spmm_launch_ex(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val, pk ? c.d_bmp : nullptr,
                               pk ? c.d_vptr : nullptr, c.d_rows, c.d_colstart, p->d_B, p->d_C, c.d_colidx, p->rowA,
-                              stream ? stream : c.stream, c.var_w, c.var_s, c.var_tpw, c.var_order, c.place,
-                              (p->prec == TSP_PREC_TF32 ? TSP_LAUNCH_OPERANDS_TF32 : 0) |
-                                  (pk && c.var_li ? TSP_LAUNCH_LANE_INDICES : 0));
+                              stream ? stream : c.stream, c.var_w, c.var_s, c.var_tpw, c.var_order, c.place, flags);
+}
+
+extern "C" int tsp_plan_set_panels(tsp_plan *p, int bm, int panel_rows, int lag)
+{
+    if (!p || panel_rows < 0 || (panel_rows > 0 && (panel_rows < 64 || (panel_rows & (panel_rows - 1)) || lag < 1)))
+        return TSP_EINVAL;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) {
+            if (panel_rows > 0 && !c.d_sync) {
+                void *d = nullptr;
+                TSP_TRY(tsp_malloc(&d, sizeof(int) * (size_t)kSyncInts));
+                TSP_TRY(tsp_memset(d, 0, sizeof(int) * (size_t)kSyncInts));
+                c.d_sync = (int *)d;
+            }
+            c.panel = panel_rows;
+            c.panel_lag = panel_rows > 0 ? lag : 1;
+            return TSP_OK;
+        }
+    return TSP_EINVAL;
+}
+
+extern "C" int tsp_plan_get_panels(tsp_plan *p, int bm, int *panel_rows, int *lag)
+{
+    if (!p || !panel_rows || !lag) return TSP_EINVAL;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) {
+            *panel_rows = c.panel;
+            *lag = c.panel_lag;
+            return TSP_OK;
+        }
+    return TSP_EINVAL;
 }
 
 extern "C" int tsp_plan_set_format(tsp_plan *p, int bm, int fmt)
@@ -317,6 +362,7 @@ extern "C" int tsp_plan_destroy(tsp_plan *p)
         tsp_free(c.d_colidx);
         tsp_free(c.d_rows);
         tsp_free(c.d_colstart);
+        tsp_free(c.d_sync);
         tsp_stream_destroy(c.stream);
         if (c.dev_built) tsp_tile_destroy(&c.own);
     }
@@ -816,13 +862,16 @@ static int tune_time_class(tsp_plan *p, int bm, double *ms)
 //      round-robin balance matrices whose heavy row-blocks sit together; with
 //      2, 4 or 8 column chunks, one chunk per XCD group shrinks each L2's B
 //      working set);
-//   3. every chunk width (32, 64, 128 columns; 32 or 64 for 64-row tiles),
+//   3. every chunk width (32, 64, 128, 256 columns; 32 or 64 for 64-row tiles),
 //      each with both chunk orders, under each placement: wider chunks mean
 //      fewer waves and longer B row segments, narrower ones a smaller B
 //      working set per wave and more waves (tf32 RMAT gains 11% at 32 when
 //      interleaved).  Step 2's choice stays unless another is 1% faster;
-//   4. the pipeline depth (1-3 tiles in flight per wave).
+//   4. the pipeline depth (1-3 tiles in flight per wave; 1-2 for 256-column
+//      chunks);
+//   5. the panel-synchronised sweep (tune_panels).
 // A class whose variant was pinned with tsp_plan_set_variant is left alone.
+static int tune_panels(tsp_plan *p, ClassDev &c, double kept_ms);
 static int tune_class(tsp_plan *p, ClassDev &c)
 {
     if (!c.active() || c.ntasks == 0 || c.var_w || c.var_order || c.var_tpw) return TSP_OK;
@@ -906,8 +955,8 @@ static int tune_class(tsp_plan *p, ClassDev &c)
         const std::vector<int> dp = places(p->colB_p / k.cols_per_task);
         if (std::find(dp.begin(), dp.end(), place) != dp.end())
             wo.push_back({0, place == TSP_PLACE_CHUNK_XCD ? 1 : c.var_order, place});
-        for (int w : {32, 64, 128}) {
-            if (w == k.cols_per_task || p->colB_p % w != 0 || (c.bm == 64 && w == 128)) continue;
+        for (int w : {32, 64, 128, 256}) {
+            if (w == k.cols_per_task || p->colB_p % w != 0 || (c.bm == 64 && w >= 128)) continue;
             const std::vector<int> wp = places(p->colB_p / w);
             if (std::find(wp.begin(), wp.end(), place) == wp.end()) continue;
             if (place == TSP_PLACE_CHUNK_XCD) {
@@ -963,7 +1012,7 @@ static int tune_class(tsp_plan *p, ClassDev &c)
         for (double &x : r) x = 1e30;
     for (int round = 0; round < 2; ++round)
         for (int li = 0; li < nli; ++li)
-            for (int st = 1; st <= 3; ++st) {
+            for (int st = 1; st <= (w_kept == 256 ? 2 : 3); ++st) {
                 c.var_w = w_kept;
                 c.var_s = st;
                 c.var_li = li;
@@ -985,7 +1034,83 @@ static int tune_class(tsp_plan *p, ClassDev &c)
             for (int st = 1; st <= 3; ++st)
                 fprintf(stderr, "tune bm=%d stages %d %s indices: %.5f ms%s\n", c.bm, st, li ? "lane" : "scalar",
                         sms[li][st], st == sb && li == lb ? "  <- kept" : "");
-    return TSP_OK;
+    return tune_panels(p, c, sms[lb][sb]);
+}
+
+// 5. The panel-synchronised sweep (tsp_spmm_launch_panels) on the dense
+//    format, one task per wave: chunk widths x both chunk orders x panels of
+//    1 and 2 MB of B row segments x a lead of 2 or 4 panels, then pipeline
+//    depth 2 for the best of them.  Tried only when the class's work items
+//    fill the device a few times at most (each generation re-reads the B
+//    panels).  It stays when it is 2% faster than `kept_ms`, the time of
+//    the variant steps 1-4 kept.
+static int tune_panels(tsp_plan *p, ClassDev &c, double kept_ms)
+{
+    if (c.fmt != 1 || (long long)c.ntasks * p->colB_p / 128 > 16384) return TSP_OK;
+    const bool log = getenv("TSP_TUNE_LOG") != nullptr;
+    const int w0 = c.var_w, s0 = c.var_s, tpw0 = c.var_tpw, o0 = c.var_order, pl0 = c.place;
+    const int vs = p->prec == TSP_PREC_FP16 ? 2 : 4;
+    struct P {
+        int w, order, rows, lag, s;
+        double ms;
+    };
+    std::vector<P> opts;
+    for (int w : {64, 128, 256}) {
+        if (p->colB_p % w != 0 || (c.bm == 64 && w != 64)) continue;
+        for (int order = 1; order <= (p->colB_p / w >= 2 ? 2 : 1); ++order)
+            for (long long bytes : {1LL << 20, 2LL << 20}) {
+                int rows = 64;
+                while ((long long)rows * 2 * w * vs <= bytes) rows *= 2;
+                for (int lag : {2, 4}) opts.push_back({w, order, rows, lag, 1, 1e30});
+            }
+    }
+    if (opts.empty()) return TSP_OK;
+    const int place = pl0 == TSP_PLACE_CHUNK_XCD ? TSP_PLACE_INTERLEAVED : pl0;
+    auto time_opt = [&](P &o) -> int {
+        c.var_w = o.w;
+        c.var_s = o.s;
+        c.var_tpw = 0;
+        c.var_order = o.order;
+        c.place = place;
+        TSP_TRY(tsp_plan_set_panels(p, c.bm, o.rows, o.lag));
+        double t = 0;
+        const int st = tune_time_class(p, c.bm, &t);
+        if (st == TSP_EINVAL) return TSP_OK;          // too many generations x panels for the counters
+        TSP_TRY(st);
+        o.ms = std::min(o.ms, t);
+        return TSP_OK;
+    };
+    for (int round = 0; round < 2; ++round)
+        for (P &o : opts) TSP_TRY(time_opt(o));
+    size_t best = 0;
+    for (size_t j = 1; j < opts.size(); ++j)
+        if (opts[j].ms < opts[best].ms) best = j;
+    P deep = opts[best];
+    deep.s = 2;
+    deep.ms = 1e30;
+    for (int round = 0; round < 2; ++round) TSP_TRY(time_opt(deep));
+    opts.push_back(deep);
+    if (deep.ms < 0.99 * opts[best].ms) best = opts.size() - 1;
+    const bool keep = opts[best].ms < 0.98 * kept_ms;
+    if (log)
+        for (size_t j = 0; j < opts.size(); ++j)
+            fprintf(stderr, "tune bm=%d panels of %d rows lead %d, chunk width %d order=%d stages %d: %.5f ms%s\n",
+                    c.bm, opts[j].rows, opts[j].lag, opts[j].w, opts[j].order, opts[j].s, opts[j].ms,
+                    keep && j == best ? "  <- kept" : "");
+    if (keep) {
+        c.var_w = opts[best].w;
+        c.var_s = opts[best].s;
+        c.var_tpw = 0;
+        c.var_order = opts[best].order;
+        c.place = place;
+        return tsp_plan_set_panels(p, c.bm, opts[best].rows, opts[best].lag);
+    }
+    c.var_w = w0;
+    c.var_s = s0;
+    c.var_tpw = tpw0;
+    c.var_order = o0;
+    c.place = pl0;
+    return tsp_plan_set_panels(p, c.bm, 0, 1);
 }
 
 // One tuning measurement of whole steps: a warm-up step, then enough steps to
@@ -1106,6 +1231,7 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
             for (ClassDev &c : p->cls) {
                 c.var_w = c.var_s = c.var_tpw = c.var_order = c.var_li = 0;
                 c.place = TSP_PLACE_CONTIGUOUS;
+                TSP_TRY(tsp_plan_set_panels(p, c.bm, 0, 1));
                 TSP_TRY(tune_class(p, c));
             }
         }
