@@ -140,9 +140,30 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     using FV = float __attribute__((ext_vector_type(CB)));  // CB output columns
 
     __shared__ __attribute__((aligned(32))) VT lds_all[kWavesPerBlock][BN * LDSW];
+    // fp16 packed A: per wave, the v_perm_b32 byte selectors that expand a
+    // lane's 4 raw values into its 4 operand slots, for each of the 16
+    // occupancy patterns (slot j takes value rank_j = set bits below j, or 0)
+    __shared__ u2 lut_all[kWavesPerBlock][F16 && PK ? 16 : 1];
 
     const int lane = threadIdx.x & 63;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform per wave
+    if constexpr (F16 && PK) {
+        // selector byte pairs: value r's halves are bytes 2r, 2r+1 of the
+        // lane's 8 raw bytes (lo dword: values 0-1, hi dword: values 2-3);
+        // 0x0c selects a zero byte.  One wave's LDS operations execute in
+        // issue order, so its own later reads see the table.
+        if (lane < 16) {
+            unsigned sel[4];
+            unsigned r = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool b = (lane >> j) & 1;
+                sel[j] = b ? 0x0100u + 0x0202u * r : 0x0c0cu;
+                r += b ? 1u : 0u;
+            }
+            lut_all[wid][lane] = u2{sel[0] | sel[1] << 16, sel[2] | sel[3] << 16};
+        }
+    }
     const long long nranges = ((long long)ntasks + tasks_per_wave - 1) / tasks_per_wave;
     const bool sync = SY && sy.cnt != nullptr;
     const int xcd = blockIdx.x % kXcds;
@@ -219,7 +240,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         // consecutive rows (lane/VPR)*NV + i, whose column indices are
         // consecutive in the tile's index list (one vector load).
         int prow[NV], pcol[NV];
-    #pragma unroll
+#pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int v = lane + 64 * i;
             prow[i] = LI ? (lane / VPR) * NV + i : v / VPR;
@@ -227,9 +248,9 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         }
 
         f4 acc[RG][CB];
-    #pragma unroll
+#pragma unroll
         for (int g = 0; g < RG; ++g)
-    #pragma unroll
+#pragma unroll
             for (int c = 0; c < CB; ++c) acc[g][c] = f4{0.f, 0.f, 0.f, 0.f};
 
         // Packed-format metadata of one tile (bitmap words, value offset): wave-
@@ -237,7 +258,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         // because the value addresses depend on them.
         auto load_meta = [&](int t, PMeta &m) {
             if constexpr (PK) {
-    #pragma unroll
+#pragma unroll
                 for (int w = 0; w < PWD; ++w) m.bw[w] = uload(bmp, (size_t)t * PWD + w);
                 m.vbase = uload(vptr, t);
             }
@@ -245,67 +266,79 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         // Packed A in two halves, so a wave never waits for a load it has just
         // issued: issue_a_packed (S tiles ahead) computes the lane's position in
         // the packed stream from the scalar bitmap words, loads its NVAL
-        // consecutive values raw and keeps its NVAL occupancy bits; finish_a_packed
-        // (just before the tile's MFMAs) expands them into operand registers.
+        // consecutive values raw and looks up how to expand them (fp16: the
+        // byte selectors of its occupancy pattern; tf32: the occupancy bits);
+        // finish_a_packed (just before the tile's MFMAs) expands them into
+        // operand registers.
         constexpr int NVAL = F16 ? 4 : KS;           // packed: operand values per lane
-        auto issue_a_packed = [&](const PMeta &m, VT (&raw)[NVAL], uint32_t &nib) {
+        using DecT = typename std::conditional<F16, u2, uint32_t>::type;
+        // the lane's first slot bit, the bitmap word holding its NVAL bits
+        // (NVAL-bit groups never straddle words) and the bits below it there
+        const int pbit = ln * BN + NVAL * lq;
+        const int pword = pbit >> 6, poff = pbit & 63;
+        const uint64_t below = (1ull << poff) - 1ull;
+        const u2 *lut = lut_all[wid];
+        auto issue_a_packed = [&](const PMeta &m, VT (&raw)[NVAL], DecT &dec) {
             static_assert(!PK || BM <= 16, "packed tiles are 8- or 16-row");
             constexpr int WD = PWD;                  // bitmap words per tile
             const uint64_t *bw = m.bw;
-            const int vbase = m.vbase;
             if (BM == 8 && ln >= 8) {
-    #pragma unroll
+#pragma unroll
                 for (int j = 0; j < NVAL; ++j) raw[j] = (VT)0;
-                nib = 0u;
+                if constexpr (F16) dec = u2{0x0c0c0c0cu, 0x0c0c0c0cu};
+                else dec = 0u;
                 return;
             }
-            // first bit of this lane's slots; NVAL-bit groups never straddle words
-            const int p = ln * BN + NVAL * lq;
-            int pre = 0;
+            // whole-word prefix counts are wave-uniform (scalar unit); the lane
+            // picks its word and counts the bits below its slots in it
             uint64_t word = bw[0];
-    #pragma unroll
-            for (int w = 0; w < WD; ++w) {
-                const int lo = 64 * w;
-                const uint64_t m = p >= lo + 64 ? ~0ull : (p <= lo ? 0ull : ((1ull << (p - lo)) - 1ull));
-                pre += __popcll(bw[w] & m);
-                if (p >= lo && p < lo + 64) word = bw[w];
+            int pre = 0, whole = 0;
+#pragma unroll
+            for (int w = 1; w < WD; ++w) {
+                whole += __popcll(bw[w - 1]);
+                if (pword == w) {
+                    word = bw[w];
+                    pre = whole;
+                }
             }
-            nib = (unsigned)(word >> (p & 63)) & ((1u << NVAL) - 1u);
+            pre += __popcll(word & below);
+            const unsigned nib = (unsigned)(word >> poff) & ((1u << NVAL) - 1u);
             // the lane's values are consecutive in the packed stream (the value
             // array is padded, so reading NVAL of them is always in bounds)
-            const VT *pv = val + vbase + pre;
-    #pragma unroll
+            const VT *pv = val + m.vbase + pre;
+#pragma unroll
             for (int j = 0; j < NVAL; ++j) raw[j] = pv[j];
+            if constexpr (F16) dec = lut[nib];
+            else dec = nib;
         };
-        auto finish_a_packed = [&](const VT (&v)[NVAL], uint32_t nib, uint32_t (&dst)[RG][AW]) {
-            VT o[NVAL];
-            int idx = 0;
-    #pragma unroll
-            for (int j = 0; j < NVAL; ++j) {
-                const bool b = (nib >> j) & 1u;
-                VT x = v[0];
-    #pragma unroll
-                for (int q = 1; q < NVAL; ++q) x = idx == q ? v[q] : x;
-                o[j] = b ? x : (VT)0;
-                idx += b ? 1 : 0;
-            }
+        auto finish_a_packed = [&](const VT (&v)[NVAL], const DecT &dec, uint32_t (&dst)[RG][AW]) {
             if constexpr (F16) {
-                const h4 hv = h4{o[0], o[1], o[2], o[3]};
-                const u2 bits = __builtin_bit_cast(u2, hv);
-                dst[0][0] = bits.x;
-                dst[0][1] = bits.y;
+                const u2 bits = __builtin_bit_cast(u2, h4{v[0], v[1], v[2], v[3]});
+                dst[0][0] = __builtin_amdgcn_perm(bits.y, bits.x, dec.x);
+                dst[0][1] = __builtin_amdgcn_perm(bits.y, bits.x, dec.y);
             } else {
-    #pragma unroll
+                VT o[NVAL];
+                int idx = 0;
+#pragma unroll
+                for (int j = 0; j < NVAL; ++j) {
+                    const bool b = (dec >> j) & 1u;
+                    VT x = v[0];
+#pragma unroll
+                    for (int q = 1; q < NVAL; ++q) x = idx == q ? v[q] : x;
+                    o[j] = b ? x : (VT)0;
+                    idx += b ? 1 : 0;
+                }
+#pragma unroll
                 for (int j = 0; j < NVAL; ++j) dst[0][j] = rnd(__float_as_uint(o[j]));
             }
         };
         auto load_a = [&](int t, uint32_t (&dst)[RG][AW]) {
             const VT *tile = val + (size_t)t * (BM * BN);
-    #pragma unroll
+#pragma unroll
             for (int g = 0; g < RG; ++g) {
                 const int r = 16 * g + ln;
                 if (BM == 8 && ln >= 8) {
-    #pragma unroll
+#pragma unroll
                     for (int w = 0; w < AW; ++w) dst[g][w] = 0u;
                     continue;
                 }
@@ -345,20 +378,20 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             else cs = *(cptr<CSV>)(colidx + (size_t)t * BN);
         };
         auto select_cid = [&](const CSV &cs, int (&dst)[NV]) {
-    #pragma unroll
+#pragma unroll
             for (int i = 0; i < NV; ++i) {
                 if constexpr (LI) {
                     dst[i] = cs[i];
                 } else {
                     int v = cs[i * RPI];
-    #pragma unroll
+#pragma unroll
                     for (int r = 1; r < RPI; ++r) v = lrow == r ? cs[i * RPI + r] : v;
                     dst[i] = v;
                 }
             }
         };
         auto load_b = [&](const int (&cid)[NV], u4 (&dst)[NV]) {
-    #pragma unroll
+#pragma unroll
             for (int i = 0; i < NV; ++i)
                 dst[i] = *(const u4 *)(Bb + ((size_t)cid[i] * ld + col0 + pcol[i]) * sizeof(VT));
         };
@@ -381,15 +414,15 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             if (!split) {
                 // MFMA column n of block c is output column n*CB + c: the lane
                 // owns CB adjacent columns of each of its rows (one vector store)
-    #pragma unroll
+#pragma unroll
                 for (int g = 0; g < RG; ++g) {
                     if (BM == 8 && lq >= 2) break;
-    #pragma unroll
+#pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const int r = row0 + 16 * g + 4 * lq + j;
                         if (r >= c_rows) continue;
                         FV v;
-    #pragma unroll
+#pragma unroll
                         for (int c = 0; c < CB; ++c) v[c] = acc[g][c][j];
                         __builtin_nontemporal_store(v, (FV *)(C + (size_t)r * ld + col0 + ln * CB));
                     }
@@ -400,19 +433,19 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 // atomic instruction covers whole rows of consecutive columns
                 static_assert(BN * LDSW * sizeof(VT) >= 8 * W * sizeof(float), "panel too small for a slab");
                 float *tr = (float *)lds;
-    #pragma unroll
+#pragma unroll
                 for (int h = 0; h < BM / 8; ++h) {
                     if ((lq >> 1) == (h & 1)) {
-    #pragma unroll
+#pragma unroll
                         for (int j = 0; j < 4; ++j) {
                             FV v;
-    #pragma unroll
+#pragma unroll
                             for (int c = 0; c < CB; ++c) v[c] = acc[h >> 1][c][j];
                             *(FV *)(tr + (4 * (lq & 1) + j) * W + ln * CB) = v;
                         }
                     }
                     __builtin_amdgcn_wave_barrier();
-    #pragma unroll
+#pragma unroll
                     for (int i = 0; i < 8 * W / 64; ++i) {
                         const int idx = lane + 64 * i;
                         const int rr = idx / W, col = idx % W;
@@ -423,9 +456,9 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                     __builtin_amdgcn_wave_barrier();
                 }
             }
-    #pragma unroll
+#pragma unroll
             for (int g = 0; g < RG; ++g)
-    #pragma unroll
+#pragma unroll
                 for (int c = 0; c < CB; ++c) acc[g][c] = f4{0.f, 0.f, 0.f, 0.f};
         };
         // B operand of MFMA block c at lane (n = ln, group lq): column n*CB + c
@@ -436,24 +469,24 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             if constexpr (F16) {
                 constexpr int KR = BN == 16 ? 4 : 8;     // B rows of one lane
                 RV rv[KR];
-    #pragma unroll
+#pragma unroll
                 for (int j = 0; j < 4; ++j) rv[j] = *(const RV *)(lb + (4 * lq + j) * LDSW);
                 if constexpr (BN == 32) {
-    #pragma unroll
+#pragma unroll
                     for (int j = 0; j < 4; ++j) rv[4 + j] = *(const RV *)(lb + (16 + 4 * lq + j) * LDSW);
                 }
-    #pragma unroll
+#pragma unroll
                 for (int c = 0; c < CB; ++c) {
                     if constexpr (BN == 16) {
                         const h4 b = h4{rv[0][c], rv[1][c], rv[2][c], rv[3][c]};
-    #pragma unroll
+#pragma unroll
                         for (int g = 0; g < RG; ++g) {
                             const h4 av = __builtin_bit_cast(h4, u2{a[g][0], a[g][1]});
                             acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, b, acc[g][c], 0, 0, 0);
                         }
                     } else {
                         const h8 b = h8{rv[0][c], rv[1][c], rv[2][c], rv[3][c], rv[4][c], rv[5][c], rv[6][c], rv[7][c]};
-    #pragma unroll
+#pragma unroll
                         for (int g = 0; g < RG; ++g) {
                             const h8 av = __builtin_bit_cast(h8, u4{a[g][0], a[g][1], a[g][2], a[g][3]});
                             acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[g][c], 0, 0, 0);
@@ -461,12 +494,12 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                     }
                 }
             } else {
-    #pragma unroll
+#pragma unroll
                 for (int s = 0; s < KS; ++s) {
                     const RV rv = *(const RV *)(lb + (KS * lq + s) * LDSW);
-    #pragma unroll
+#pragma unroll
                     for (int c = 0; c < CB; ++c)
-    #pragma unroll
+#pragma unroll
                         for (int g = 0; g < RG; ++g)
                             acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[g][s]), rv[c],
                                                                               acc[g][c], 0, 0, 0);
@@ -474,7 +507,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             }
         };
         auto stage_b = [&](const u4 (&src)[NV]) {
-    #pragma unroll
+#pragma unroll
             for (int i = 0; i < NV; ++i) {
                 u4 x = src[i];
                 if constexpr (RND) {
@@ -499,7 +532,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         u4 bv[S][NV];
         uint32_t ar[S][RG][AW];          // dense A: operand words
         VT araw[S][NVAL];                 // packed A: raw values and occupancy bits
-        uint32_t anib[S];
+        DecT anib[S];
         CSV cs[S];
         PMeta pm[S];
         int cid[NV];
@@ -507,13 +540,13 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             if constexpr (PK) issue_a_packed(pm[s], araw[s], anib[s]);
             else load_a(t, ar[s]);
         };
-    #pragma unroll
+#pragma unroll
         for (int s = 0; s < S; ++s)
             if (tb + s < te) {
                 load_cs(tb + s, cs[s]);
                 load_meta(tb + s, pm[s]);
             }
-    #pragma unroll
+#pragma unroll
         for (int s = 0; s < S; ++s)
             if (tb + s < te) {
                 gate(__builtin_amdgcn_readfirstlane(cs[s][0]));
@@ -521,7 +554,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 load_b(cid, bv[s]);
                 issue_a(tb + s, s);
             }
-    #pragma unroll
+#pragma unroll
         for (int s = 0; s < S; ++s)
             if (tb + S + s < te) {
                 load_cs(tb + S + s, cs[s]);
@@ -529,7 +562,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             }
 
         for (int t0 = tb; t0 < te; t0 += S) {
-    #pragma unroll
+#pragma unroll
             for (int s = 0; s < S; ++s) {
                 const int t = t0 + s;
                 if (t < te) {
@@ -551,9 +584,9 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                     if constexpr (PK) {
                         finish_a_packed(araw[s], anib[s], acur);
                     } else {
-    #pragma unroll
+#pragma unroll
                         for (int g = 0; g < RG; ++g)
-    #pragma unroll
+#pragma unroll
                             for (int w = 0; w < AW; ++w) acur[g][w] = ar[s][g][w];
                     }
                     if (t + S < te) {
