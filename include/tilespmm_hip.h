@@ -209,12 +209,16 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
  * With one task per wave the tiles of a task come in ascending column
  * order.  The result is the same as tsp_spmm_launch_ex's with the same
  * arguments; only the timing changes.  d_sync: sync_ints ints of device
- * memory for the wave counters, which each launch zeroes on the stream
- * before it runs.  A launch needs generations x 8 x (panels + 1) x 512 of
- * them; TSP_EINVAL if sync_ints is smaller, for TSP_PLACE_CHUNK_XCD, for a
- * bad panel_rows or for panel_lag < 1.  Launches that share d_sync must not
- * overlap.  No counterpart in the reference (its grid is one block per
- * task). */
+ * memory for the wave counters; a launch needs generations x 8 x (panels +
+ * 1) x 512 of them (TSP_EINVAL if sync_ints is smaller, for
+ * TSP_PLACE_CHUNK_XCD, for a bad panel_rows or for panel_lag < 1).  A launch
+ * leaves the counters ready for the next launch with the same arguments; the
+ * first launch on a buffer, and the first after any argument changes, passes
+ * TSP_LAUNCH_SYNC_RESET in flags, which zeroes them on the stream first
+ * (with stale counters the waits only run into their time limit).  Launches
+ * that share d_sync must not overlap.  No counterpart in the reference (its
+ * grid is one block per task). */
+#define TSP_LAUNCH_SYNC_RESET 4
 int tsp_spmm_launch_panels(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
                            const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,
                            const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,

@@ -296,7 +296,7 @@ int tsp_spmm_launch_panels(int bm, int prec, int rowblkblock, int colB_p, const 
                            int placement, int flags, int b_rows, int panel_rows, int panel_lag, int *d_sync,
                            long long sync_ints)
 {
-    if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES)) return TSP_EINVAL;
+    if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES | TSP_LAUNCH_SYNC_RESET)) return TSP_EINVAL;
     if ((flags & TSP_LAUNCH_LANE_INDICES) && !d_bitmap) return TSP_EINVAL;
     if (bm != 64 && bm != 16 && bm != 8) return TSP_EINVAL;
     if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
@@ -312,7 +312,7 @@ int tsp_spmm_launch_panels(int bm, int prec, int rowblkblock, int colB_p, const 
     return tsp::launch(bm, kprec, rowblkblock, colB_p, d_val, d_bitmap, d_vptr, d_rows, d_colstart, d_B,
                        d_C, d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave, order,
                        placement, (flags & TSP_LAUNCH_LANE_INDICES) != 0, b_rows, panel_rows, panel_lag, d_sync,
-                       sync_ints);
+                       sync_ints, (flags & TSP_LAUNCH_SYNC_RESET) != 0);
 }
 
 int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,

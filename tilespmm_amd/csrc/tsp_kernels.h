@@ -60,8 +60,11 @@ constexpr int kPlaceChunkXcd = 2;
 // until as many waves have announced panel q - lag as have registered, for at
 // most `spin` wall-clock ticks: the wait only shapes the timing, never the
 // result.  The grid holds at most the waves that fit on the device at once;
-// each wave runs one work item per generation (ngen generations).  The
-// launch zeroes the counters first.  cnt == nullptr: no synchronisation, one
+// each wave runs one work item per generation (ngen generations).  Every
+// registered wave announces every panel by the end of its item, so a launch
+// leaves each panel count equal to its registration count: the counters
+// carry over to the next launch with the same layout and are zeroed only
+// when the layout changes.  cnt == nullptr: no synchronisation, one
 // generation over a grid of every work item.
 constexpr int kSyncStripes = 16;   // words per count, one per 128-byte line
 constexpr int kSyncLine = 32;      // ints per 128-byte line
@@ -88,13 +91,14 @@ const void *select_kernel_bm8(int prec, int w, int s, bool packed, bool lane_idx
 // w, s, tpw <= 0 select the defaults; order 0 = default, 1 = chunks of one
 // task range adjacent, 2 = chunk-major.  bmp != nullptr selects the
 // bitmap-packed A format (val = packed values, vptr = per-tile offsets).
-// b_rows, panel_rows, panel_lag, sync, sync_ints: the panel-synchronised
-// sweep (sync != nullptr; see SyncArgs) with a buffer of sync_ints counters.
+// b_rows, panel_rows, panel_lag, sync, sync_ints, sync_reset: the
+// panel-synchronised sweep (sync != nullptr; see SyncArgs) with a buffer of
+// sync_ints counters, zeroed first when sync_reset is set.
 int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint64_t *bmp,
            const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
            const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order,
            int placement = kPlaceContiguous, bool lane_idx = false, int b_rows = 0, int panel_rows = 0,
-           int panel_lag = 1, int *sync = nullptr, long long sync_ints = 0);
+           int panel_lag = 1, int *sync = nullptr, long long sync_ints = 0, bool sync_reset = false);
 int launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
 constexpr int kGatherBlocks = 8192;      // gather probe grid: 8192 x 256 threads
 int launch_gather(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed, void *sink,

@@ -24,8 +24,9 @@ __global__ __launch_bounds__(256) void copy_kernel(u4 *__restrict__ dst, const u
     for (; i < n; i += stride) dst[i] = src[i];
 }
 
-// Zeroes n ints (the panel sweep's counters, before each launch; a kernel
-// rather than a memset so that a captured stream holds no memset node).
+// Zeroes n ints (the panel sweep's counters when their layout changes; a
+// kernel rather than a memset so that a captured stream holds no memset
+// node).
 __global__ __launch_bounds__(256) void fill_kernel(int *__restrict__ p, long long n)
 {
     for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
@@ -121,7 +122,8 @@ constexpr int kSyncSpinUs = 20;
 int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint64_t *bmp,
            const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
            const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order,
-           int placement, bool lane_idx, int b_rows, int panel_rows, int panel_lag, int *sync, long long sync_ints)
+           int placement, bool lane_idx, int b_rows, int panel_rows, int panel_lag, int *sync, long long sync_ints,
+           bool sync_reset)
 {
     const bool packed = bmp != nullptr;
     if (packed && (bm == 64 || !vptr)) return TSP_EINVAL;
@@ -158,9 +160,11 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
         sy.ngen = (int)gen;
         sy.spin = wall_ticks(kSyncSpinUs);
         sy.lag = panel_lag;
-        fill_kernel<<<(unsigned)std::min<long long>((n + 255) / 256, 1024), 256, 0, st>>>(sync, n);
-        const hipError_t fe = hipGetLastError();
-        if (fe != hipSuccess) return (int)fe;
+        if (sync_reset) {
+            fill_kernel<<<(unsigned)std::min<long long>((n + 255) / 256, 1024), 256, 0, st>>>(sync, n);
+            const hipError_t fe = hipGetLastError();
+            if (fe != hipSuccess) return (int)fe;
+        }
     } else if (placement == kPlaceInterleaved) {
         // whole runs on every XCD (workgroups past the last logical block
         // find no task range and exit)

@@ -224,7 +224,9 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             lp = q;
             if (q < sy.lag) return;
             const long long t0 = wall_clock64();
-            while (total(g, 1 + q - sy.lag) < total(g, 0) && wall_clock64() - t0 < sy.spin)
+            // the counts carry over from earlier launches, which leave every
+            // panel's count equal to the registrations: compare differences
+            while ((int)(total(g, 1 + q - sy.lag) - total(g, 0)) < 0 && wall_clock64() - t0 < sy.spin)
                 __builtin_amdgcn_s_sleep(2);
         };
 

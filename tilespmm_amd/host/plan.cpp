@@ -47,7 +47,8 @@ struct ClassDev {
     int place = TSP_PLACE_CONTIGUOUS;   // workgroup placement on the XCDs
     int panel = 0;                // panel-synchronised sweep: B rows per panel (0 = off)
     int panel_lag = 1;            // ... and how many panels a wave may lead the slowest by
-    int *d_sync = nullptr;        // its wave counters (kSyncInts; each launch zeroes the part it uses)
+    int *d_sync = nullptr;        // its wave counters (kSyncInts)
+    std::vector<long long> sync_sig;   // launch arguments the counters are balanced for
     bool active() const { return m && m->tilenum > 0; }
 };
 
@@ -213,12 +214,20 @@ static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
     const bool pk = c.fmt == 2;
     const int flags = (p->prec == TSP_PREC_TF32 ? TSP_LAUNCH_OPERANDS_TF32 : 0) |
                       (pk && c.var_li ? TSP_LAUNCH_LANE_INDICES : 0);
-    if (c.panel > 0)
-        return tsp_spmm_launch_panels(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val,
-                                      pk ? c.d_bmp : nullptr, pk ? c.d_vptr : nullptr, c.d_rows, c.d_colstart,
-                                      p->d_B, p->d_C, c.d_colidx, p->rowA, stream ? stream : c.stream, c.var_w,
-                                      c.var_s, c.var_tpw, c.var_order, c.place, flags, p->colA + p->nhot,
-                                      c.panel, c.panel_lag, c.d_sync, kSyncInts);
+    if (c.panel > 0) {
+        // the counters are zeroed whenever the launch arguments change
+        const std::vector<long long> sig{c.ntasks, c.var_w, c.var_s, c.var_tpw, c.var_order, c.place,
+                                         c.panel, c.panel_lag, p->colA + p->nhot, c.fmt};
+        const int reset = sig != c.sync_sig ? TSP_LAUNCH_SYNC_RESET : 0;
+        const int st = tsp_spmm_launch_panels(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val,
+                                              pk ? c.d_bmp : nullptr, pk ? c.d_vptr : nullptr, c.d_rows,
+                                              c.d_colstart, p->d_B, p->d_C, c.d_colidx, p->rowA,
+                                              stream ? stream : c.stream, c.var_w, c.var_s, c.var_tpw, c.var_order,
+                                              c.place, flags | reset, p->colA + p->nhot, c.panel, c.panel_lag,
+                                              c.d_sync, kSyncInts);
+        c.sync_sig = st == TSP_OK ? sig : std::vector<long long>();
+        return st;
+    }
     return tsp_spmm_launch_ex(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val, pk ? c.d_bmp : nullptr,
                               pk ? c.d_vptr : nullptr, c.d_rows, c.d_colstart, p->d_B, p->d_C, c.d_colidx, p->rowA,
                               stream ? stream : c.stream, c.var_w, c.var_s, c.var_tpw, c.var_order, c.place, flags);
@@ -233,8 +242,8 @@ extern "C" int tsp_plan_set_panels(tsp_plan *p, int bm, int panel_rows, int lag)
             if (panel_rows > 0 && !c.d_sync) {
                 void *d = nullptr;
                 TSP_TRY(tsp_malloc(&d, sizeof(int) * (size_t)kSyncInts));
-                TSP_TRY(tsp_memset(d, 0, sizeof(int) * (size_t)kSyncInts));
                 c.d_sync = (int *)d;
+                c.sync_sig.clear();      // the first launch zeroes the counters
             }
             c.panel = panel_rows;
             c.panel_lag = panel_rows > 0 ? lag : 1;
