@@ -95,17 +95,20 @@ __device__ __forceinline__ int place_block(int b, int nb, int placement)
 // of its set bits, in bit order, at `val_` + vptr[tile].  Each lane expands its
 // slice of the tile into MFMA operand registers.  Without PK, `val_` holds
 // dense canonical tiles and `bmp` / `vptr` are unused.
-// Waves per SIMD the register allocation must leave room for: the 64-row
-// kernel with 64-column chunks (unsynchronised) fits 3 waves in 168
-// registers, a couple short of what the compiler picks unprompted;
-// elsewhere the compiler's own choice.
-template <int BM, int W, int S, bool SY>
-constexpr int kMinWaves = BM == 64 && W == 64 && S == 1 && !SY ? 3 : 1;
+// Waves per SIMD the register allocation must leave room for, where the
+// compiler's own choice lands a few registers past a step in occupancy: the
+// 64-row kernel with 64-column chunks fits 3 waves in 168 registers, the
+// synchronised fp16 16-row kernel with 128-column chunks (configuration 4's)
+// 5 waves in 96; elsewhere the compiler decides.
+template <int BM, int W, int PREC, int S, bool SY>
+constexpr int kMinWaves = BM == 64 && W == 64 && S == 1 && !SY                                      ? 3
+                          : SY && PREC == TSP_PREC_FP16 && BM == 16 && W == 128 && S == 1 ? 5
+                                                                                           : 1;
 
 // SY: the panel-synchronised sweep (SyncArgs) is compiled in; without it the
 // kernel runs one generation and the sync arguments are ignored.
 template <int BM, int W, int PREC, int S, bool PK, bool LI, bool SY>
-__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(kMinWaves<BM, W, S, SY>))) void spmm_kernel(
+__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(kMinWaves<BM, W, PREC, S, SY>))) void spmm_kernel(
     int ntasks, int nchunks, int tasks_per_wave, int chunk_major, const void *__restrict__ val_,
     const uint64_t *__restrict__ bmp, const int *__restrict__ vptr,
     const unsigned *__restrict__ rows, const int *__restrict__ colstart,
@@ -113,6 +116,12 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     int c_rows, int placement, SyncArgs sy)
 {
     constexpr bool F16 = PREC == TSP_PREC_FP16;
+    // fp16 dense tiles read their B operands with LDS transpose reads and
+    // keep MFMA block c on chunk columns 16c .. 16c + 15; fp16 packed and tf32
+    // tiles map MFMA column n of block c to chunk column n*CB + c (the
+    // packed kernels are gather-bound, and at the occupancy the transpose
+    // reads allow they ran 1-2% slower)
+    constexpr bool TR = F16 && !PK;
     // tf32 operands are rounded in registers, unless the launch guarantees
     // they are tf32 values already (kPrecTf32Exact: the plan rounds its copies
     // of A and B once when they enter it)
@@ -414,8 +423,6 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 split = !(from_start && to_end);
             }
             if (!split) {
-                // MFMA column n of block c is output column n*CB + c: the lane
-                // owns CB adjacent columns of each of its rows (one vector store)
 #pragma unroll
                 for (int g = 0; g < RG; ++g) {
                     if (BM == 8 && lq >= 2) break;
@@ -423,10 +430,20 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                     for (int j = 0; j < 4; ++j) {
                         const int r = row0 + 16 * g + 4 * lq + j;
                         if (r >= c_rows) continue;
-                        FV v;
+                        float *crow = C + (size_t)r * ld + col0;
+                        if constexpr (TR) {
+                            // MFMA column n of block c is output column 16c + n:
+                            // the 16 lanes of a group store 64 contiguous bytes
 #pragma unroll
-                        for (int c = 0; c < CB; ++c) v[c] = acc[g][c][j];
-                        __builtin_nontemporal_store(v, (FV *)(C + (size_t)r * ld + col0 + ln * CB));
+                            for (int c = 0; c < CB; ++c) __builtin_nontemporal_store(acc[g][c][j], crow + 16 * c + ln);
+                        } else {
+                            // MFMA column n of block c is output column n*CB + c:
+                            // the lane owns CB adjacent columns (one vector store)
+                            FV v;
+#pragma unroll
+                            for (int c = 0; c < CB; ++c) v[c] = acc[g][c][j];
+                            __builtin_nontemporal_store(v, (FV *)(crow + ln * CB));
+                        }
                     }
                 }
             } else {
@@ -440,10 +457,16 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                     if ((lq >> 1) == (h & 1)) {
 #pragma unroll
                         for (int j = 0; j < 4; ++j) {
-                            FV v;
+                            float *trow = tr + (4 * (lq & 1) + j) * W;
+                            if constexpr (TR) {
 #pragma unroll
-                            for (int c = 0; c < CB; ++c) v[c] = acc[h >> 1][c][j];
-                            *(FV *)(tr + (4 * (lq & 1) + j) * W + ln * CB) = v;
+                                for (int c = 0; c < CB; ++c) trow[16 * c + ln] = acc[h >> 1][c][j];
+                            } else {
+                                FV v;
+#pragma unroll
+                                for (int c = 0; c < CB; ++c) v[c] = acc[h >> 1][c][j];
+                                *(FV *)(trow + ln * CB) = v;
+                            }
                         }
                     }
                     __builtin_amdgcn_wave_barrier();
@@ -463,12 +486,43 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
 #pragma unroll
                 for (int c = 0; c < CB; ++c) acc[g][c] = f4{0.f, 0.f, 0.f, 0.f};
         };
-        // B operand of MFMA block c at lane (n = ln, group lq): column n*CB + c
-        // of the chunk, so one LDS read of CB adjacent values per B row serves
-        // all CB blocks.
+        // B operand of MFMA block c at lane (n = ln, group lq).  Dense fp16
+        // (TR): column 16c + n of the chunk, read with LDS transpose reads
+        // (ds_read_b64_tr_b16): within a 16-lane group, lane j receives
+        // element j % 4 of the 8 bytes that lanes 4k + j / 4 (k = 0..3) point
+        // at, so lane L pointing at columns 16c + 4(L % 4) .. +3 of panel row
+        // 4 lq + (L % 16) / 4 hands lane (n, lq) rows 4 lq .. 4 lq + 3 of
+        // column 16c + n -- the K-ordered operand, with no VALU shuffling.
+        // Otherwise column n*CB + c of the chunk, so one LDS read of CB
+        // adjacent values per B row serves all CB blocks (fp16 packed: four
+        // rows' reads are then shuffled into K order).
         auto compute = [&](const uint32_t (&a)[RG][AW]) {
-            const VT *lb = lds + ln * CB;
-            if constexpr (F16) {
+            if constexpr (TR) {
+                typedef short s4 __attribute__((ext_vector_type(4)));
+                using lds_s4 = __attribute__((address_space(3))) s4 *;
+                const VT *tb = lds + (4 * lq + (ln >> 2)) * LDSW + 4 * (ln & 3);
+#pragma unroll
+                for (int c = 0; c < CB; ++c) {
+                    const h4 b0 = __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(tb + 16 * c)));
+                    if constexpr (BN == 16) {
+#pragma unroll
+                        for (int g = 0; g < RG; ++g) {
+                            const h4 av = __builtin_bit_cast(h4, u2{a[g][0], a[g][1]});
+                            acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x16f16(av, b0, acc[g][c], 0, 0, 0);
+                        }
+                    } else {
+                        const h4 b1 =
+                            __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(tb + 16 * LDSW + 16 * c)));
+                        const h8 b = h8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+#pragma unroll
+                        for (int g = 0; g < RG; ++g) {
+                            const h8 av = __builtin_bit_cast(h8, u4{a[g][0], a[g][1], a[g][2], a[g][3]});
+                            acc[g][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[g][c], 0, 0, 0);
+                        }
+                    }
+                }
+            } else if constexpr (F16) {
+                const VT *lb = lds + ln * CB;
                 constexpr int KR = BN == 16 ? 4 : 8;     // B rows of one lane
                 RV rv[KR];
 #pragma unroll
@@ -496,6 +550,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                     }
                 }
             } else {
+                const VT *lb = lds + ln * CB;
 #pragma unroll
                 for (int s = 0; s < KS; ++s) {
                     const RV rv = *(const RV *)(lb + (KS * lq + s) * LDSW);
