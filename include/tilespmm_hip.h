@@ -200,7 +200,8 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
 
 /* Panel-synchronised sweep: tsp_spmm_launch_ex whose waves step through
  * the B rows in panels of panel_rows rows (a power of two, at least 64;
- * b_rows = rows of B the column indices can name).  The grid holds at most
+ * b_rows = rows of B that panels cover; a tile whose first column index is
+ * b_rows or more, such as a hot-row copy, is not held back).  The grid holds at most
  * the workgroups that fit on the device at once, each wave running one task
  * range per generation.  Within a generation, a wave about to load from
  * panel q first waits (at most 20 us) until every wave of its XCD that has

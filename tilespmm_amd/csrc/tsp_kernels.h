@@ -72,6 +72,7 @@ struct SyncArgs {
     int *cnt;        // [ngen][kXcds][npanels + 1][kSyncStripes][kSyncLine]
     int pshift;
     int npanels;
+    int brows;       // canonical B rows: tiles whose first column lies past them (hot-row copies) are not gated
     int ngen;
     int lag;         // a wave loads from panel q once all have reached q - lag
     long long spin;  // longest wait per panel, wall-clock ticks

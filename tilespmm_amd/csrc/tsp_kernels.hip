@@ -139,7 +139,7 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
     const long long waves = ranges * nchunks;
     long long blocks = (waves + kWavesPerBlock - 1) / kWavesPerBlock;
     if (blocks <= 0) return 0;
-    SyncArgs sy{nullptr, 0, 1, 1, 1, 0};
+    SyncArgs sy{nullptr, 0, 1, 0, 1, 1, 0};
     if (sync) {
         // panel-synchronised sweep: at most the resident workgroups, in whole
         // runs of kXcds * kXcdRun (every XCD holds the same number of waves)
@@ -157,6 +157,7 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
         sy.cnt = sync;
         sy.pshift = __builtin_ctz((unsigned)panel_rows);
         sy.npanels = (int)np;
+        sy.brows = b_rows;
         sy.ngen = (int)gen;
         sy.spin = wall_ticks(kSyncSpinUs);
         sy.lag = panel_lag;

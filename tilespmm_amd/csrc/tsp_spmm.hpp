@@ -224,10 +224,12 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         // panel q and wait (bounded) until every registered wave of this XCD
         // has reached panel q - lag.  The tiles of one task run in ascending
         // column order, so with one task per wave a wave's panels only grow
-        // (later tasks of a longer range are simply not held back).
+        // (later tasks of a longer range are simply not held back).  A tile
+        // whose first column is a hot-row copy (past the canonical rows) is
+        // not gated.
         auto gate = [&](int fc) {
-            if (!sync) return;
-            const int q = min(fc >> sy.pshift, sy.npanels - 1);
+            if (!sync || fc >= sy.brows) return;
+            const int q = fc >> sy.pshift;
             if (q <= lp) return;
             announce(g, lp + 1, q);
             lp = q;

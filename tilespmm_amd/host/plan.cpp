@@ -217,13 +217,13 @@ static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
     if (c.panel > 0) {
         // the counters are zeroed whenever the launch arguments change
         const std::vector<long long> sig{c.ntasks, c.var_w, c.var_s, c.var_tpw, c.var_order, c.place,
-                                         c.panel, c.panel_lag, p->colA + p->nhot, c.fmt};
+                                         c.panel, c.panel_lag, p->colA, c.fmt};
         const int reset = sig != c.sync_sig ? TSP_LAUNCH_SYNC_RESET : 0;
         const int st = tsp_spmm_launch_panels(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val,
                                               pk ? c.d_bmp : nullptr, pk ? c.d_vptr : nullptr, c.d_rows,
                                               c.d_colstart, p->d_B, p->d_C, c.d_colidx, p->rowA,
                                               stream ? stream : c.stream, c.var_w, c.var_s, c.var_tpw, c.var_order,
-                                              c.place, flags | reset, p->colA + p->nhot, c.panel, c.panel_lag,
+                                              c.place, flags | reset, p->colA, c.panel, c.panel_lag,
                                               c.d_sync, kSyncInts);
         c.sync_sig = st == TSP_OK ? sig : std::vector<long long>();
         return st;
@@ -1048,7 +1048,7 @@ static int tune_class(tsp_plan *p, ClassDev &c)
 
 // 5. The panel-synchronised sweep (tsp_spmm_launch_panels) on the dense
 //    format, one task per wave: chunk widths x both chunk orders x panels of
-//    1 and 2 MB of B row segments x a lead of 2 or 4 panels, then pipeline
+//    1 and 2 MB of B row segments x a lead of 2, 3 or 4 panels, then pipeline
 //    depth 2 for the best of them.  Tried only when the class's work items
 //    fill the device a few times at most (each generation re-reads the B
 //    panels).  It stays when it is 2% faster than `kept_ms`, the time of
@@ -1070,7 +1070,7 @@ static int tune_panels(tsp_plan *p, ClassDev &c, double kept_ms)
             for (long long bytes : {1LL << 20, 2LL << 20}) {
                 int rows = 64;
                 while ((long long)rows * 2 * w * vs <= bytes) rows *= 2;
-                for (int lag : {2, 4}) opts.push_back({w, order, rows, lag, 1, 1e30});
+                for (int lag : {2, 3, 4}) opts.push_back({w, order, rows, lag, 1, 1e30});
             }
     }
     if (opts.empty()) return TSP_OK;
