@@ -881,6 +881,7 @@ static int tune_time_class(tsp_plan *p, int bm, double *ms)
 //   5. the panel-synchronised sweep (tune_panels).
 // A class whose variant was pinned with tsp_plan_set_variant is left alone.
 static int tune_panels(tsp_plan *p, ClassDev &c, double kept_ms);
+static int tune_time_step(tsp_plan *p, double min_ms, double *ms);
 static int tune_class(tsp_plan *p, ClassDev &c)
 {
     if (!c.active() || c.ntasks == 0 || c.var_w || c.var_order || c.var_tpw) return TSP_OK;
@@ -1052,7 +1053,8 @@ static int tune_class(tsp_plan *p, ClassDev &c)
 //    depth 2 for the best of them.  Tried only when the class's work items
 //    fill the device a few times at most (each generation re-reads the B
 //    panels).  It stays when it is 2% faster than `kept_ms`, the time of
-//    the variant steps 1-4 kept.
+//    the variant steps 1-4 kept, and, when other classes run beside this one
+//    in a step, when whole steps are 2% faster with it.
 static int tune_panels(tsp_plan *p, ClassDev &c, double kept_ms)
 {
     if (c.fmt != 1 || (long long)c.ntasks * p->colB_p / 128 > 16384) return TSP_OK;
@@ -1100,26 +1102,49 @@ static int tune_panels(tsp_plan *p, ClassDev &c, double kept_ms)
     for (int round = 0; round < 2; ++round) TSP_TRY(time_opt(deep));
     opts.push_back(deep);
     if (deep.ms < 0.99 * opts[best].ms) best = opts.size() - 1;
-    const bool keep = opts[best].ms < 0.98 * kept_ms;
+    bool keep = opts[best].ms < 0.98 * kept_ms;
     if (log)
         for (size_t j = 0; j < opts.size(); ++j)
             fprintf(stderr, "tune bm=%d panels of %d rows lead %d, chunk width %d order=%d stages %d: %.5f ms%s\n",
                     c.bm, opts[j].rows, opts[j].lag, opts[j].w, opts[j].order, opts[j].s, opts[j].ms,
                     keep && j == best ? "  <- kept" : "");
-    if (keep) {
+    auto apply_best = [&]() -> int {
         c.var_w = opts[best].w;
         c.var_s = opts[best].s;
         c.var_tpw = 0;
         c.var_order = opts[best].order;
         c.place = place;
         return tsp_plan_set_panels(p, c.bm, opts[best].rows, opts[best].lag);
+    };
+    auto restore = [&]() -> int {
+        c.var_w = w0;
+        c.var_s = s0;
+        c.var_tpw = tpw0;
+        c.var_order = o0;
+        c.place = pl0;
+        return tsp_plan_set_panels(p, c.bm, 0, 1);
+    };
+    // The capped grid assumes the device to itself: when other classes run
+    // beside this one in a step, the sweep must also win whole steps.
+    bool others = false;
+    for (const ClassDev &o : p->cls) others |= &o != &c && o.active() && o.ntasks > 0;
+    if (keep && others) {
+        double with = 1e30, without = 1e30;
+        for (int round = 0; round < 2; ++round) {
+            double t = 0;
+            TSP_TRY(apply_best());
+            TSP_TRY(tune_time_step(p, 20.0, &t));
+            with = std::min(with, t);
+            TSP_TRY(restore());
+            TSP_TRY(tune_time_step(p, 20.0, &t));
+            without = std::min(without, t);
+        }
+        keep = with < 0.98 * without;
+        if (log)
+            fprintf(stderr, "tune bm=%d panel sweep in whole steps: %.5f ms against %.5f ms%s\n", c.bm, with, without,
+                    keep ? "  <- kept" : "");
     }
-    c.var_w = w0;
-    c.var_s = s0;
-    c.var_tpw = tpw0;
-    c.var_order = o0;
-    c.place = pl0;
-    return tsp_plan_set_panels(p, c.bm, 0, 1);
+    return keep ? apply_best() : restore();
 }
 
 // One tuning measurement of whole steps: a warm-up step, then enough steps to
