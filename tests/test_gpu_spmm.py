@@ -178,7 +178,7 @@ def test_panel_sweep_and_wide_chunks(gpu, orc, prec):
             for th in ((4096, 4096, 4096), (8, 8, 8)):
                 plan.set_th(*th)
                 full = th[0] == 4096
-                for w in ((64,) if bm == 64 else (64, 128, 256) if full else (128,)):
+                for w in ((64,) if bm == 64 else (64, 128, 256) if full else (128, 256)):
                     for s, order, place in ((1, 1, 0), (2, 2, 1), (1, 2, 1)) if full else ((1, 2, 1),):
                         plan.set_variant(bm, w, s, 1, order)
                         plan.set_placement(bm, place)
