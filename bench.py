@@ -76,10 +76,10 @@ def gather_calibration(hip, reps):
     hip.tsp_free(sink)
 
 
-def copy_calibration(hip, nbytes, reps):
+def copy_calibration(hip, nbytes, reps, quiet=False):
     """Plain 16-byte-vector copy of nbytes (dst = src): its FETCH_SIZE /
     WRITE_SIZE per dispatch calibrate the HBM byte counters, its time gives the
-    achievable copy bandwidth."""
+    achievable copy bandwidth (returned in GB/s, read plus write)."""
     import ctypes as C
     nbytes = (nbytes + 15) // 16 * 16
     src, dst = C.c_void_p(), C.c_void_p()
@@ -98,10 +98,14 @@ def copy_calibration(hip, nbytes, reps):
     ms = C.c_float()
     hip.tsp_event_elapsed_ms(C.byref(ms), e0, e1)
     t = ms.value / reps
-    print(json.dumps({"copy_bytes": nbytes, "ms": round(t, 5),
-                      "gbs_read_plus_write": round(2 * nbytes / (t * 1e-3) / 1e9, 1)}), flush=True)
+    gbs = 2 * nbytes / (t * 1e-3) / 1e9
+    if not quiet:
+        print(json.dumps({"copy_bytes": nbytes, "ms": round(t, 5), "gbs_read_plus_write": round(gbs, 1)}), flush=True)
+    hip.tsp_event_destroy(e0)
+    hip.tsp_event_destroy(e1)
     hip.tsp_free(src)
     hip.tsp_free(dst)
+    return gbs
 
 
 def cold_steps(hip, plan, reps, stream_bytes, flush_bytes=512 << 20):
@@ -560,6 +564,16 @@ def main():
     plan.close()
     del A, subs
     ceiling = gather_ceiling(hip)
+    # the measured copy-bandwidth peak (a 512 MB copy back to back, read plus
+    # write), beside the 8 TB/s spec peak the roofline fraction uses
+    copy_gbs = copy_calibration(hip, 512 << 20, 10, quiet=True)
+
+    def vs_copy(roof):
+        roof["copy_peak_gbs"] = round(copy_gbs, 1)
+        roof["frac_of_copy"] = round(roof["achieved"] / copy_gbs, 4)
+        return roof
+
+    vs_copy(rec["roofline"])
 
     def gather_stats(r):
         dk = r["classes"][max(r["classes"], key=lambda k: r["classes"][k]["ms"])]
@@ -581,6 +595,7 @@ def main():
             "workload": t["workload"], "ms_per_step": round(t["ms_per_step"], 6), "tflops": round(t["tflops"], 4),
             "long_window": t["long_window"], "kernel": t["roofline"]["kernel"],
             "kernel_ms": t["roofline"]["kernel_ms"], "frac": t["roofline"]["frac"],
+            "frac_of_copy": vs_copy(t["roofline"])["frac_of_copy"],
             "alg_bytes_per_launch": t["roofline"]["alg_bytes_per_launch"], "traffic": t["roofline"]["traffic"],
             "traffic_over_alg": t["roofline"]["traffic_over_alg"], "traffic_source": t["roofline"]["traffic_source"],
             "gather": gather_stats(t), "hot_rows": t["hot_rows"], "th": t["th"], "tilenum": t["tilenum"],

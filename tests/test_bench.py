@@ -47,6 +47,9 @@ def test_bench_json_line(tsp):
         assert k in roof, k
     assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and roof["peak"] == 8000.0
     assert roof["frac"] == pytest.approx(roof["achieved"] / roof["peak"], rel=1e-2, abs=1e-4)
+    # the same achieved rate against the copy bandwidth measured in the run
+    assert 1000 < roof["copy_peak_gbs"] < roof["peak"]
+    assert roof["frac_of_copy"] == pytest.approx(roof["achieved"] / roof["copy_peak_gbs"], rel=1e-2, abs=1e-4)
     cpu = d["cpu_baseline"]
     for k in ("value", "unit", "cores", "kind", "sample"):
         assert k in cpu, k
