@@ -68,4 +68,5 @@ def test_bench_json_line(tsp):
     assert "fp16, colB 128" in t["workload"] and t["tflops"] > 0
     assert t["tflops"] == pytest.approx(2 * 32768 * 128 / (t["ms_per_step"] * 1e-3) / 1e12, rel=2e-3)
     assert t["frac"] > 0 and t["kernel"].startswith("spmm_kernel<")
+    assert t["cold_cache"]["reps"] == 3 and t["cold_cache"]["ms_per_step"] > 0
     assert d["replay"].startswith("--no-tune --th ")
