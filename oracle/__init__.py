@@ -6,8 +6,8 @@ algorithms.  Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 ``cpu_baseline`` leg may import this package, and only as the checker or the
 reported CPU baseline -- never as the computation under test.
 
-Parity status of each function (what pins it) is documented in oracle.c and
-DESIGN.md; the pinning tests are tests/test_oracle_*.py.
+Parity status of each function (what pins it) is documented in the header
+of oracle.c; the pinning tests are tests/test_oracle_*.py.
 """
 from __future__ import annotations
 

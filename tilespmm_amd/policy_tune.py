@@ -26,11 +26,11 @@ tool rebuilds the policy for gfx950:
             thresholds, which the runtime tuning times, contain a near-best
             one; writes tilespmm_amd/host/th_calibration.h.
 
-  python -m tilespmm_amd.policy_tune sweep --corpus small --out gpurun_out/policy.jsonl
-  python -m tilespmm_amd.policy_tune fit --inp gpurun_out/policy.jsonl
-  python -m tilespmm_amd.policy_tune check --inp gpurun_out/policy.jsonl
-  python -m tilespmm_amd.policy_tune thsweep --configs 1 2 3 4 --corpus small --out gpurun_out/th.jsonl
-  python -m tilespmm_amd.policy_tune thfit --inp gpurun_out/th.jsonl --header tilespmm_amd/host/th_calibration.h
+  python -m tilespmm_amd.policy_tune sweep --corpus small --out sweeps/policy.jsonl
+  python -m tilespmm_amd.policy_tune fit --inp sweeps/policy.jsonl
+  python -m tilespmm_amd.policy_tune check --inp sweeps/policy.jsonl
+  python -m tilespmm_amd.policy_tune thsweep --configs 1 2 3 4 --corpus small --out sweeps/th.jsonl
+  python -m tilespmm_amd.policy_tune thfit --inp sweeps/th.jsonl --header tilespmm_amd/host/th_calibration.h
 """
 from __future__ import annotations
 
