@@ -98,17 +98,20 @@ __device__ __forceinline__ int place_block(int b, int nb, int placement)
 // Waves per SIMD the register allocation must leave room for, where the
 // compiler's own choice lands a few registers past a step in occupancy: the
 // 64-row kernel with 64-column chunks fits 3 waves in 168 registers, the
-// synchronised fp16 16-row kernel with 128-column chunks (configuration 4's)
-// 5 waves in 96; elsewhere the compiler decides.
-template <int BM, int W, int PREC, int S, bool SY>
+// synchronised fp16 16-row and 8-row kernels with 128-column chunks
+// (configuration 4's) 5 waves in 96, the dense fp16 8-row kernel with
+// 256-column chunks 4 waves in 128; elsewhere the compiler decides.
+template <int BM, int W, int PREC, int S, bool PK, bool SY>
 constexpr int kMinWaves = BM == 64 && W == 64 && S == 1 && !SY                                      ? 3
                           : SY && PREC == TSP_PREC_FP16 && BM == 16 && W == 128 && S == 1 ? 5
+                          : SY && PREC == TSP_PREC_FP16 && BM == 8 && W == 128 && S == 1  ? 5
+                          : !SY && !PK && PREC == TSP_PREC_FP16 && BM == 8 && W == 256 && S == 1 ? 4
                                                                                            : 1;
 
 // SY: the panel-synchronised sweep (SyncArgs) is compiled in; without it the
 // kernel runs one generation and the sync arguments are ignored.
 template <int BM, int W, int PREC, int S, bool PK, bool LI, bool SY>
-__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(kMinWaves<BM, W, PREC, S, SY>))) void spmm_kernel(
+__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(kMinWaves<BM, W, PREC, S, PK, SY>))) void spmm_kernel(
     int ntasks, int nchunks, int tasks_per_wave, int chunk_major, const void *__restrict__ val_,
     const uint64_t *__restrict__ bmp, const int *__restrict__ vptr,
     const unsigned *__restrict__ rows, const int *__restrict__ colstart,
