@@ -621,7 +621,9 @@ def test_tf32_prerounded_launch_matches_rounding_launch(gpu, orc, bm):
     reference-compatible launch (tsp_switch_v*) rounds in the kernel.  On raw
     fp32 inputs, NaN included, both give the same C bit for bit (unsplit
     schedule: no atomics), and tsp_round_tf32_device equals the host
-    rounding."""
+    rounding.  The same holds for the packed format with lane-loaded column
+    indices (whose 64-column kernels take their B operands straight from
+    the gathered registers), rounding or pre-rounded."""
     tsp = gpu
     hip, _ = tsp.load()
     rng = np.random.default_rng(40 + bm)
@@ -681,6 +683,28 @@ def test_tf32_prerounded_launch_matches_rounding_launch(gpu, orc, bm):
         # an unknown flag is refused before any launch
         assert hip.tsp_spmm_launch_ex(bm, 1, len(rows), cbp, bufs["valr"], None, None, bufs["rows"], bufs["cs"],
                                       bufs["Br"], bufs["C2"], bufs["col"], A.rows, None, 0, 0, 0, 0, 0, 2) != 0
+        if bm != 64:
+            # packed A with lane-loaded indices and 64-column chunks (the
+            # gathered B registers are the MFMA operands, no LDS panel): the
+            # rounding launch on the raw values and the pre-rounded launch
+            # both equal the dense rounding launch bit for bit
+            bn = tsp.tile_bn(bm, 1)
+            up("bmp", np.ascontiguousarray(arr["bitmap"]))
+            for src, flags, cname in (("val", 2, "C3"), ("valr", 3, "C4")):
+                nv = C.c_longlong()
+                pv, vp = C.c_void_p(), C.c_void_p()
+                assert hip.tsp_tiles_pack_device(t.tilenum, bm, bn, 1, bufs[src], bufs["bmp"], C.byref(nv),
+                                                 C.byref(pv), C.byref(vp), None) == 0
+                bufs[src + "_pv"], bufs[src + "_vp"] = pv, vp
+                up(cname, Cz)
+                for s in (1, 2, 3):
+                    say(f"packed tf32 lane indices bm={bm} flags={flags} stages={s}")
+                    assert hip.tsp_spmm_launch_ex(bm, 1, len(rows), cbp, pv, bufs["bmp"], vp, bufs["rows"],
+                                                  bufs["cs"], bufs["B" if src == "val" else "Br"], bufs[cname],
+                                                  bufs["col"], A.rows, None, 64, s, 0, 0, 0, flags) == 0
+                    assert hip.tsp_device_sync() == 0
+                    c = down(cname, Cz)
+                    assert np.array_equal(c.view(np.uint32), c1.view(np.uint32)), (flags, s)
     finally:
         for p in bufs.values():
             hip.tsp_free(p)

@@ -141,6 +141,12 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     constexpr int RG = BM >= 16 ? BM / 16 : 1;   // 16-row MFMA row groups
     constexpr int CB = W / 16;                   // 16-column MFMA blocks
     constexpr int KS = F16 ? 1 : BN / 4;         // tf32 MFMA steps per tile
+    // tf32 with lane-loaded indices and 64-column chunks: lane (n, q)
+    // gathers panel row KS*q + i, columns 4n .. 4n+3 with its load i, which
+    // is exactly its B operand of MFMA step i (CB = 4 adjacent columns of row
+    // KS*q + i), so the gathered registers feed the MFMAs directly and the
+    // panel never passes through LDS
+    constexpr bool DB = !F16 && LI && VPR == 16 && NV == KS && CB == VV;
     constexpr int AW = F16 ? (BN == 32 ? 4 : 2) : KS;   // A words per row group
     using VT = typename std::conditional<F16, _Float16, float>::type;
     using RV = VT __attribute__((ext_vector_type(CB)));     // CB values of one B row
@@ -501,7 +507,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         // Otherwise column n*CB + c of the chunk, so one LDS read of CB
         // adjacent values per B row serves all CB blocks (fp16 packed: four
         // rows' reads are then shuffled into K order).
-        auto compute = [&](const uint32_t (&a)[RG][AW]) {
+        auto compute = [&](const uint32_t (&a)[RG][AW], const u4 (&bd)[NV]) {
             if constexpr (TR) {
                 typedef short s4 __attribute__((ext_vector_type(4)));
                 using lds_s4 = __attribute__((address_space(3))) s4 *;
@@ -558,7 +564,17 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 const VT *lb = lds + ln * CB;
 #pragma unroll
                 for (int s = 0; s < KS; ++s) {
-                    const RV rv = *(const RV *)(lb + (KS * lq + s) * LDSW);
+                    RV rv;
+                    if constexpr (DB) {
+                        u4 x = bd[s];
+                        if constexpr (RND) {
+                            x.x = rnd(x.x); x.y = rnd(x.y);
+                            x.z = rnd(x.z); x.w = rnd(x.w);
+                        }
+                        rv = __builtin_bit_cast(RV, x);
+                    } else {
+                        rv = *(const RV *)(lb + (KS * lq + s) * LDSW);
+                    }
 #pragma unroll
                     for (int c = 0; c < CB; ++c)
 #pragma unroll
@@ -569,6 +585,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             }
         };
         auto stage_b = [&](const u4 (&src)[NV]) {
+            if constexpr (DB) return;
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
                 u4 x = src[i];
@@ -642,6 +659,9 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                         k = kn;
                     }
                     stage_b(bv[s]);
+                    u4 bcur[NV];
+#pragma unroll
+                    for (int i = 0; i < NV; ++i) bcur[i] = DB ? bv[s][i] : u4{0u, 0u, 0u, 0u};
                     uint32_t acur[RG][AW];
                     if constexpr (PK) {
                         finish_a_packed(araw[s], anib[s], acur);
@@ -661,7 +681,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                             load_meta(t + 2 * S, pm[s]);
                         }
                     }
-                    compute(acur);
+                    compute(acur, bcur);
                 }
             }
         }
