@@ -141,12 +141,12 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     constexpr int RG = BM >= 16 ? BM / 16 : 1;   // 16-row MFMA row groups
     constexpr int CB = W / 16;                   // 16-column MFMA blocks
     constexpr int KS = F16 ? 1 : BN / 4;         // tf32 MFMA steps per tile
-    // tf32 with lane-loaded indices and 64-column chunks: lane (n, q)
-    // gathers panel row KS*q + i, columns 4n .. 4n+3 with its load i, which
-    // is exactly its B operand of MFMA step i (CB = 4 adjacent columns of row
-    // KS*q + i), so the gathered registers feed the MFMAs directly and the
-    // panel never passes through LDS
-    constexpr bool DB = !F16 && LI && VPR == 16 && NV == KS && CB == VV;
+    // tf32 with 64-column chunks: lane (n, q) gathers panel row KS*q + i,
+    // columns 4n .. 4n+3 with its load i, which is exactly its B operand of
+    // MFMA step i (CB = 4 adjacent columns of row KS*q + i), so the gathered
+    // registers feed the MFMAs directly and the panel never passes through
+    // LDS.  Each load instruction still covers 4 whole 256-byte rows.
+    constexpr bool DB = !F16 && VPR == 16 && NV == KS && CB == VV;
     constexpr int AW = F16 ? (BN == 32 ? 4 : 2) : KS;   // A words per row group
     using VT = typename std::conditional<F16, _Float16, float>::type;
     using RV = VT __attribute__((ext_vector_type(CB)));     // CB values of one B row
@@ -258,14 +258,15 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
 
         // Panel rows of the lane's NV B loads.  Scalar column indices (LI
         // false): load i covers rows i*RPI .. i*RPI+RPI-1, row i*RPI + lane/VPR
-        // for this lane.  Lane-loaded indices (LI): the lane's rows are the NV
-        // consecutive rows (lane/VPR)*NV + i, whose column indices are
-        // consecutive in the tile's index list (one vector load).
+        // for this lane.  Lane-loaded indices (LI), and the direct tf32
+        // operands (DB): the lane's rows are the NV consecutive rows
+        // (lane/VPR)*NV + i (with LI their column indices are consecutive in
+        // the tile's index list: one vector load).
         int prow[NV], pcol[NV];
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int v = lane + 64 * i;
-            prow[i] = LI ? (lane / VPR) * NV + i : v / VPR;
+            prow[i] = LI || DB ? (lane / VPR) * NV + i : v / VPR;
             pcol[i] = (v % VPR) * VV;
         }
 
@@ -405,9 +406,12 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 if constexpr (LI) {
                     dst[i] = cs[i];
                 } else {
-                    int v = cs[i * RPI];
+                    // the lane's row: i*RPI + lrow, or KS*lrow + i when the
+                    // gathered registers are the MFMA operands
+                    auto row = [&](int r) { return DB ? KS * r + i : i * RPI + r; };
+                    int v = cs[row(0)];
 #pragma unroll
-                    for (int r = 1; r < RPI; ++r) v = lrow == r ? cs[i * RPI + r] : v;
+                    for (int r = 1; r < RPI; ++r) v = lrow == r ? cs[row(r)] : v;
                     dst[i] = v;
                 }
             }
