@@ -25,7 +25,10 @@
 //     operations execute in issue order, so one buffer is safe).  MFMA
 //     column n of 16-column block c is chunk column n*CB + c (CB = W/16
 //     blocks), so a lane reads CB adjacent values of a B row with one LDS
-//     read and owns CB adjacent output columns (one vector store per row);
+//     read and owns CB adjacent output columns (one vector store per row).
+//     Dense fp16 tiles read the panel with LDS transpose reads instead, and
+//     tf32 tiles with 64-column chunks gather their MFMA operands straight
+//     into registers (no LDS panel);
 //   * A tiles are canonical row-major BM x BN blocks read straight into MFMA
 //     operand registers (8 or 16 bytes per lane);
 //   * fp16: v_mfma_f32_16x16x16_f16 (BN = 16) and v_mfma_f32_16x16x32_f16
