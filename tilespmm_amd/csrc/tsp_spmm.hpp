@@ -513,7 +513,8 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         // column 16c + n -- the K-ordered operand, with no VALU shuffling.
         // Otherwise column n*CB + c of the chunk, so one LDS read of CB
         // adjacent values per B row serves all CB blocks (fp16 packed: four
-        // rows' reads are then shuffled into K order).
+        // rows' reads are then shuffled into K order); with DB those CB
+        // values are the lane's gathered registers `bd` instead.
         auto compute = [&](const uint32_t (&a)[RG][AW], const u4 (&bd)[NV]) {
             if constexpr (TR) {
                 typedef short s4 __attribute__((ext_vector_type(4)));
