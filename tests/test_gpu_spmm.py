@@ -13,9 +13,9 @@ import sys
 import numpy as np
 import pytest
 
-pytestmark = pytest.mark.gpu
+from parity_checks import TOL, assert_checksums
 
-TOL = {0: 1e-3, 1: 1e-4}
+pytestmark = pytest.mark.gpu
 
 
 def say(*a):
@@ -414,7 +414,8 @@ def test_config_full_parity(gpu, orc, config):
 def test_config_sampled_rows(gpu, orc, config, prec, colB):
     """Large configurations: full GPU run with the runtime tuning (the variant
     the bench ships), oracle on a row sample that includes the heaviest rows
-    and a uniform stride."""
+    and a uniform stride, and the row-sum and column-sum identities over all
+    of C."""
     tsp = gpu
     say(f"config {config} prec {prec} colB {colB}: generating")
     A, B, colB, cbp = tsp.gen_config(config, prec, colB)
@@ -425,6 +426,8 @@ def test_config_sampled_rows(gpu, orc, config, prec, colB):
     rows = np.unique(np.concatenate([np.argsort(lens)[-64:], np.arange(0, A.rows, max(1, A.rows // 3000))]))
     Cref, Cabs = reference(orc, A, B, colB, rows)
     assert_close(Cg[rows, :colB], Cref, Cabs, A.prec, f"config {config} sampled")
+    say(f"config {config}: row and column sums over all of C")
+    assert_checksums(orc, A, B, colB, Cg, f"config {config}")
 
 
 def skewed_matrix(tsp, rng, rows, cols, maxlen, prec):
