@@ -57,7 +57,7 @@ def test_policy_against_exhaustive_tuning(tsp):
         assert a, (pg, pd)
         slow.append(r["times_ms"][a[0]] / r["best_ms"])
     # The retrained table is within a few percent of the exhaustive optimum on
-    # its sweep; the provisional single-leaf table (candidate 24) is x1.06.
+    # its sweep; the provisional single-leaf table (candidate 24) is x1.07.
     assert np.mean(slow) <= 1.03 and max(slow) <= 1.25, (np.mean(slow), max(slow))
     prov = [r["times_ms"][24] / r["best_ms"] for r in records()]
     assert np.mean(slow) < np.mean(prov)
@@ -70,7 +70,7 @@ def test_policy_on_held_out_config5(tsp):
     """Configuration 5 (RMAT scale 22) is not in the training sweep.  Its
     exhaustive sweep with the full shipped path (runtime tuning of every
     candidate) puts the policy's pick within a few percent of the best
-    candidate: fp16 x1.004 (colB 64) and x1.028 (colB 128), tf32 x1.012 and
+    candidate: fp16 x1.000 (colB 64) and x1.038 (colB 128), tf32 x1.000 and
     x1.000."""
     g, d = tsp.policy_candidates()
     recs = [json.loads(l) for l in open(HELDOUT) if l.strip()]
