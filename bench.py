@@ -421,6 +421,21 @@ def measure(tsp, hip, config, prec, colB, args, headline):
            "roofline": roof, "classes": cls, "pre_ms": pre,
            "replay": pins_of(plan, th, cls)}
 
+    # the same steps replayed from one HIP graph: one submission per graph
+    # instead of one launch per kernel (reported beside the eager protocol,
+    # which stays the value, as the reference times it)
+    if headline and not args.no_graph:
+        gsteps = max(10, args.steps)
+        plan.graph_capture(gsteps)
+        greps = max(3, min(1000, int(round(50.0 / (gsteps * ms)))))
+        plan.graph_time(1)
+        gms = plan.graph_time(greps)
+        plan.graph_free()
+        rec["graph"] = {
+            "steps_per_graph": gsteps, "replays": greps, "ms_per_step": round(gms, 6),
+            "tflops": round(2.0 * A.nnz * colB / (gms * 1e-3) / 1e12, 4),
+            "note": "the same steps captured once (tsp_plan_graph_capture) and replayed as HIP graphs; "
+                    "`value` and `ms_per_step` are eager back-to-back launches"}
     # the cold-cache leg runs for the headline and for the target records
     if args.cold_reps > 0:
         cms, wms, cpms, cpb = cold_steps(hip, plan, args.cold_reps, step_bytes)
@@ -525,6 +540,7 @@ def main():
                     help="tune for single steps from a cold cache (TSP_TUNE_COLD) instead of back-to-back steps")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-vendor", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="skip the HIP graph replay leg")
     ap.add_argument("--class-reps", type=int, default=200,
                     help="launches per class in the class-alone timing (at least)")
     ap.add_argument("--class-min-ms", type=float, default=20.0,
@@ -624,6 +640,7 @@ def main():
         "classes": {f"bm{k}": {kk: (round(vv, 5) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in rec["classes"].items()},
         "cold_cache": rec.get("cold_cache"),
+        "graph": rec.get("graph"),
         "tune_mode": rec["tune_mode"],
         "vendor": rec.get("vendor"),
         "pre_ms": rec["pre_ms"],

@@ -268,6 +268,24 @@ int tsp_plan_warmup_clock(tsp_plan *plan, int max_iters, int *iters_run, unsigne
 int tsp_plan_warmup(tsp_plan *plan, int max_iters);
 /* Time `reps` back-to-back runs bracketed by events on the plan's main stream. */
 int tsp_plan_time(tsp_plan *plan, int reps, double *ms_per_iter);
+/* Steps replayed from a HIP graph.  No counterpart in the reference, which
+ * launches every kernel from the host; for callers that repeat the product
+ * many times (iterative methods, serving), where steps of a few
+ * microseconds are bound by the host's launch rate.
+ * tsp_plan_graph_capture runs one step, then captures `steps` steps (1 to
+ * 100000: the hot-row copy, the class kernels and their fork/join) into a
+ * graph on the plan's main stream; tsp_plan_graph_run replays it `replays`
+ * times there (asynchronously); tsp_plan_graph_time times replays as
+ * tsp_plan_time does, per step.  Every call that changes the configuration
+ * (tsp_plan_set_th / _variant / _format / _lane_indices / _placement /
+ * _panels / _hot_rows, tsp_plan_tune) makes the graph stale: run and time
+ * then return TSP_EINVAL until it is captured again.  Steps do not zero C
+ * (as with tsp_plan_time): with split tasks C accumulates across steps.
+ * tsp_plan_graph_free releases the graph (tsp_plan_destroy does too). */
+int tsp_plan_graph_capture(tsp_plan *plan, int steps);
+int tsp_plan_graph_run(tsp_plan *plan, int replays);
+int tsp_plan_graph_time(tsp_plan *plan, int replays, double *ms_per_step);
+int tsp_plan_graph_free(tsp_plan *plan);
 /* Time one class alone (reps launches) on the stream a step launches it on:
    its own stream, or the main stream when it is the plan's only class. */
 int tsp_plan_time_class(tsp_plan *plan, int bm, int reps, double *ms_per_launch);

@@ -107,6 +107,16 @@ int tsp_event_elapsed_ms(float *ms, void *start, void *stop);
  * explicit stream -> event dependency, used to join class streams. */
 int tsp_stream_create_nonblocking(void **stream);
 int tsp_stream_wait_event(void *stream, void *event);
+/* HIP graphs (no counterpart in the reference, which launches every kernel
+ * from the host): tsp_stream_begin_capture starts a thread-local capture of
+ * `stream` (work recorded on other streams that wait on its events joins
+ * it); tsp_stream_end_capture ends it and instantiates the graph into
+ * *graph_exec (NULL on failure; the capture is ended either way);
+ * tsp_graph_launch replays it on a stream; tsp_graph_destroy frees it. */
+int tsp_stream_begin_capture(void *stream);
+int tsp_stream_end_capture(void *stream, void **graph_exec);
+int tsp_graph_launch(void *graph_exec, void *stream);
+int tsp_graph_destroy(void *graph_exec);
 
 /* Tile SpMM launch, one row-block class:
  *   C[rows of task][cols] (=, or += atomically for split tasks)

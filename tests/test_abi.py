@@ -89,6 +89,18 @@ def test_error_strings_and_arg_checks(tsp):
     assert panels(0, 1000, 256, dummy, 0) == 1001
     assert panels(0, 1000, 256, dummy, 1024, lag=0) == 1001          # a lead of at least one panel
     assert panels(1, 1000, 256, dummy, 1024, ntasks=0) == 0          # nothing to do
+    # HIP graphs: the null stream cannot be captured, a null graph is neither
+    # launched nor an error to free, and a null plan is refused; all before
+    # any device call
+    assert hip.tsp_stream_begin_capture(None) == 1001
+    assert hip.tsp_stream_end_capture(None, None) == 1001
+    assert hip.tsp_graph_launch(None, None) == 1001
+    assert hip.tsp_graph_destroy(None) == 0
+    _, host = tsp.load()
+    assert host.tsp_plan_graph_capture(None, 1) == 1001
+    assert host.tsp_plan_graph_run(None, 1) == 1001
+    assert host.tsp_plan_graph_time(None, 1, None) == 1001
+    assert host.tsp_plan_graph_free(None) == 1001
 
 
 def test_cli_usage_and_errors(tmp_path):

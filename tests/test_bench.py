@@ -57,6 +57,10 @@ def test_bench_json_line(tsp):
     assert "whole matrix" in cpu["sample"]
     cold = d["cold_cache"]
     assert cold["reps"] == 3 and cold["ms_per_step"] > 0 and cold["copy_cold_ms"] > 0
+    # the HIP graph leg: the same steps replayed from a graph
+    gr = d["graph"]
+    assert gr["steps_per_graph"] >= 10 and gr["replays"] >= 3 and gr["ms_per_step"] > 0
+    assert gr["tflops"] == pytest.approx(2 * 32768 * 32 / (gr["ms_per_step"] * 1e-3) / 1e12, rel=2e-3)
     # the roofline's kernel runs inside the step: its time cannot exceed the
     # step's (C1's 4-microsecond steps are launch-bound and excepted)
     if d["ms_per_step"] > 0.05:

@@ -492,6 +492,67 @@ def test_hot_rows_bit_identical(gpu, orc, prec):
                 plan.close()
 
 
+@pytest.mark.parametrize("prec", [0, 1])
+def test_graph_replay_matches_eager_steps(gpu, orc, prec):
+    """Steps replayed from a HIP graph (tsp_plan_graph_*) give the eager
+    step's C bit for bit (unsplit schedule: plain stores), replay after
+    replay with eager work in between: every class (fork/join across the
+    class streams), hot B rows re-copied inside each step, and a dense class
+    on the panel-synchronised sweep.  A configuration change makes the graph
+    stale until it is captured again; split tasks stay within tolerance."""
+    tsp = gpu
+    hip, host = tsp.load()
+    rng = np.random.default_rng(88 + prec)
+    A = skewed_matrix(tsp, rng, 3000, 4096, 60, prec)
+    colB = 128
+    B, cbp = random_b(tsp, rng, A.cols, colB, prec)
+    Cref, Cabs = reference(orc, A, B, colB)
+    subs = tsp.matrix_split(A, 1.0, 1.0)
+    assert all(s.rows > 0 for s in subs)
+    tiles = [tsp.tile_create(s, A.cols, bm, A.prec) for s, bm in zip(subs, (64, 16, 8))]
+    plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, A.prec, B)
+    dc = C.c_void_p()
+    assert host.tsp_plan_device_c(plan.p, C.byref(dc)) == 0
+    cbytes = A.rows * cbp * 4
+    try:
+        unsplit = (1 << 20,) * 3
+        for label, setup in (("default", lambda: None),
+                             ("hot rows", lambda: plan.set_hot_rows(1 << 20)),
+                             ("panel sweep", lambda: (plan.set_format(16, 1), plan.set_panels(16, 256, 2)))):
+            say(f"graph replay prec={prec}: {label}")
+            plan.set_th(*unsplit)
+            setup()
+            plan.run(zero_c=True)
+            eager = plan.download_c()
+            assert_close(eager[:, :colB], Cref, Cabs, prec, label)
+            plan.graph_capture(3)
+            for rnd in range(3):
+                assert hip.tsp_memset(dc, 0, cbytes) == 0
+                plan.graph_run(1 + rnd)
+                assert hip.tsp_device_sync() == 0
+                got = plan.download_c()
+                assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), (label, rnd)
+                plan.run(zero_c=True)             # eager work between replays
+                plan.time(2)
+            assert plan.graph_time(2) > 0
+            # a configuration change makes the captured graph stale
+            plan.set_th(*unsplit)
+            with pytest.raises(tsp.TspError):
+                plan.graph_run(1)
+        # split tasks (atomic flushes): one zeroed replay of one step
+        plan.set_th(8, 8, 8)
+        plan.graph_capture(1)
+        assert hip.tsp_memset(dc, 0, cbytes) == 0
+        plan.graph_run(1)
+        assert hip.tsp_device_sync() == 0
+        assert_close(plan.download_c()[:, :colB], Cref, Cabs, prec, "split tasks, graph")
+        plan.graph_free()
+        with pytest.raises(tsp.TspError):
+            plan.graph_run(1)
+    finally:
+        plan.close()
+
+
 def test_hot_row_device_helpers(gpu):
     """tsp_colidx_count / tsp_colidx_remap / tsp_hot_rows_gather against numpy."""
     tsp = gpu

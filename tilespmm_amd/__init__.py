@@ -155,6 +155,10 @@ HIP_SYMBOLS = {
     "tsp_event_elapsed_ms": (C.c_int, [C.POINTER(C.c_float), _P, _P]),
     "tsp_stream_create_nonblocking": (C.c_int, [C.POINTER(C.c_void_p)]),
     "tsp_stream_wait_event": (C.c_int, [_P, _P]),
+    "tsp_stream_begin_capture": (C.c_int, [_P]),
+    "tsp_stream_end_capture": (C.c_int, [_P, C.POINTER(_P)]),
+    "tsp_graph_launch": (C.c_int, [_P, _P]),
+    "tsp_graph_destroy": (C.c_int, [_P]),
     "tsp_spmm_launch": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P,
                                   C.c_int, _P]),
     "tsp_spmm_launch_variant": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P,
@@ -246,6 +250,10 @@ HOST_SYMBOLS = {
     "tsp_plan_warmup": (C.c_int, [_P, C.c_int]),
     "tsp_plan_warmup_clock": (C.c_int, [_P, C.c_int, _IP, C.POINTER(C.c_uint)]),
     "tsp_plan_time": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double)]),
+    "tsp_plan_graph_capture": (C.c_int, [_P, C.c_int]),
+    "tsp_plan_graph_run": (C.c_int, [_P, C.c_int]),
+    "tsp_plan_graph_time": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double)]),
+    "tsp_plan_graph_free": (C.c_int, [_P]),
     "tsp_plan_time_class": (C.c_int, [_P, C.c_int, C.c_int, C.POINTER(C.c_double)]),
     "tsp_plan_download_c": (C.c_int, [_P, _P]),
     "tsp_plan_device_c": (C.c_int, [_P, C.POINTER(C.c_void_p)]),
@@ -722,6 +730,22 @@ class Plan:
         ms = C.c_double()
         _check("tsp_plan_time", load()[1].tsp_plan_time(self.p, reps, C.byref(ms)))
         return ms.value
+
+    def graph_capture(self, steps: int) -> None:
+        """Capture `steps` steps into a HIP graph (tsp_plan_graph_capture)."""
+        _check("tsp_plan_graph_capture", load()[1].tsp_plan_graph_capture(self.p, steps))
+
+    def graph_run(self, replays: int = 1) -> None:
+        _check("tsp_plan_graph_run", load()[1].tsp_plan_graph_run(self.p, replays))
+
+    def graph_time(self, replays: int) -> float:
+        """Milliseconds per step over `replays` replays of the captured graph."""
+        ms = C.c_double()
+        _check("tsp_plan_graph_time", load()[1].tsp_plan_graph_time(self.p, replays, C.byref(ms)))
+        return ms.value
+
+    def graph_free(self) -> None:
+        _check("tsp_plan_graph_free", load()[1].tsp_plan_graph_free(self.p))
 
     def time_class(self, bm: int, reps: int) -> float:
         ms = C.c_double()

@@ -222,6 +222,34 @@ int tsp_event_elapsed_ms(float *ms, void *start, void *stop)
     if (!ms) return TSP_EINVAL;
     return (int)hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop);
 }
+int tsp_stream_begin_capture(void *stream)
+{
+    if (!stream) return TSP_EINVAL;       // the null stream cannot be captured
+    return (int)hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal);
+}
+int tsp_stream_end_capture(void *stream, void **graph_exec)
+{
+    if (!stream) return TSP_EINVAL;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture((hipStream_t)stream, &g);
+    if (graph_exec) *graph_exec = nullptr;
+    if (e == hipSuccess && graph_exec) {
+        hipGraphExec_t x = nullptr;
+        e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+        if (e == hipSuccess) *graph_exec = (void *)x;
+    }
+    if (g) (void)hipGraphDestroy(g);
+    return (int)e;
+}
+int tsp_graph_launch(void *graph_exec, void *stream)
+{
+    if (!graph_exec) return TSP_EINVAL;
+    return (int)hipGraphLaunch((hipGraphExec_t)graph_exec, (hipStream_t)stream);
+}
+int tsp_graph_destroy(void *graph_exec)
+{
+    return graph_exec ? (int)hipGraphExecDestroy((hipGraphExec_t)graph_exec) : TSP_OK;
+}
 
 int tsp_spmm_launch(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
                     const unsigned *d_rows, const int *d_colstart, const void *d_B, float *d_C,

@@ -85,6 +85,12 @@ struct tsp_plan {
     void *main = nullptr;
     void *ev0 = nullptr, *ev1 = nullptr;
     void *done[3] = {nullptr, nullptr, nullptr};
+    // A captured HIP graph of graph_steps steps; it holds the kernel
+    // arguments of the configuration it was captured under (version), and
+    // every call that changes the configuration bumps the version.
+    void *graph = nullptr;
+    int graph_steps = 0;
+    unsigned long long version = 0, graph_version = 0;
 };
 
 #define TSP_TRY(x)                  \
@@ -235,6 +241,7 @@ static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
 
 extern "C" int tsp_plan_set_panels(tsp_plan *p, int bm, int panel_rows, int lag)
 {
+    if (p) ++p->version;          // any captured graph is stale now
     if (!p || panel_rows < 0 || (panel_rows > 0 && (panel_rows < 64 || (panel_rows & (panel_rows - 1)) || lag < 1)))
         return TSP_EINVAL;
     for (ClassDev &c : p->cls)
@@ -266,6 +273,7 @@ extern "C" int tsp_plan_get_panels(tsp_plan *p, int bm, int *panel_rows, int *la
 
 extern "C" int tsp_plan_set_format(tsp_plan *p, int bm, int fmt)
 {
+    if (p) ++p->version;          // any captured graph is stale now
     if (!p || fmt < 0 || fmt > 2) return TSP_EINVAL;
     for (ClassDev &c : p->cls)
         if (c.bm == bm) {
@@ -291,6 +299,7 @@ extern "C" int tsp_plan_get_format(tsp_plan *p, int bm)
 extern "C" int tsp_plan_set_variant(tsp_plan *p, int bm, int w, int stages, int tasks_per_wave,
                                     int order)
 {
+    if (p) ++p->version;          // any captured graph is stale now
     if (!p) return TSP_EINVAL;
     for (ClassDev &c : p->cls)
         if (c.bm == bm) {
@@ -306,6 +315,7 @@ extern "C" int tsp_plan_set_variant(tsp_plan *p, int bm, int w, int stages, int 
 
 extern "C" int tsp_plan_set_lane_indices(tsp_plan *p, int bm, int on)
 {
+    if (p) ++p->version;          // any captured graph is stale now
     if (!p || (on != 0 && on != 1)) return TSP_EINVAL;
     for (ClassDev &c : p->cls)
         if (c.bm == bm) {
@@ -326,6 +336,7 @@ extern "C" int tsp_plan_get_lane_indices(tsp_plan *p, int bm)
 
 extern "C" int tsp_plan_set_placement(tsp_plan *p, int bm, int placement)
 {
+    if (p) ++p->version;          // any captured graph is stale now
     if (!p || (placement != TSP_PLACE_CONTIGUOUS && placement != TSP_PLACE_INTERLEAVED &&
                placement != TSP_PLACE_CHUNK_XCD))
         return TSP_EINVAL;
@@ -363,6 +374,7 @@ extern "C" int tsp_plan_destroy(tsp_plan *p)
 {
     if (!p) return TSP_OK;
     tsp_device_sync();
+    tsp_graph_destroy(p->graph);
     for (ClassDev &c : p->cls) {
         tsp_free(c.d_val);
         tsp_free(c.d_pval);
@@ -566,6 +578,7 @@ extern "C" int tsp_plan_create_csr(tsp_plan **out, int device_id, const tsp_sub_
 
 extern "C" int tsp_plan_set_th(tsp_plan *p, int th64, int th16, int th8)
 {
+    if (p) ++p->version;          // any captured graph is stale now
     if (!p) return TSP_EINVAL;
     const int th[3] = {th64, th16, th8};
     for (int i = 0; i < 3; ++i) {
@@ -653,6 +666,7 @@ static int count_gathers(tsp_plan *p)
 
 extern "C" int tsp_plan_set_hot_rows(tsp_plan *p, long long budget_bytes)
 {
+    if (p) ++p->version;          // any captured graph is stale now
     if (!p || budget_bytes < 0) return TSP_EINVAL;
     const long long rb = b_row_bytes(p);
     const long long want = std::min<long long>(p->hot_cap, std::min(budget_bytes, TSP_HOT_MAX_BYTES) / rb);
@@ -727,6 +741,69 @@ extern "C" int tsp_plan_time(tsp_plan *p, int reps, double *ms)
     float t = 0.f;
     TSP_TRY(tsp_event_elapsed_ms(&t, start, p->ev1));
     *ms = (double)t / reps;
+    return TSP_OK;
+}
+
+// HIP graph of `steps` steps: one graph launch replays them with a single
+// submission, so back-to-back steps of a few microseconds are no longer
+// bound by the host's per-kernel launch rate.  One step runs eagerly first
+// (it settles the per-class launch state, e.g. the first launch of a
+// synchronised sweep zeroes its counters), then the steps are captured on
+// the main stream; the class streams join the capture through the step's
+// own fork and join events.
+extern "C" int tsp_plan_graph_capture(tsp_plan *p, int steps)
+{
+    if (!p || steps < 1 || steps > 100000) return TSP_EINVAL;
+    TSP_TRY(tsp_plan_graph_free(p));
+    TSP_TRY(fork_join(p, 1));
+    TSP_TRY(tsp_stream_sync(p->main));
+    TSP_TRY(tsp_stream_begin_capture(p->main));
+    const int st = fork_join(p, steps);
+    void *g = nullptr;
+    const int se = tsp_stream_end_capture(p->main, st == TSP_OK ? &g : nullptr);
+    if (st != TSP_OK || se != TSP_OK) {
+        tsp_graph_destroy(g);
+        return st != TSP_OK ? st : se;
+    }
+    p->graph = g;
+    p->graph_steps = steps;
+    p->graph_version = p->version;
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_graph_free(tsp_plan *p)
+{
+    if (!p) return TSP_EINVAL;
+    if (p->graph) {
+        TSP_TRY(tsp_stream_sync(p->main));
+        TSP_TRY(tsp_graph_destroy(p->graph));
+    }
+    p->graph = nullptr;
+    p->graph_steps = 0;
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_graph_run(tsp_plan *p, int replays)
+{
+    if (!p || replays < 0) return TSP_EINVAL;
+    if (!p->graph || p->graph_version != p->version) return TSP_EINVAL;   // none, or stale
+    for (int r = 0; r < replays; ++r) TSP_TRY(tsp_graph_launch(p->graph, p->main));
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_graph_time(tsp_plan *p, int replays, double *ms_per_step)
+{
+    if (!p || replays <= 0 || !ms_per_step) return TSP_EINVAL;
+    void *start = nullptr;
+    TSP_TRY(tsp_event_create(&start));
+    std::unique_ptr<void, int (*)(void *)> guard(start, tsp_event_destroy);
+    TSP_TRY(tsp_event_record(start, p->main));
+    TSP_TRY(tsp_plan_graph_run(p, replays));
+    TSP_TRY(tsp_event_record(p->ev1, p->main));
+    TSP_TRY(tsp_event_sync(p->ev1));
+    float t = 0.f;
+    TSP_TRY(tsp_event_elapsed_ms(&t, start, p->ev1));
+    *ms_per_step = (double)t / ((double)replays * p->graph_steps);
     return TSP_OK;
 }
 
@@ -1202,6 +1279,7 @@ static int decide_hot_rows(tsp_plan *p, bool *kept)
 
 extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model_ms, double *tune_ms)
 {
+    if (p) ++p->version;          // any captured graph is stale now
     if (!p) return TSP_EINVAL;
     const double t0 = now_ms();
     std::vector<int> opts[3];
