@@ -12,6 +12,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <chrono>
 #include <map>
@@ -1038,6 +1039,7 @@ static int tune_class(tsp_plan *p, ClassDev &c)
         int w, order, place;
     };
     std::vector<WOpt> wo;
+    WOpt runner{-1, 0, 0};               // the next best of step 3, when close
     for (int place = TSP_PLACE_CONTIGUOUS; place <= TSP_PLACE_CHUNK_XCD; ++place) {
         const std::vector<int> dp = places(p->colB_p / k.cols_per_task);
         if (std::find(dp.begin(), dp.end(), place) != dp.end())
@@ -1076,6 +1078,10 @@ static int tune_class(tsp_plan *p, ClassDev &c)
         for (size_t j = 0; j < wo.size(); ++j)
             if (wo[j].w == 0 && wo[j].place == keep.place) kj = j;
         if (wms[bw] > 0.99 * wms[kj]) bw = kj;
+        size_t br = bw;
+        for (size_t j = 0; j < wo.size(); ++j)
+            if (j != bw && (br == bw || wms[j] < wms[br])) br = j;
+        if (br != bw && wms[br] < 1.03 * wms[bw]) runner = wo[br];
         c.var_w = wo[bw].w;
         c.var_order = wo[bw].order;
         c.place = wo[bw].place;
@@ -1087,41 +1093,64 @@ static int tune_class(tsp_plan *p, ClassDev &c)
     }
 
     // 4. pipeline depth (1-3 tiles in flight per wave) x, on the packed
-    //    format, scalar or lane-loaded column indices; the rest as kept.  A
-    //    deeper pipeline holds more B gathers in flight per wave but costs
-    //    registers (occupancy); lane-loaded indices save the select chain
-    //    for a vector load.  Depth 1 with scalar indices stays unless another
-    //    option is 1% faster.
-    const int w_kept = c.var_w ? c.var_w : k.cols_per_task;
+    //    format, scalar or lane-loaded column indices, for step 3's choice and
+    //    for its runner-up when that was within 3% (a width that wins at
+    //    depth 1 can lose once both are tuned); the rest as kept.  A deeper
+    //    pipeline holds more B gathers in flight per wave but costs registers
+    //    (occupancy); lane-loaded indices save the select chain for a vector
+    //    load.  The fastest option wins unless it is within 1% of step 3's
+    //    choice at depth 1 with scalar indices (comparing each option with
+    //    the best so far instead would make the pick depend on the order).
+    std::vector<WOpt> dw{{c.var_w, c.var_order, c.place}};
+    if (runner.w >= 0) dw.push_back(runner);
     const int nli = c.fmt == 2 ? 2 : 1;
-    double sms[2][4];
-    for (auto &r : sms)
-        for (double &x : r) x = 1e30;
+    std::vector<std::array<std::array<double, 4>, 2>> sms(dw.size());
+    for (auto &t : sms)
+        for (auto &r : t) r.fill(1e30);
     for (int round = 0; round < 2; ++round)
-        for (int li = 0; li < nli; ++li)
-            for (int st = 1; st <= (w_kept == 256 ? 2 : 3); ++st) {
-                c.var_w = w_kept;
-                c.var_s = st;
-                c.var_li = li;
-                double t = 0;
-                TSP_TRY(tune_time_class(p, c.bm, &t));
-                sms[li][st] = std::min(sms[li][st], t);
+        for (size_t d = 0; d < dw.size(); ++d)
+            for (int li = 0; li < nli; ++li) {
+                const int wd = dw[d].w ? dw[d].w : k.cols_per_task;
+                for (int st = 1; st <= (wd == 256 ? 2 : 3); ++st) {
+                    c.var_w = dw[d].w;
+                    c.var_order = dw[d].order;
+                    c.place = dw[d].place;
+                    c.var_s = st;
+                    c.var_li = li;
+                    double t = 0;
+                    TSP_TRY(tune_time_class(p, c.bm, &t));
+                    sms[d][li][st] = std::min(sms[d][li][st], t);
+                }
             }
+    size_t db = 0;
     int sb = 1, lb = 0;
-    for (int li = 0; li < nli; ++li)
-        for (int st = 1; st <= 3; ++st)
-            if (sms[li][st] < 0.99 * sms[lb][sb]) {
-                sb = st;
-                lb = li;
-            }
+    for (size_t d = 0; d < dw.size(); ++d)
+        for (int li = 0; li < nli; ++li)
+            for (int st = 1; st <= 3; ++st)
+                if (sms[d][li][st] < sms[db][lb][sb]) {
+                    db = d;
+                    sb = st;
+                    lb = li;
+                }
+    if (sms[db][lb][sb] > 0.99 * sms[0][0][1]) {
+        db = 0;
+        sb = 1;
+        lb = 0;
+    }
+    c.var_w = dw[db].w;
+    c.var_order = dw[db].order;
+    c.place = dw[db].place;
     c.var_s = sb;
     c.var_li = lb;
     if (log)
-        for (int li = 0; li < nli; ++li)
-            for (int st = 1; st <= 3; ++st)
-                fprintf(stderr, "tune bm=%d stages %d %s indices: %.5f ms%s\n", c.bm, st, li ? "lane" : "scalar",
-                        sms[li][st], st == sb && li == lb ? "  <- kept" : "");
-    return tune_panels(p, c, sms[lb][sb]);
+        for (size_t d = 0; d < dw.size(); ++d)
+            for (int li = 0; li < nli; ++li)
+                for (int st = 1; st <= 3; ++st)
+                    fprintf(stderr, "tune bm=%d chunk width %d order=%d placement=%s stages %d %s indices: %.5f ms%s\n",
+                            c.bm, dw[d].w ? dw[d].w : k.cols_per_task, dw[d].order, place_name[dw[d].place], st,
+                            li ? "lane" : "scalar", sms[d][li][st],
+                            d == db && st == sb && li == lb ? "  <- kept" : "");
+    return tune_panels(p, c, sms[db][lb][sb]);
 }
 
 // 5. The panel-synchronised sweep (tsp_spmm_launch_panels) on the dense
