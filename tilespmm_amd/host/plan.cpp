@@ -1330,6 +1330,17 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
     int best[3] = {opts[0][0], opts[1][0], opts[2][0]};
     TSP_TRY(tsp_plan_set_th(p, best[0], best[1], best[2]));
     double t2 = now_ms(), t3 = t2;
+    // bring the clock up before the first option is timed: right after plan
+    // creation the GPU can still be ramping, which made the first options
+    // of the first step (the dense format of an 8-row class: 3.95 and 4.54
+    // us against 3.56 us later) look slower than they are
+    // (at most about 100 ms of steps)
+    if (tune && p->tune_mode == TSP_TUNE_BACK_TO_BACK) {
+        double one = 0;
+        TSP_TRY(tsp_plan_time(p, 1, &one));
+        const int iters = (int)std::min(20000.0, std::max(20.0, 100.0 / std::max(one, 1e-3)));
+        TSP_TRY(tsp_plan_warmup_clock(p, iters, nullptr, nullptr));
+    }
     bool hot_tuning = false;
     if (const char *pin = getenv("TSP_HOT_BYTES")) {
         TSP_TRY(tsp_plan_set_hot_rows(p, atoll(pin)));
