@@ -35,8 +35,11 @@ def log(*a):
 
 
 def alg_bytes(rows, nnz, s_a, k_rows, n, s_b):
-    """Compulsory bytes: CSR A (rowptr + colidx + values), the B rows the
-    product touches read once, C written once in fp32."""
+    """Compulsory bytes: CSR A (rowptr + colidx + values), k_rows rows of B
+    read once, C written once in fp32.  The roofline figure takes k_rows = K,
+    all of B's rows (4(M+1) + nnz(4+s_A) + K*N*s_B + M*N*4); with k_rows =
+    the distinct columns of A it is the touched-row figure reported beside
+    it."""
     return 4 * (rows + 1) + nnz * (4 + s_a) + k_rows * n * s_b + rows * n * 4
 
 
@@ -264,6 +267,13 @@ def apply_pins(plan, args):
     return th
 
 
+def variant_of(c):
+    """The runtime choices of one class beyond its kernel instantiation, as a
+    traffic profile records them."""
+    return {"order": c["order"], "placement": c["placement"], "tasks_per_wave": c["tasks_per_wave"],
+            "panel_rows": c["panel_rows"], "panel_lag": c["panel_lag"] if c["panel_rows"] else 0}
+
+
 def pins_of(plan, th, cls):
     """The bench flags that replay this plan's tuned configuration."""
     f, o, t, w, s, p, li, pr, lg = [], [], [], [], [], [], [], [], []
@@ -360,7 +370,8 @@ def measure(tsp, hip, config, prec, colB, args, headline):
         warm = plan.time_class(bm, args.class_reps)
         reps = int(min(20000, max(args.class_reps, args.class_min_ms / max(warm, 1e-4))))
         cms = plan.time_class(bm, reps)
-        b = alg_bytes(sb.rows, sb.nnz, s, kcols[bm], colB, s)
+        b = alg_bytes(sb.rows, sb.nnz, s, A.cols, colB, s)
+        b_touched = alg_bytes(sb.rows, sb.nnz, s, kcols[bm], colB, s)
         v = plan.get_variant(bm)
         w = v[0] or default_width(hip, bm, prec, cbp)
         bn = tsp.tile_bn(bm, prec)
@@ -372,12 +383,12 @@ def measure(tsp, hip, config, prec, colB, args, headline):
                    "lane_indices": max(0, plan.get_lane_indices(bm)),
                    "placement": {0: "contiguous", 1: "interleaved", 2: "chunk-xcd"}.get(plan.get_placement(bm), "?"),
                    "panel_rows": plan.get_panels(bm)[0], "panel_lag": plan.get_panels(bm)[1],
-                   "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9,
+                   "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9, "alg_bytes_touched": b_touched,
                    "gathered_lines": lines, "glines_per_s": lines / (cms * 1e-3) / 1e9}
     dom = max(cls, key=lambda k: cls[k]["ms"])
     dk = cls[dom]
     k_all = int(np.unique(A.colidx).size)
-    step_bytes = alg_bytes(A.rows, A.nnz, s, k_all, colB, s)
+    step_bytes = alg_bytes(A.rows, A.nnz, s, A.cols, colB, s)
     step_gbs = step_bytes / (ms * 1e-3) / 1e9
 
     # the dominant kernel's instantiation spmm_kernel<BM, W, PREC, S, PK, LI, SY>;
@@ -395,18 +406,25 @@ def measure(tsp, hip, config, prec, colB, args, headline):
         # the tuned instantiation may be the profile's main entry or one of
         # the alternatives profiled beside it
         entries = [pj.get(f"bm{dom}", {})] + [e for e in pj.get("alternatives", []) if e.get("bm") == dom]
-        hit = [e for e in entries if e.get("kernel", "").endswith(kname) and e.get("hot_rows", 0) == hot_n]
+        # the same instantiation, hot rows and runtime variant (chunk order,
+        # XCD placement, tasks per wave, panel sweep), as the profile's
+        # replay flags ran it
+        run_variant = variant_of(dk)
+        hit = [e for e in entries if e.get("kernel", "").endswith(kname) and e.get("hot_rows", 0) == hot_n
+               and e.get("variant") == run_variant]
         if hit:
             traffic, traffic_note = hit[0].get("hbm_bytes_per_launch"), os.path.relpath(prof, ROOT)
         else:
             traffic_note = (f"{os.path.relpath(prof, ROOT)} profiles "
-                            f"{', '.join(e.get('kernel', '?') + ' with ' + str(e.get('hot_rows', 0)) + ' hot rows' for e in entries)}"
-                            f", not the tuned {kname} with {hot_n}")
+                            f"{'; '.join(e.get('kernel', '?') + ' ' + json.dumps(e.get('variant')) + ' with ' + str(e.get('hot_rows', 0)) + ' hot rows' for e in entries)}"
+                            f", not the tuned {kname} {json.dumps(run_variant)} with {hot_n}")
     roof = {"bound": "hbm", "achieved": round(dk["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
             "traffic_over_alg": round(traffic / dk["alg_bytes"], 3) if traffic else None,
             "traffic_source": traffic_note, "kernel": kname, "kernel_ms": round(dk["ms"], 5),
             "alg_bytes_per_launch": dk["alg_bytes"],
+            "alg_bytes_touched_per_launch": dk["alg_bytes_touched"],
+            "frac_touched": round(dk["alg_bytes_touched"] / (dk["ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "step_achieved": round(step_gbs, 2), "step_frac": round(step_gbs / HBM_PEAK_GBS, 4),
             "step_alg_bytes": step_bytes}
 
@@ -472,8 +490,8 @@ def vendor_spmm(hip, A, B, colB, cbp, prec):
 
 def cpu_baseline(A, B, colB, prec):
     """The oracle's OpenMP CSR SpMM (fp32 accumulate, dynamic(64)) over the
-    WHOLE matrix on the host's cores: one warm-up run, then timed runs until
-    three are done or 20 s have passed; the median is reported."""
+    WHOLE matrix on the host's cores: one warm-up run, then five timed runs
+    (fewer only if they would pass 30 s); the median is reported."""
     import oracle
     a32 = oracle.values_f64(A.val, prec).astype(np.float32)
     b32 = oracle.values_f64(B[:, :colB].reshape(-1), prec).astype(np.float32).reshape(A.cols, colB)
@@ -482,7 +500,7 @@ def cpu_baseline(A, B, colB, prec):
     _, used = oracle.spmm_f32_omp(A.rows, A.rowptr, A.colidx, a32, b32, colB, out)
     first = time.perf_counter() - t1
     times, spent = [], 0.0
-    while len(times) < 3 and spent < 20.0:
+    while len(times) < 5 and spent + first < 30.0:
         t1 = time.perf_counter()
         oracle.spmm_f32_omp(A.rows, A.rowptr, A.colidx, a32, b32, colB, out)
         times.append(time.perf_counter() - t1)

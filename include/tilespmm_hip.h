@@ -335,8 +335,10 @@ int tsp_dev_tiles_free(tsp_dev_tiles *t);
  * *nvals = set bits over all tiles; when d_pval/d_vptr are non-NULL also
  * allocates and fills d_vptr[tilenum+1] (per-tile offsets) and d_pval
  * (values at the set bits in row-major bit order, + 4 zero elements).
- * d_val/d_bitmap as in tsp_dev_tiles.  No reference counterpart (the
- * reference has no packed format). */
+ * d_val/d_bitmap as in tsp_dev_tiles.  The offsets are ints: when the set
+ * bits plus the 4 padding elements exceed INT_MAX the call returns
+ * TSP_EINVAL (before any offset is formed) with *nvals = the 64-bit count.
+ * No reference counterpart (the reference has no packed format). */
 int tsp_tiles_pack_device(int tilenum, int bm, int bn, int prec, const void *d_val,
                           const unsigned long long *d_bitmap, long long *nvals, void **d_pval,
                           int **d_vptr, void *stream);
@@ -348,13 +350,15 @@ int tsp_tiles_pack_device(int tilenum, int bm, int bn, int prec, const void *d_v
  * for pval_capacity elements of the value type, which must hold the packed
  * values plus 4 padding elements.  *nvals = number of packed values (also
  * on failure for lack of room, which returns TSP_EINVAL, so the caller can
- * size the buffer).  The scan's per-block sums live in a static 1 MiB
+ * size the buffer).  As in tsp_tiles_pack_device, a count whose values plus
+ * padding exceed INT_MAX returns TSP_EINVAL (d_vptr then holds the per-tile
+ * counts, not offsets).  The scan's per-block sums live in a static 1 MiB
  * device array, so tilenum is limited to TSP_PACK_NOALLOC_MAX_TILES (larger
  * requests return TSP_EINVAL).  Calls no hipMalloc/hipFree; synchronises
  * `stream`.  Every call on one GPU shares that array: calls that overlap on
  * the same GPU (other threads, other streams) race and must be serialised
  * by the caller. */
-#define TSP_PACK_NOALLOC_MAX_TILES (((1LL << 18) - 1) * 2048)
+#define TSP_PACK_NOALLOC_MAX_TILES (((1LL << 18) - 3) * 2048)
 int tsp_tiles_pack_device_noalloc(int tilenum, int bm, int bn, int prec, const void *d_val,
                                   const unsigned long long *d_bitmap, void *d_pval,
                                   long long pval_capacity, int *d_vptr, long long *nvals,

@@ -13,6 +13,16 @@ from conftest import ROOT
 BENCH = os.path.join(ROOT, "bench.py")
 
 
+def test_alg_bytes_formula():
+    """The roofline's unit of work: configuration 5 (RMAT scale 22, tf32,
+    colB 64; nnz as the generator makes it) moves 3190.7 MB."""
+    sys.path.insert(0, ROOT)
+    import bench
+    m = 1 << 22
+    assert bench.alg_bytes(m, 128305642, 4, m, 64, 4) == 4 * (m + 1) + 128305642 * 8 + 2 * m * 64 * 4
+    assert round(bench.alg_bytes(m, 128305642, 4, m, 64, 4) / 1e6, 1) == 3190.7
+
+
 def test_bench_refuses_several_gpus():
     r = subprocess.run([sys.executable, BENCH, "--gpus", "2"], capture_output=True, text=True, timeout=120)
     assert r.returncode == 2
@@ -47,6 +57,10 @@ def test_bench_json_line(tsp):
         assert k in roof, k
     assert roof["bound"] == "hbm" and roof["unit"] == "GB/s" and roof["peak"] == 8000.0
     assert roof["frac"] == pytest.approx(roof["achieved"] / roof["peak"], rel=1e-2, abs=1e-4)
+    # algorithmic bytes: CSR A, all K rows of B once, C once in fp32
+    # (4(M+1) + nnz(4+s) + K*N*s + M*N*4 at M = K = 4096, nnz 32768, N 32, fp16)
+    assert roof["step_alg_bytes"] == 4 * 4097 + 32768 * 6 + 4096 * 32 * 2 + 4096 * 32 * 4
+    assert roof["alg_bytes_touched_per_launch"] <= roof["alg_bytes_per_launch"]
     # the same achieved rate against the copy bandwidth measured in the run
     assert 1000 < roof["copy_peak_gbs"] < roof["peak"]
     assert roof["frac_of_copy"] == pytest.approx(roof["achieved"] / roof["copy_peak_gbs"], rel=1e-2, abs=1e-4)

@@ -11,7 +11,7 @@ import pytest
 from conftest import ROOT
 
 DATA = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep.jsonl")
-HEADER = os.path.join(ROOT, "tilespmm_amd", "host", "policy_model.h")
+HEADER = os.path.join(ROOT, "tilespmm_amd", "host", "model.h")
 
 
 def header_tree(orc):
@@ -24,8 +24,10 @@ def header_tree(orc):
                                   "child3", "missing_left_mask"]):
             setattr(nodes[i], name, int(r[j]))
         nodes[i].cut, nodes[i].left_cut, nodes[i].right_cut = float(r[8]), float(r[9]), float(r[10])
-    r16 = int(re.search(r"tsp_policy_root_fp16 = (-?\d+)", text).group(1))
-    r32 = int(re.search(r"tsp_policy_root_tf32 = (-?\d+)", text).group(1))
+    r16 = int(re.search(r"predictparams_fp16\(.*?tilespmm_policy_select\(features, gamma, delta, (-?\d+)\)",
+                        text, re.S).group(1))
+    r32 = int(re.search(r"predictparams_tf32\(.*?tilespmm_policy_select\(features, gamma, delta, (-?\d+)\)",
+                        text, re.S).group(1))
     return nodes, r16, r32
 
 
@@ -46,6 +48,62 @@ def test_product_walk_matches_oracle_walk(tsp, orc):
     for f in feats:
         assert tsp.predict(f, 0) == orc.policy_select(f, nodes, cands, r16)
         assert tsp.predict(f, 1) == orc.policy_select(f, nodes, cands, r32)
+
+
+def _predictor(path):
+    import ctypes as C
+    lib = C.CDLL(path)
+    for name in ("tilespmm_predict_fp16", "tilespmm_predict_tf32"):
+        fn = getattr(lib, name)
+        fn.restype = None
+        fn.argtypes = [C.POINTER(C.c_double), C.POINTER(C.c_float), C.POINTER(C.c_float)]
+
+    def predict(f, prec):
+        f = np.ascontiguousarray(f, dtype=np.float64)
+        g, d = C.c_float(), C.c_float()
+        fn = lib.tilespmm_predict_fp16 if prec == 0 else lib.tilespmm_predict_tf32
+        fn(f.ctypes.data_as(C.POINTER(C.c_double)), C.byref(g), C.byref(d))
+        return np.float32(g.value), np.float32(d.value)
+    return predict
+
+
+REF_SRC = "/root/reference/src"
+
+
+def test_table_is_a_model_so_drop_in(tsp):
+    """The retrained table is written in the reference's model.h format: the
+    reference's own src/ml_predict.c, built against it (oracle/Makefile,
+    target _ref/model_mi355x.so), predicts exactly what this build's
+    CPU-only lib/model.so and the host library predict -- on the reference's
+    golden feature vectors, the sweep's features and perturbed ones, NaN
+    features included.  The reference's own table picks differently, so the
+    build really used the retrained one."""
+    import subprocess
+    if not os.path.exists(os.path.join(REF_SRC, "ml_predict.c")):
+        pytest.skip("reference checkout not mounted: src/ml_predict.c is needed to build the drop-in check")
+    r = subprocess.run(["make", "-C", os.path.join(ROOT, "oracle"), "_ref/model_mi355x.so", "_ref/model.so"],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    ref_built = _predictor(os.path.join(ROOT, "oracle", "_ref", "model_mi355x.so"))
+    ours = _predictor(os.path.join(ROOT, "tilespmm_amd", "lib", "model.so"))
+    ref_table = _predictor(os.path.join(ROOT, "oracle", "_ref", "model.so"))
+    gold = json.load(open(os.path.join(ROOT, "tests", "golden", "policy_golden.json")))["vectors"]
+    feats = [np.array(v["f"], dtype=np.float64) for v in gold] + [np.array(r["features"]) for r in records()]
+    rng = np.random.default_rng(5)
+    for f in list(feats[:400]):
+        g = f.copy()
+        g[2 + rng.integers(9)] *= rng.uniform(0.3, 3.0)
+        feats.append(g)
+        h = f.copy()
+        h[2 + rng.integers(9)] = np.nan
+        feats.append(h)
+    differs = 0
+    for f in feats:
+        for prec in (0, 1):
+            a = ref_built(f, prec)
+            assert a == ours(f, prec) == tsp.predict(f, prec), (f, prec)
+            differs += a != ref_table(f, prec)
+    assert differs > 0
 
 
 def test_policy_against_exhaustive_tuning(tsp):

@@ -2,7 +2,8 @@
 against the allocating one (tsp_tiles_pack_device), through the C ABI: the
 same vptr and packed values bit for bit, on two calls in a row (the second on
 a smaller input, so stale scratch from the first would show), plus its
-refusals (no room for the values, more tiles than its scratch covers)."""
+refusals (no room for the values, more tiles than its scratch covers, and
+-- for both entry points -- more packed values than the int offsets hold)."""
 import ctypes as C
 import sys
 
@@ -86,7 +87,7 @@ def test_pack_noalloc_matches_allocating_entry(tsp, prec):
                                                        out_v.p, C.byref(got_n), None)
                 assert st != 0 and got_n.value == nv
                 # more tiles than the scratch covers: refused on the host, nothing launched
-                big = (2 ** 18 - 1) * 2048 + 1
+                big = (2 ** 18 - 3) * 2048 + 1
                 assert hip.tsp_tiles_pack_device_noalloc(big, bm, bn, prec, d_val, d_bmp, out_p.p, nv + 4,
                                                          out_v.p, C.byref(got_n), None) != 0
             finally:
@@ -112,3 +113,42 @@ def test_pack_noalloc_empty(tsp):
     finally:
         out_v.free()
         out_p.free()
+
+
+def test_pack_refuses_counts_past_int_max(tsp):
+    """A bitmap whose set bits (plus the 4 padding elements) exceed INT_MAX:
+    both entry points return TSP_EINVAL with the 64-bit count, before any
+    int offset could wrap (and nothing is written to the values)."""
+    if not tsp.device_available():
+        pytest.fail("no gfx950 device: GPU tests need an MI355X")
+    hip = tsp.load()[0]
+    assert hip.tsp_device_init(0) == 0
+    bm, bn, prec = 64, 32, 0                      # 2048 slots = 32 bitmap words per tile
+    tilenum = (2 ** 31) // 2048 + 1               # every bit set: 2^31 + 2048 values
+    words = tilenum * (bm * bn // 64)
+    say(f"pack overflow guard: tilenum={tilenum}, {words * 8 >> 20} MiB of all-ones bitmap")
+    d_bmp, d_vp, d_pv = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    assert hip.tsp_malloc(C.byref(d_bmp), words * 8) == 0
+    try:
+        assert hip.tsp_memset(d_bmp, 0xFF, words * 8) == 0
+        assert hip.tsp_malloc(C.byref(d_vp), 4 * (tilenum + 1)) == 0
+        assert hip.tsp_malloc(C.byref(d_pv), 64) == 0
+        want = tilenum * bm * bn
+        n = C.c_longlong(-1)
+        pv, vp = C.c_void_p(), C.c_void_p()
+        st = hip.tsp_tiles_pack_device(tilenum, bm, bn, prec, d_bmp, d_bmp, C.byref(n), C.byref(pv), C.byref(vp),
+                                       None)
+        assert st != 0 and n.value == want and not pv.value and not vp.value
+        n.value = -1
+        st = hip.tsp_tiles_pack_device_noalloc(tilenum, bm, bn, prec, d_bmp, d_bmp, d_pv, 1 << 40, d_vp,
+                                               C.byref(n), None)
+        assert st != 0 and n.value == want
+        # one tile fewer than the limit needs: both accept the count query
+        ok = (2 ** 31 - 1 - 4) // 2048
+        n.value = -1
+        assert hip.tsp_tiles_pack_device(ok, bm, bn, prec, d_bmp, d_bmp, C.byref(n), None, None, None) == 0
+        assert n.value == ok * 2048
+    finally:
+        for p in (d_bmp, d_vp, d_pv):
+            if p.value:
+                hip.tsp_free(p)

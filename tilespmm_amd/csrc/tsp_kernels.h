@@ -108,5 +108,7 @@ int launch_gather(const void *table, size_t table_bytes, int row_bytes, int iter
 // Address of the allocation-free entry points' `scratch` array on the current
 // device (looked up once per device; tsp_device_init calls it).
 int scratch_init_current_device(int **ptr);
+// whether a packed-value total plus the 4 padding elements fits the int offsets
+bool pack_total_fits(long long total);
 
 }  // namespace tsp

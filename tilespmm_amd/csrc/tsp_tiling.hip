@@ -33,7 +33,9 @@
 
 // Scratch of the allocation-free packing entry point
 // (tsp_tiles_pack_device_noalloc): per-block partial sums of the per-tile
-// value counts, one int per kPackBlockTiles tiles, plus the total.  Every
+// value counts, one int per kPackBlockTiles tiles, plus the total, and the
+// 64-bit total in the last two ints (checked before any offset is formed,
+// so the int offsets never wrap).  Every
 // GPU the library runs on holds one copy for the life of the process; host
 // code uses only its per-device address from hipGetSymbolAddress
 // (tsp::scratch_init_current_device), never this name.
@@ -224,21 +226,43 @@ __global__ __launch_bounds__(kThreads) void pack_count_kernel(const unsigned lon
     if (threadIdx.x == 0) sums[blockIdx.x] = total;
 }
 
-__global__ __launch_bounds__(kThreads) void pack_block_scan_kernel(int *__restrict__ sums, int nb)
+// The block offsets are scanned in 64 bits; the int copies in sums[] are
+// only used (pass 3) when the 64-bit total stored in *total64 leaves room
+// for the padding within INT_MAX, which the host checks first.
+__global__ __launch_bounds__(kThreads) void pack_block_scan_kernel(int *__restrict__ sums, int nb,
+                                                                   long long *__restrict__ total64)
 {
-    using BS = rocprim::block_scan<int, kThreads>;
+    using BS = rocprim::block_scan<long long, kThreads>;
     __shared__ typename BS::storage_type st;
-    int carry = 0;
+    long long carry = 0;
     for (int base = 0; base < nb; base += kThreads) {
         const int i = base + (int)threadIdx.x;
-        const int v = i < nb ? sums[i] : 0;
-        int ex = 0, agg = 0;
-        BS().exclusive_scan(v, ex, 0, agg, st, rocprim::plus<int>());
-        if (i < nb) sums[i] = carry + ex;
+        const long long v = i < nb ? sums[i] : 0;
+        long long ex = 0, agg = 0;
+        BS().exclusive_scan(v, ex, 0ll, agg, st, rocprim::plus<long long>());
+        if (i < nb) sums[i] = (int)min(carry + ex, (long long)INT_MAX);
         carry += agg;
         __syncthreads();
     }
-    if (threadIdx.x == 0) sums[nb] = carry;
+    if (threadIdx.x == 0) {
+        sums[nb] = (int)min(carry, (long long)INT_MAX);
+        *total64 = carry;
+    }
+}
+
+// 64-bit sum of the per-tile value counts (the allocating entry point's
+// overflow check before its int scan)
+__global__ __launch_bounds__(kThreads) void count_total_kernel(const int *__restrict__ cnt, int n,
+                                                               unsigned long long *__restrict__ total)
+{
+    using BR = rocprim::block_reduce<long long, kThreads>;
+    __shared__ typename BR::storage_type st;
+    long long s = 0;
+    for (long long i = (long long)blockIdx.x * kThreads + threadIdx.x; i < n; i += (long long)gridDim.x * kThreads)
+        s += cnt[i];
+    long long b = 0;
+    BR().reduce(s, b, st, rocprim::plus<long long>());
+    if (threadIdx.x == 0) atomicAdd(total, (unsigned long long)b);
 }
 
 __global__ __launch_bounds__(kThreads) void pack_offsets_kernel(int *__restrict__ vptr, int tilenum,
@@ -433,6 +457,8 @@ int tile_create_device(tsp_dev_tiles *out, int rows, int colA, long long nnz, co
 
 namespace tsp {
 
+bool pack_total_fits(long long total) { return total >= 0 && total <= (long long)INT_MAX - 4; }
+
 // Per-device address of `scratch`, looked up with the device current (each
 // GPU holds its own copy at its own address).
 constexpr int kScratchDevices = 64;
@@ -475,21 +501,22 @@ int tsp_tiles_pack_device_noalloc(int tilenum, int bm, int bn, int prec, const v
     int *sums = nullptr;
     int st = tsp::scratch_init_current_device(&sums);
     if (st) return st;
+    long long *total64 = (long long *)(sums + kScratchInts - 2);
     hipStream_t s = (hipStream_t)stream;
     const int words = (bm * bn + 63) / 64;
     const int nb = (int)(((long long)tilenum + kPackBlockTiles - 1) / kPackBlockTiles);
     if (nb > 0) pack_count_kernel<<<nb, kThreads, 0, s>>>(d_bitmap, tilenum, words, d_vptr, sums);
-    pack_block_scan_kernel<<<1, kThreads, 0, s>>>(sums, nb);
-    if (nb > 0) pack_offsets_kernel<<<nb, kThreads, 0, s>>>(d_vptr, tilenum, sums);
+    pack_block_scan_kernel<<<1, kThreads, 0, s>>>(sums, nb, total64);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    int total = 0;
-    if ((e = hipMemcpyAsync(&total, sums + nb, sizeof(int), hipMemcpyDeviceToHost, s)) != hipSuccess) return (int)e;
+    long long total = 0;
+    if ((e = hipMemcpyAsync(&total, total64, sizeof total, hipMemcpyDeviceToHost, s)) != hipSuccess) return (int)e;
     if ((e = hipStreamSynchronize(s)) != hipSuccess) return (int)e;
     *nvals = total;
     // the values plus 4 elements of zero padding (the kernels' packed loads
-    // may read past the last value) must fit
-    if ((long long)total + 4 > pval_capacity) return TSP_EINVAL;
+    // may read past the last value) must fit, and the offsets are ints
+    if (!tsp::pack_total_fits(total) || total + 4 > pval_capacity) return TSP_EINVAL;
+    if (nb > 0) pack_offsets_kernel<<<nb, kThreads, 0, s>>>(d_vptr, tilenum, sums);
     if (prec == TSP_PREC_FP16) {
         pack_tail_kernel<uint16_t><<<1, 64, 0, s>>>(d_vptr, tilenum, sums, nb, (uint16_t *)d_pval, pval_capacity, 4);
         if (tilenum > 0)
@@ -528,7 +555,10 @@ int tsp_tiles_pack_device(int tilenum, int bm, int bn, int prec, const void *d_v
     const int words = (bm * bn + 63) / 64;
     int *vptr = nullptr, *cnt = nullptr;
     Scratch tmp;
-    TCHK(hipMalloc(&cnt, sizeof(int) * ((size_t)tilenum + 1)));
+    // the counts, then (8-byte aligned) their 64-bit total
+    const size_t cnt_bytes = (sizeof(int) * ((size_t)tilenum + 1) + 7) / 8 * 8;
+    TCHK(hipMalloc(&cnt, cnt_bytes + sizeof(unsigned long long)));
+    unsigned long long *total64 = (unsigned long long *)((char *)cnt + cnt_bytes);
     struct FreeCnt {
         int *p;
         ~FreeCnt() { (void)hipFree(p); }
@@ -540,7 +570,19 @@ int tsp_tiles_pack_device(int tilenum, int bm, int bn, int prec, const void *d_v
         return st;
     };
     if ((e = hipMemsetAsync(cnt + tilenum, 0, sizeof(int), s)) != hipSuccess) return fail((int)e);
-    if (tilenum > 0) popcount_kernel<<<nblocks(tilenum), kThreads, 0, s>>>(d_bitmap, tilenum, words, cnt);
+    if ((e = hipMemsetAsync(total64, 0, sizeof *total64, s)) != hipSuccess) return fail((int)e);
+    if (tilenum > 0) {
+        popcount_kernel<<<nblocks(tilenum), kThreads, 0, s>>>(d_bitmap, tilenum, words, cnt);
+        count_total_kernel<<<min(1024u, nblocks(tilenum)), kThreads, 0, s>>>(cnt, tilenum, total64);
+    }
+    unsigned long long total_u = 0;
+    if ((e = hipMemcpyAsync(&total_u, total64, sizeof total_u, hipMemcpyDeviceToHost, s)) != hipSuccess)
+        return fail((int)e);
+    if ((e = hipStreamSynchronize(s)) != hipSuccess) return fail((int)e);
+    *nvals = (long long)total_u;
+    // the int scan below and the kernels' int offsets need the values plus
+    // the padding to stay within INT_MAX
+    if (!tsp::pack_total_fits((long long)total_u)) return fail(TSP_EINVAL);
     size_t need = 0;
     if ((e = rocprim::exclusive_scan(nullptr, need, cnt, vptr, 0, (size_t)tilenum + 1, rocprim::plus<int>(), s)) !=
         hipSuccess)
@@ -549,11 +591,7 @@ int tsp_tiles_pack_device(int tilenum, int bm, int bn, int prec, const void *d_v
     if ((e = rocprim::exclusive_scan(tmp.p, need, cnt, vptr, 0, (size_t)tilenum + 1, rocprim::plus<int>(), s)) !=
         hipSuccess)
         return fail((int)e);
-    int total = 0;   // <= slots of all tiles; a class's nnz bounds it below 2^31
-    if ((e = hipMemcpyAsync(&total, vptr + tilenum, sizeof(int), hipMemcpyDeviceToHost, s)) != hipSuccess)
-        return fail((int)e);
-    if ((e = hipStreamSynchronize(s)) != hipSuccess) return fail((int)e);
-    *nvals = total;
+    const int total = (int)total_u;
     if (!d_pval) return fail(TSP_OK);
     // 4 elements of zero padding: the kernels' packed loads may read past the last value
     const size_t vs = prec == TSP_PREC_FP16 ? 2 : 4;

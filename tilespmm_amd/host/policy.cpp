@@ -9,70 +9,18 @@
 // Candidate action space: three fixed-group actions, a grid of ten gammas x
 // six deltas, and three extra pairs -- 66 actions in the same order as the
 // reference's candidate list (src/model.h:14-38), so tables trained for
-// either build index the same (gamma, delta) pairs.
+// either build index the same (gamma, delta) pairs.  The table and its walk
+// live in the generated model.h, which the reference's src/ml_predict.c
+// also builds against (lib/model.so, the CPU-only policy library).
 #include <math.h>
 #include <omp.h>
 
 #include <vector>
 
 #include "common.hpp"
-#include "policy_model.h"
-
-namespace {
-
-struct Cands {
-    float g[66], d[66];
-    int n = 0;
-    Cands()
-    {
-        auto add = [&](float gg, float dd) { g[n] = gg; d[n] = dd; ++n; };
-        add(0.0f, 1.5f);   // everything in 64-row tiles
-        add(5.0f, 0.0f);   // everything in 16-row tiles
-        add(5.0f, 3.0f);   // everything in 8-row tiles
-        const float gammas[10] = {1.0f, 1.4f, 1.8f, 2.0f, 2.4f, 2.8f, 3.0f, 3.4f, 3.8f, 4.0f};
-        const float deltas[6] = {1.0f, 1.2f, 1.4f, 1.5f, 1.8f, 2.0f};
-        for (float gg : gammas)
-            for (float dd : deltas) add(gg, dd);
-        add(2.5f, 1.0f);
-        add(2.5f, 1.2f);
-        add(3.5f, 1.0f);
-    }
-};
-
-const Cands &cands()
-{
-    static const Cands c;
-    return c;
-}
-
-void select(const double *f, int index, float *gamma, float *delta)
-{
-    while (index >= 0) {
-        const tsp_policy_node &n = tsp_policy_nodes[index];
-        float v = (float)f[n.feature + 2];
-        bool left = isnan(v) ? (n.missing_left_mask & 1) != 0 : v < n.cut;
-        if (left) {
-            if (n.left_feature < 0) index = n.child0;
-            else {
-                v = (float)f[n.left_feature + 2];
-                left = isnan(v) ? (n.missing_left_mask & 2) != 0 : v < n.left_cut;
-                index = left ? n.child0 : n.child1;
-            }
-        } else {
-            if (n.right_feature < 0) index = n.child2;
-            else {
-                v = (float)f[n.right_feature + 2];
-                left = isnan(v) ? (n.missing_left_mask & 4) != 0 : v < n.right_cut;
-                index = left ? n.child2 : n.child3;
-            }
-        }
-    }
-    const int a = -1 - index;
-    *gamma = cands().g[a];
-    *delta = cands().d[a];
-}
-
-}  // namespace
+// the retrained table, in the format of the reference's src/model.h
+// (tilespmm_shared_nodes, tilespmm_model_candidates, predictparams_*)
+#include "model.h"
 
 extern "C" int tsp_features_from_csr(int rows, int cols, long long nnz, const int *rowptr,
                                      double capability, int colB, double *f)
@@ -105,21 +53,21 @@ extern "C" int tsp_features_from_csr(int rows, int cols, long long nnz, const in
 
 extern "C" void tilespmm_predict_fp16(const double *f, float *gamma, float *delta)
 {
-    select(f, tsp_policy_root_fp16, gamma, delta);
+    predictparams_fp16(f, gamma, delta);
 }
 
 extern "C" void tilespmm_predict_tf32(const double *f, float *gamma, float *delta)
 {
-    select(f, tsp_policy_root_tf32, gamma, delta);
+    predictparams_tf32(f, gamma, delta);
 }
 
 // Candidate list access for tuning drivers.
 extern "C" int tsp_policy_candidates(float *gamma, float *delta)
 {
-    const Cands &c = cands();
-    for (int i = 0; i < c.n; ++i) {
-        if (gamma) gamma[i] = c.g[i];
-        if (delta) delta[i] = c.d[i];
+    constexpr int n = (int)(sizeof tilespmm_model_candidates / sizeof tilespmm_model_candidates[0]);
+    for (int i = 0; i < n; ++i) {
+        if (gamma) gamma[i] = tilespmm_model_candidates[i][0];
+        if (delta) delta[i] = tilespmm_model_candidates[i][1];
     }
-    return c.n;
+    return n;
 }

@@ -12,9 +12,13 @@ tool rebuilds the policy for gfx950:
   fit    -- fit a regret-minimising decision tree on the sweep results: every
             leaf holds the candidate with the lowest mean normalised time
             (time / best time of that matrix) over its training matrices.  The
-            tree is written as tilespmm_amd/host/policy_model.h in the node
-            layout of the reference's tilespmm_policy_node (binary nodes:
-            left_feature = right_feature = -1).
+            tree is written as tilespmm_amd/host/model.h in the format of
+            the reference's src/model.h (tilespmm_policy_node table,
+            candidates, tilespmm_policy_select, predictparams_*; binary
+            nodes: left_feature = right_feature = -1), so the reference's
+            src/ml_predict.c builds against it into a drop-in lib/model.so.
+  export -- rewrite model.h (or --out FILE) from the tree the last fit
+            stored beside it (model_tree.json), without refitting.
   check  -- report, per swept matrix, the policy's pick vs the exhaustive
             optimum (the "checked against exhaustive tuning" figure).
   thsweep -- per matrix / precision / colB and active row class, the class
@@ -308,36 +312,101 @@ def fit_tree(recs, max_depth, min_leaf):
     return root, nodes
 
 
+def policy_candidates_f32():
+    """The 66 (gamma, delta) actions in the reference's order
+    (src/model.h:14-38): three fixed-group actions, ten gammas x six deltas,
+    and three extra pairs -- built by rule, as float32."""
+    c = [(0.0, 1.5), (5.0, 0.0), (5.0, 3.0)]
+    c += [(g, d) for g in (1.0, 1.4, 1.8, 2.0, 2.4, 2.8, 3.0, 3.4, 3.8, 4.0) for d in (1.0, 1.2, 1.4, 1.5, 1.8, 2.0)]
+    c += [(2.5, 1.0), (2.5, 1.2), (3.5, 1.0)]
+    return [(np.float32(g), np.float32(d)) for g, d in c]
+
+
+def _cf(x):
+    """A float32 as a C literal that reads back to the same float."""
+    return f"{np.float32(x).item()!r}f"
+
+
+# The walk over the 4-way node format (one node may test two adjacent
+# levels: child0/child1 under the left branch, child2/child3 under the
+# right; a branch with feature -1 goes straight to child0 / child2), as the
+# reference's policy ABI defines it; NaN features follow missing_left_mask.
+_WALK = """static inline void tilespmm_policy_select(const double *features, float *gamma, float *delta, int index)
+{
+    while (index >= 0) {
+        const tilespmm_policy_node *n = &tilespmm_shared_nodes[index];
+        float v = (float)features[n->feature + 2];
+        const int go_left = isnan(v) ? (n->missing_left_mask & 1) != 0 : v < n->cut;
+        const int sub = go_left ? n->left_feature : n->right_feature;
+        const float sub_cut = go_left ? n->left_cut : n->right_cut;
+        const int lo = go_left ? n->child0 : n->child2;
+        const int hi = go_left ? n->child1 : n->child3;
+        if (sub < 0) {
+            index = lo;
+        } else {
+            v = (float)features[sub + 2];
+            const int bit = go_left ? 2 : 4;
+            index = (isnan(v) ? (n->missing_left_mask & bit) != 0 : v < sub_cut) ? lo : hi;
+        }
+    }
+    const int action = -1 - index;
+    *gamma = tilespmm_model_candidates[action][0];
+    *delta = tilespmm_model_candidates[action][1];
+}"""
+
+
 def export_header(path, roots, nodes_all, note):
+    """Writes the policy table in the reference's model.h format (type
+    tilespmm_policy_node, tables tilespmm_model_candidates and
+    tilespmm_shared_nodes, tilespmm_policy_select, predictparams_fp16/_tf32;
+    src/model.h:1-40,3463-3499), so the reference's own src/ml_predict.c
+    builds against it unchanged and lib/model.so stays a drop-in."""
     lines = [
-        "// policy_model.h -- (gamma, delta) policy table for MI355X.",
-        "//",
-        "// Node layout and walk semantics are those of the reference's exported",
-        "// decision tree (tilespmm_policy_node, src/model.h:9-13; walk",
-        "// src/model.h:3463-3491) so that a retrained table drops into the same",
-        "// tilespmm_predict_* C ABI.  Action a selects candidate a of the list built",
-        "// by policy_candidates(); a root or child < 0 is a leaf holding -1 - action.",
-        "//",
-        f"// GENERATED by tilespmm_amd/policy_tune.py fit ({note}).",
-        "#pragma once",
-        "",
-        "struct tsp_policy_node {",
+        "/* model.h -- (gamma, delta) split policy retrained on MI355X (gfx950).",
+        " *",
+        f" * GENERATED by tilespmm_amd/policy_tune.py fit ({note}).",
+        " *",
+        " * Same layout as the policy table the reference's src/ml_predict.c",
+        " * includes: 11 input features [0, 0, rows, cols, nnz, sparsity,",
+        " * avg_row_nnz, max_row_nnz, min_row_nnz, capability, colB], nodes that",
+        " * compare (float)features[feature + 2] < cut, leaves -1 - action, and",
+        " * 66 actions.  Binary nodes here: left_feature = right_feature = -1. */",
+        "#ifndef TILESPMM_MODEL_H",
+        "#define TILESPMM_MODEL_H",
+        "#include <math.h>",
+        "#define TILESPMM_MODEL_FEATURE_COUNT 11",
+        "typedef struct {",
         "    int feature, left_feature, right_feature;",
         "    int child0, child1, child2, child3, missing_left_mask;",
         "    float cut, left_cut, right_cut;",
-        "};",
-        "",
-        "static const tsp_policy_node tsp_policy_nodes[] = {",
+        "} tilespmm_policy_node;",
+        "static const float tilespmm_model_candidates[66][2] = {",
     ]
+    for g, d in policy_candidates_f32():
+        lines.append(f"    {{{_cf(g)}, {_cf(d)}}},")
+    lines += ["};", "static const tilespmm_policy_node tilespmm_shared_nodes[] = {"]
     for n in nodes_all:
         lines.append(f"    {{{n['feature']}, -1, -1, {n['left']}, -1, {n['right']}, -1, 1, "
-                     f"{np.float32(n['cut']).item()!r}f, 0.0f, 0.0f}},")
+                     f"{_cf(n['cut'])}, 0.0f, 0.0f}},")
     if not nodes_all:
         lines.append("    {4, -1, -1, -1, -1, -1, -1, 0, 0.0f, 0.0f, 0.0f},")
-    lines += ["};", "",
-              f"static const int tsp_policy_root_fp16 = {roots[0]};",
-              f"static const int tsp_policy_root_tf32 = {roots[1]};", ""]
+    lines += ["};", _WALK,
+              "static inline void predictparams_fp16(const double *features, float *gamma, float *delta)",
+              "{", f"    tilespmm_policy_select(features, gamma, delta, {roots[0]});", "}",
+              "static inline void predictparams_tf32(const double *features, float *gamma, float *delta)",
+              "{", f"    tilespmm_policy_select(features, gamma, delta, {roots[1]});", "}",
+              "#endif /* TILESPMM_MODEL_H */", ""]
     open(path, "w").write("\n".join(lines))
+    # the tree beside it, so `export` can rewrite the table without refitting
+    with open(os.path.splitext(path)[0] + "_tree.json", "w") as fh:
+        json.dump({"roots": roots, "nodes": nodes_all, "note": note}, fh, indent=1)
+
+
+def cmd_export(args):
+    """Rewrites the header from the tree the last fit stored beside it."""
+    tree = json.load(open(os.path.splitext(args.header)[0] + "_tree.json"))
+    export_header(args.out or args.header, tree["roots"], tree["nodes"], tree["note"])
+    print(f"wrote {args.out or args.header}: {len(tree['nodes'])} nodes, roots {tree['roots']}")
 
 
 def cmd_fit(args):
@@ -594,15 +663,21 @@ def main():
     s.add_argument("--out", required=True)
     f = sub.add_parser("fit")
     f.add_argument("--inp", required=True)
-    f.add_argument("--header", default=os.path.join(HERE, "host", "policy_model.h"))
+    f.add_argument("--header", default=os.path.join(HERE, "host", "model.h"))
     f.add_argument("--depth", type=int, default=4)
     f.add_argument("--min-leaf", type=int, default=3)
     f.add_argument("--lomo", action="store_true", help="also report leave-one-matrix-out regret")
     c = sub.add_parser("check")
     c.add_argument("--inp", required=True)
+    e = sub.add_parser("export")
+    e.add_argument("--header", default=os.path.join(HERE, "host", "model.h"),
+                   help="the fitted table whose model_tree.json is read")
+    e.add_argument("--out", default=None, help="write here instead (e.g. a reference checkout's src/model.h)")
+    e.add_argument("--reference", action="store_true",
+                   help="the reference's src/model.h format (the only format this build writes)")
     args = ap.parse_args()
     {"sweep": cmd_sweep, "fit": cmd_fit, "check": cmd_check, "thsweep": cmd_thsweep,
-     "thfit": cmd_thfit}[args.cmd](args)
+     "thfit": cmd_thfit, "export": cmd_export}[args.cmd](args)
 
 
 if __name__ == "__main__":
