@@ -258,6 +258,9 @@ def apply_pins(plan, args):
     for bm, li in zip((64, 16, 8), args.lane_idx or ()):
         if li:
             plan.set_lane_indices(bm, li - 1)
+    for bm, pr in zip((64, 16, 8), args.pairs or ()):
+        if pr:
+            plan.set_pairs(bm, pr - 1)
     lags = args.panel_lag or (2, 2, 2)
     for bm, pr, lg in zip((64, 16, 8), args.panels or (), lags):
         if pr:
@@ -276,7 +279,7 @@ def variant_of(c):
 
 def pins_of(plan, th, cls):
     """The bench flags that replay this plan's tuned configuration."""
-    f, o, t, w, s, p, li, pr, lg = [], [], [], [], [], [], [], [], []
+    f, o, t, w, s, p, li, pr, lg, tp = [], [], [], [], [], [], [], [], [], []
     for bm in (64, 16, 8):
         c = cls.get(bm)
         f.append({"dense": 1, "packed": 2}[c["format"]] if c else 0)
@@ -288,10 +291,11 @@ def pins_of(plan, th, cls):
         li.append(c["lane_indices"] + 1 if c else 0)
         pr.append(c["panel_rows"] if c else 0)
         lg.append(c["panel_lag"] if c else 0)
+        tp.append(c["tile_pairs"] + 1 if c else 0)
     j = lambda v: ",".join(str(x) for x in v)
     return (f"--no-tune --th {j(th)} --format {j(f)} --order {j(o)} --tpw {j(t)} --width {j(w)} "
-            f"--stages {j(s)} --place {j(p)} --lane-idx {j(li)} --panels {j(pr)} --panel-lag {j(lg)} "
-            f"--hot-bytes {plan.get_hot_rows()[1]}")
+            f"--stages {j(s)} --place {j(p)} --lane-idx {j(li)} --pairs {j(tp)} --panels {j(pr)} "
+            f"--panel-lag {j(lg)} --hot-bytes {plan.get_hot_rows()[1]}")
 
 
 def measure(tsp, hip, config, prec, colB, args, headline):
@@ -381,6 +385,7 @@ def measure(tsp, hip, config, prec, colB, args, headline):
                    "order": {0: "side-by-side", 1: "side-by-side", 2: "chunk-major"}[v[3]],
                    "tasks_per_wave": max(1, v[2]), "stages": max(1, v[1]), "chunk_width": w,
                    "lane_indices": max(0, plan.get_lane_indices(bm)),
+                   "tile_pairs": max(0, plan.get_pairs(bm)),
                    "placement": {0: "contiguous", 1: "interleaved", 2: "chunk-xcd"}.get(plan.get_placement(bm), "?"),
                    "panel_rows": plan.get_panels(bm)[0], "panel_lag": plan.get_panels(bm)[1],
                    "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9, "alg_bytes_touched": b_touched,
@@ -391,13 +396,14 @@ def measure(tsp, hip, config, prec, colB, args, headline):
     step_bytes = alg_bytes(A.rows, A.nnz, s, A.cols, colB, s)
     step_gbs = step_bytes / (ms * 1e-3) / 1e9
 
-    # the dominant kernel's instantiation spmm_kernel<BM, W, PREC, S, PK, LI, SY>;
+    # the dominant kernel's instantiation spmm_kernel<BM, W, PREC, S, PK, LI, SY, PR>;
     # the profiled HBM traffic applies only to the same instantiation and hot
     # rows (plans launch tf32 on operands they rounded once: kernel precision
     # code 2)
     tf = lambda b: "true" if b else "false"
     kname = (f"spmm_kernel<{dom}, {dk['chunk_width']}, {2 if prec == 1 else 0}, {dk['stages']}, "
-             f"{tf(dk['format'] == 'packed')}, {tf(dk['lane_indices'])}, {tf(dk['panel_rows'])}>")
+             f"{tf(dk['format'] == 'packed')}, {tf(dk['lane_indices'])}, {tf(dk['panel_rows'])}, "
+             f"{tf(dk['tile_pairs'])}>")
     traffic, traffic_note = None, "no profile of this workload in profiles/"
     prof = os.path.join(ROOT, "profiles", f"traffic_config{config}_{pname}_{colB}.json")
     if os.path.exists(prof):
@@ -514,6 +520,70 @@ def cpu_baseline(A, B, colB, prec):
                       f"run ({first * 1e3:.0f} ms), {tm * 1e3:.1f} ms per run"}
 
 
+def hub_split(tsp, hip, args):
+    """The hub-row experiment: split A by column into the entries whose
+    columns are the H most gathered (distinct (8-row block, column) pairs)
+    and the rest, and time three plans -- the whole matrix, the hub part and
+    the cold part -- each tuned as the headline is, with the policy split of
+    the whole matrix.  If L2 reuse of the hub rows were what bounds the
+    kernel, the hub part (every gather from an L2-sized set of rows) would
+    run far faster per tile and hub + cold would beat the whole; a real
+    two-phase kernel would also pay a read-modify-write of C.  One JSON line
+    per H, after lines for each plan.  Between the timed launches of the
+    three plans a 16-byte copy kernel marks the boundary (for profilers)."""
+    import ctypes as C
+    prec = {"fp16": 0, "tf32": 1, None: -1}[args.prec]
+    A, B, colB, cbp = tsp.gen_config(args.config, prec, args.colB)
+    prec = A.prec
+    g, d = tsp.predict(tsp.features(A, 9.5, colB), prec)
+    rows = np.repeat(np.arange(A.rows, dtype=np.int64), np.diff(A.rowptr))
+    pairs = np.unique((rows // 8) * A.cols + A.colidx)
+    cnt = np.bincount((pairs % A.cols).astype(np.int64), minlength=A.cols)
+    del pairs
+    order = np.argsort(-cnt, kind="stable")
+    mark_src, mark_dst = C.c_void_p(), C.c_void_p()
+    assert hip.tsp_malloc(C.byref(mark_src), 256) == 0 and hip.tsp_malloc(C.byref(mark_dst), 256) == 0
+
+    def part(mask):
+        rp = np.concatenate([[0], np.cumsum(np.bincount(rows[mask], minlength=A.rows))]).astype(np.int32)
+        return tsp.Csr(A.rows, A.cols, rp, A.colidx[mask], A.val[mask], prec)
+
+    def plan_of(Ap):
+        plan = tsp.Plan.from_csr(tsp.matrix_split(Ap, g, d), Ap.rows, Ap.cols, cbp, prec, B)
+        th, _, _ = plan.tune(True)
+        plan.warmup(300)
+        plan.run(zero_c=True)
+        return plan, th
+
+    def timed(name, plan, th, Ap):
+        hip.tsp_copy_kernel(mark_dst, mark_src, 16, None)
+        hip.tsp_device_sync()
+        ms = plan.time(args.steps)
+        rec = {"hub_split": name, "nnz": Ap.nnz, "tiles": [plan.tilenum(bm) for bm in (64, 16, 8)],
+               "ms_per_step": round(ms, 5), "tiles_per_us": round(sum(plan.tilenum(bm) for bm in (64, 16, 8))
+                                                                    / (ms * 1e3), 1),
+               "th": list(th), "hot_rows": plan.get_hot_rows()[0]}
+        print(json.dumps(rec), flush=True)
+        return ms
+
+    for H in args.hub_split:
+        hub = np.zeros(A.cols, bool)
+        hub[order[:H]] = True
+        m = hub[A.colidx]
+        parts = [("whole", A), ("hub", part(m)), ("cold", part(~m))]
+        plans = [plan_of(Ap) for _, Ap in parts]
+        ms = [timed(f"{n} H={H}", p, th, Ap) for (n, Ap), (p, th) in zip(parts, plans)]
+        for p, _ in plans:
+            p.close()
+        print(json.dumps({"hub_split_summary": H, "workload": NAMES[args.config], "prec": prec, "colB": colB,
+                          "hub_share_of_gathers": round(float(cnt[order[:H]].sum() / cnt.sum()), 4),
+                          "hub_share_of_nnz": round(float(m.mean()), 4), "whole_ms": round(ms[0], 5),
+                          "hub_ms": round(ms[1], 5), "cold_ms": round(ms[2], 5),
+                          "hub_plus_cold_ms": round(ms[1] + ms[2], 5)}), flush=True)
+    hip.tsp_free(mark_src)
+    hip.tsp_free(mark_dst)
+
+
 TARGETS = {3: "T3", 5: "T5"}
 
 
@@ -548,6 +618,8 @@ def main():
                          "chunk per XCD group, 0 keep)")
     ap.add_argument("--lane-idx", type=ints3, default=None,
                     help="pin lane-loaded column indices per class 64,16,8 (1 off, 2 on, 0 keep)")
+    ap.add_argument("--pairs", type=ints3, default=None,
+                    help="pin tile pairs per class 64,16,8 (1 off, 2 on, 0 keep; fp16 8-/16-row classes)")
     ap.add_argument("--panels", type=ints3, default=None,
                     help="pin the panel-synchronised sweep per class: B rows per panel (0 = off)")
     ap.add_argument("--panel-lag", type=ints3, default=None,
@@ -570,6 +642,8 @@ def main():
                     help="only run the random row-gather probe (gather bandwidth ceiling)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run the plain copy kernel on this many bytes (counter calibration)")
+    ap.add_argument("--hub-split", type=lambda v: [int(x) for x in v.split(",")], default=None,
+                    help="only run the hub-row experiment for these hub set sizes (columns), e.g. 16384")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -585,6 +659,9 @@ def main():
         return
     if args.copy_bytes:
         copy_calibration(hip, args.copy_bytes, args.steps)
+        return
+    if args.hub_split:
+        hub_split(tsp, hip, args)
         return
 
     prec = {"fp16": 0, "tf32": 1, None: -1}[args.prec]
@@ -618,7 +695,8 @@ def main():
     targets = {}
     for cfg in [int(x) for x in args.targets.split(",") if x.strip()]:
         targ = argparse.Namespace(**vars(args))
-        for k in ("th", "format", "order", "tpw", "width", "stages", "place", "lane_idx", "panels", "panel_lag", "hot_bytes",
+        for k in ("th", "format", "order", "tpw", "width", "stages", "place", "lane_idx", "pairs", "panels", "panel_lag",
+                  "hot_bytes",
                   "gamma",
                   "delta"):
             setattr(targ, k, None)

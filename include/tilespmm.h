@@ -215,6 +215,11 @@ int tsp_plan_get_variant(tsp_plan *plan, int bm, int *w, int *stages, int *tasks
  * get returns -1 on a bad argument. */
 int tsp_plan_set_lane_indices(tsp_plan *plan, int bm, int on);
 int tsp_plan_get_lane_indices(tsp_plan *plan, int bm);
+/* Tile pairs (TSP_LAUNCH_TILE_PAIRS) for one class: 1 on, 0 off; fp16 8- and
+ * 16-row classes only, with 64- or 128-column chunks (a launch with another
+ * width fails).  tsp_plan_tune picks.  No counterpart in the reference. */
+int tsp_plan_set_pairs(tsp_plan *plan, int bm, int on);
+int tsp_plan_get_pairs(tsp_plan *plan, int bm);
 int tsp_plan_set_placement(tsp_plan *plan, int bm, int placement);
 int tsp_plan_get_placement(tsp_plan *plan, int bm);
 /* Panel-synchronised sweep (tsp_spmm_launch_panels) for one class on the

@@ -202,6 +202,17 @@ int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const 
  * per class (faster on the gather-bound RMAT and power-law fp16 classes,
  * slower on banded and block-sparse ones). */
 #define TSP_LAUNCH_LANE_INDICES 2
+/* TSP_LAUNCH_TILE_PAIRS (fp16 8- and 16-row tiles, chunk width w 64 or 128,
+ * given explicitly): each wave multiplies two consecutive tiles of a task at
+ * a time, as one 16 x 32 tile on v_mfma_f32_16x16x32_f16 (the K = 16 form
+ * runs at half the fp16 rate); a task with an odd tile count ends with a
+ * single tile.  Same products, accumulated in another order (fp32).
+ * tsp_pairs_supported(bm, prec, w) says whether a launch with chunk width w
+ * may pass it (a launch given w <= 0 checks its default width).  No
+ * counterpart in the reference (its 16-row kernel covers both k-halves of
+ * one 16 x 16 tile with two m16n8k16 steps). */
+#define TSP_LAUNCH_TILE_PAIRS 8
+int tsp_pairs_supported(int bm, int prec, int w);
 int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
                        const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,
                        const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,

@@ -97,6 +97,10 @@ def test_error_strings_and_arg_checks(tsp):
     assert hip.tsp_graph_launch(None, None) == 1001
     assert hip.tsp_graph_destroy(None) == 0
     _, host = tsp.load()
+    # tile pairs: fp16 8- and 16-row tiles at 64- or 128-column chunks only
+    assert [hip.tsp_pairs_supported(bm, pr, w) for bm, pr, w in
+            ((16, 0, 64), (8, 0, 128), (16, 1, 64), (64, 0, 64), (8, 0, 32), (16, 0, 256))] == [1, 1, 0, 0, 0, 0]
+    assert host.tsp_plan_set_pairs(None, 16, 1) == 1001 and host.tsp_plan_get_pairs(None, 16) == -1
     assert host.tsp_plan_graph_capture(None, 1) == 1001
     assert host.tsp_plan_graph_run(None, 1) == 1001
     assert host.tsp_plan_graph_time(None, 1, None) == 1001

@@ -88,3 +88,21 @@ def test_bench_json_line(tsp):
     assert t["frac"] > 0 and t["kernel"].startswith("spmm_kernel<")
     assert t["cold_cache"]["reps"] == 3 and t["cold_cache"]["ms_per_step"] > 0
     assert d["replay"].startswith("--no-tune --th ")
+
+
+@pytest.mark.gpu
+def test_bench_hub_split(tsp):
+    """bench.py --hub-split: the whole matrix, its hub part and its cold part
+    as three tuned plans; one line per plan, then the summary."""
+    if not tsp.device_available():
+        pytest.fail("no gfx950 device: GPU tests need an MI355X")
+    print("bench.py --config 1 --hub-split 256 --steps 10", flush=True)
+    r = subprocess.run([sys.executable, "-u", BENCH, "--config", "1", "--hub-split", "256", "--steps", "10"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = [json.loads(l) for l in r.stdout.splitlines() if l.strip()]
+    assert [l.get("hub_split", "summary").split()[0] for l in lines] == ["whole", "hub", "cold", "summary"]
+    s = lines[-1]
+    assert s["hub_split_summary"] == 256 and 0 < s["hub_share_of_nnz"] < 1
+    assert lines[1]["nnz"] + lines[2]["nnz"] == lines[0]["nnz"] == 32768
+    assert s["hub_plus_cold_ms"] == pytest.approx(s["hub_ms"] + s["cold_ms"], abs=2e-5)

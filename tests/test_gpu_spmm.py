@@ -152,6 +152,78 @@ def test_every_kernel_variant(gpu, orc, prec):
             plan.close()
 
 
+def test_tile_pairs(gpu, orc):
+    """Tile pairs (two tiles of a task per K = 32 MFMA; fp16 8- and 16-row
+    classes, 64- and 128-column chunks): every depth, format, index mode,
+    tasks per wave, order and placement gives the oracle's result, with
+    thresholds that leave tasks of odd and even tile counts (the last unit of
+    an odd task holds one tile) and split tasks; the panel sweep with pairs
+    is bit-identical to the unsynchronised pair launch.  tf32 plans and other
+    chunk widths refuse pairs."""
+    tsp = gpu
+    prec = 0
+    rng = np.random.default_rng(91)
+    A = random_matrix(tsp, rng, 611, 509, 45, prec, heavy_rows=4)
+    colB = 128
+    B, cbp = random_b(tsp, rng, A.cols, colB, prec)
+    Cref, Cabs = reference(orc, A, B, colB)
+    for g, d, bm in [(5.0, 0.0, 16), (5.0, 3.0, 8)]:
+        subs = tsp.matrix_split(A, g, d)
+        tiles = [tsp.tile_create(s, A.cols, b, prec) for s, b in zip(subs, (64, 16, 8))]
+        plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
+        try:
+            for th in ((3, 3, 3), (8, 8, 8), (4096, 4096, 4096)):
+                plan.set_th(*th)
+                for fmt in (1, 2):
+                    plan.set_format(bm, fmt)
+                    for w in (64, 128):
+                        for st, li in [(st, li) for st in ((1, 2, 3) if fmt == 2 else (1, 2))
+                                       for li in ((0, 1) if fmt == 2 else (0,))]:
+                            for tpw, order in ((1, 1), (3, 2)):
+                                for place in ((0, 1, 2) if cbp // w == 2 else (0, 1)):
+                                    tag = (f"pairs bm={bm} th={th[0]} fmt={fmt} w={w} s={st} lane_idx={li} "
+                                           f"tpw={tpw} order={order} place={place}")
+                                    say(tag)
+                                    plan.set_variant(bm, w, st, tpw, order)
+                                    plan.set_lane_indices(bm, li)
+                                    plan.set_placement(bm, place)
+                                    plan.set_pairs(bm, 1)
+                                    assert plan.get_pairs(bm) == 1
+                                    plan.run(zero_c=True)
+                                    Cg = plan.download_c()
+                                    assert_close(Cg[:, :colB], Cref, Cabs, prec, tag)
+                                    plan.set_pairs(bm, 0)
+                # the panel sweep over pair units (dense format, one task per wave)
+                if th[0] == 4096:
+                    plan.set_format(bm, 1)
+                    plan.set_lane_indices(bm, 0)
+                    for w in (64, 128):
+                        plan.set_variant(bm, w, 1, 1, 1)
+                        plan.set_placement(bm, 1)
+                        plan.set_pairs(bm, 1)
+                        plan.set_panels(bm, 0, 1)
+                        plan.run(zero_c=True)
+                        C0 = plan.download_c()
+                        for pr, lag in ((256, 1), (512, 2)):
+                            say(f"pairs bm={bm} panels={pr} lag={lag} w={w}")
+                            plan.set_panels(bm, pr, lag)
+                            for rep in range(2):
+                                plan.run(zero_c=True)
+                                Cg = plan.download_c()
+                                assert np.array_equal(Cg, C0), f"pairs bm={bm} w={w} panels={pr} rep={rep}"
+                        plan.set_panels(bm, 0, 1)
+                        assert_close(C0[:, :colB], Cref, Cabs, prec, f"pairs bm={bm} w={w} unsynchronised")
+                        plan.set_pairs(bm, 0)
+            # a width without pair kernels: the launch refuses
+            plan.set_variant(bm, 32, 1, 1, 1)
+            plan.set_pairs(bm, 1)
+            with pytest.raises(tsp.TspError):
+                plan.run(zero_c=True)
+            plan.set_pairs(bm, 0)
+        finally:
+            plan.close()
+
+
 @pytest.mark.parametrize("prec", [0, 1])
 def test_panel_sweep_and_wide_chunks(gpu, orc, prec):
     """The panel-synchronised sweep (tsp_plan_set_panels, dense format) and

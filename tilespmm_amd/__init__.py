@@ -172,6 +172,7 @@ HIP_SYMBOLS = {
     "tsp_spmm_launch_panels": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, _P, _P,
                                          C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                          C.c_int, C.c_int, C.c_int, _P, C.c_longlong]),
+    "tsp_pairs_supported": (C.c_int, [C.c_int, C.c_int, C.c_int]),
     "tsp_switch_v64": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v16": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v8": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
@@ -239,6 +240,8 @@ HOST_SYMBOLS = {
     "tsp_plan_set_placement": (C.c_int, [_P, C.c_int, C.c_int]),
     "tsp_plan_set_lane_indices": (C.c_int, [_P, C.c_int, C.c_int]),
     "tsp_plan_get_lane_indices": (C.c_int, [_P, C.c_int]),
+    "tsp_plan_set_pairs": (C.c_int, [_P, C.c_int, C.c_int]),
+    "tsp_plan_get_pairs": (C.c_int, [_P, C.c_int]),
     "tsp_plan_get_placement": (C.c_int, [_P, C.c_int]),
     "tsp_plan_set_panels": (C.c_int, [_P, C.c_int, C.c_int, C.c_int]),
     "tsp_plan_get_panels": (C.c_int, [_P, C.c_int, _IP, _IP]),
@@ -679,6 +682,13 @@ class Plan:
 
     def get_lane_indices(self, bm: int) -> int:
         return load()[1].tsp_plan_get_lane_indices(self.p, bm)
+
+    def set_pairs(self, bm: int, on: bool):
+        """Tile pairs (two tiles per K = 32 MFMA; fp16 8-/16-row classes)."""
+        _check("tsp_plan_set_pairs", load()[1].tsp_plan_set_pairs(self.p, bm, int(on)))
+
+    def get_pairs(self, bm: int) -> int:
+        return load()[1].tsp_plan_get_pairs(self.p, bm)
 
     def set_placement(self, bm: int, placement: int):
         """XCD placement: 0 = contiguous eighths, 1 = runs dealt round-robin."""

@@ -293,14 +293,21 @@ int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const 
                               d_colidx, c_rows, stream, w, stages, tasks_per_wave, order, placement, 0);
 }
 
+int tsp_pairs_supported(int bm, int prec, int w)
+{
+    return prec == TSP_PREC_FP16 && (bm == 8 || bm == 16) && (w == 64 || w == 128);
+}
+
 int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
                        const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,
                        const int *d_colstart, const void *d_B, float *d_C, const int *d_colidx,
                        int c_rows, void *stream, int w, int stages, int tasks_per_wave, int order,
                        int placement, int flags)
 {
-    if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES)) return TSP_EINVAL;
+    if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES | TSP_LAUNCH_TILE_PAIRS)) return TSP_EINVAL;
     if ((flags & TSP_LAUNCH_LANE_INDICES) && !d_bitmap) return TSP_EINVAL;
+    if ((flags & TSP_LAUNCH_TILE_PAIRS) && !tsp_pairs_supported(bm, prec, w > 0 ? w : tsp::default_chunk_width(bm, colB_p)))
+        return TSP_EINVAL;
     if (bm != 64 && bm != 16 && bm != 8) return TSP_EINVAL;
     if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
     if (colB_p != 32 && (colB_p <= 0 || colB_p % 64 != 0)) return TSP_EINVAL;
@@ -314,7 +321,8 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
     const int kprec = prec == TSP_PREC_TF32 && (flags & TSP_LAUNCH_OPERANDS_TF32) ? tsp::kPrecTf32Exact : prec;
     return tsp::launch(bm, kprec, rowblkblock, colB_p, d_val, d_bitmap, d_vptr, d_rows, d_colstart, d_B,
                        d_C, d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave, order,
-                       placement, (flags & TSP_LAUNCH_LANE_INDICES) != 0);
+                       placement, (flags & TSP_LAUNCH_LANE_INDICES) != 0, 0, 0, 1, nullptr, 0, false,
+                       (flags & TSP_LAUNCH_TILE_PAIRS) != 0);
 }
 
 int tsp_spmm_launch_panels(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
@@ -324,8 +332,11 @@ int tsp_spmm_launch_panels(int bm, int prec, int rowblkblock, int colB_p, const 
                            int placement, int flags, int b_rows, int panel_rows, int panel_lag, int *d_sync,
                            long long sync_ints)
 {
-    if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES | TSP_LAUNCH_SYNC_RESET)) return TSP_EINVAL;
+    if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES | TSP_LAUNCH_SYNC_RESET | TSP_LAUNCH_TILE_PAIRS))
+        return TSP_EINVAL;
     if ((flags & TSP_LAUNCH_LANE_INDICES) && !d_bitmap) return TSP_EINVAL;
+    if ((flags & TSP_LAUNCH_TILE_PAIRS) && !tsp_pairs_supported(bm, prec, w > 0 ? w : tsp::default_chunk_width(bm, colB_p)))
+        return TSP_EINVAL;
     if (bm != 64 && bm != 16 && bm != 8) return TSP_EINVAL;
     if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
     if (colB_p != 32 && (colB_p <= 0 || colB_p % 64 != 0)) return TSP_EINVAL;
@@ -340,7 +351,7 @@ int tsp_spmm_launch_panels(int bm, int prec, int rowblkblock, int colB_p, const 
     return tsp::launch(bm, kprec, rowblkblock, colB_p, d_val, d_bitmap, d_vptr, d_rows, d_colstart, d_B,
                        d_C, d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave, order,
                        placement, (flags & TSP_LAUNCH_LANE_INDICES) != 0, b_rows, panel_rows, panel_lag, d_sync,
-                       sync_ints, (flags & TSP_LAUNCH_SYNC_RESET) != 0);
+                       sync_ints, (flags & TSP_LAUNCH_SYNC_RESET) != 0, (flags & TSP_LAUNCH_TILE_PAIRS) != 0);
 }
 
 int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,

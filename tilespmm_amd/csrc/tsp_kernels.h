@@ -82,24 +82,28 @@ struct SyncArgs {
 int default_chunk_width(int bm, int colB_p);
 int default_stages(int bm, int prec, int w);
 bool valid_variant(int bm, int w, int s);
-const void *select_kernel(int bm, int prec, int w, int s, bool packed, bool lane_idx = false, bool sync = false);
+const void *select_kernel(int bm, int prec, int w, int s, bool packed, bool lane_idx = false, bool sync = false,
+                          bool pair = false);
 // The instantiations of one row-block class (tsp_spmm_bm{64,16,8}.hip);
 // nullptr for a variant that is not built.  prec: TSP_PREC_FP16,
-// TSP_PREC_TF32 or kPrecTf32Exact.
-const void *select_kernel_bm64(int prec, int w, int s, bool packed, bool lane_idx, bool sync);
-const void *select_kernel_bm16(int prec, int w, int s, bool packed, bool lane_idx, bool sync);
-const void *select_kernel_bm8(int prec, int w, int s, bool packed, bool lane_idx, bool sync);
+// TSP_PREC_TF32 or kPrecTf32Exact.  pair: the tile-pair form (fp16 8- and
+// 16-row tiles, 64- and 128-column chunks).
+const void *select_kernel_bm64(int prec, int w, int s, bool packed, bool lane_idx, bool sync, bool pair);
+const void *select_kernel_bm16(int prec, int w, int s, bool packed, bool lane_idx, bool sync, bool pair);
+const void *select_kernel_bm8(int prec, int w, int s, bool packed, bool lane_idx, bool sync, bool pair);
 // w, s, tpw <= 0 select the defaults; order 0 = default, 1 = chunks of one
 // task range adjacent, 2 = chunk-major.  bmp != nullptr selects the
 // bitmap-packed A format (val = packed values, vptr = per-tile offsets).
 // b_rows, panel_rows, panel_lag, sync, sync_ints, sync_reset: the
 // panel-synchronised sweep (sync != nullptr; see SyncArgs) with a buffer of
-// sync_ints counters, zeroed first when sync_reset is set.
+// sync_ints counters, zeroed first when sync_reset is set.  pair: tile pairs
+// (TSP_LAUNCH_TILE_PAIRS).
 int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint64_t *bmp,
            const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
            const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order,
            int placement = kPlaceContiguous, bool lane_idx = false, int b_rows = 0, int panel_rows = 0,
-           int panel_lag = 1, int *sync = nullptr, long long sync_ints = 0, bool sync_reset = false);
+           int panel_lag = 1, int *sync = nullptr, long long sync_ints = 0, bool sync_reset = false,
+           bool pair = false);
 int launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
 constexpr int kGatherBlocks = 8192;      // gather probe grid: 8192 x 256 threads
 int launch_gather(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed, void *sink,

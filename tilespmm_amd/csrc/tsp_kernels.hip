@@ -66,11 +66,11 @@ bool valid_variant(int bm, int w, int s)
     return w == 32 || w == 64 || w == 128;
 }
 
-const void *select_kernel(int bm, int prec, int w, int s, bool packed, bool lane_idx, bool sync)
+const void *select_kernel(int bm, int prec, int w, int s, bool packed, bool lane_idx, bool sync, bool pair)
 {
-    if (bm == 64) return select_kernel_bm64(prec, w, s, packed, lane_idx, sync);
-    if (bm == 16) return select_kernel_bm16(prec, w, s, packed, lane_idx, sync);
-    if (bm == 8) return select_kernel_bm8(prec, w, s, packed, lane_idx, sync);
+    if (bm == 64) return select_kernel_bm64(prec, w, s, packed, lane_idx, sync, pair);
+    if (bm == 16) return select_kernel_bm16(prec, w, s, packed, lane_idx, sync, pair);
+    if (bm == 8) return select_kernel_bm8(prec, w, s, packed, lane_idx, sync, pair);
     return nullptr;
 }
 
@@ -123,7 +123,7 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
            const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
            const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order,
            int placement, bool lane_idx, int b_rows, int panel_rows, int panel_lag, int *sync, long long sync_ints,
-           bool sync_reset)
+           bool sync_reset, bool pair)
 {
     const bool packed = bmp != nullptr;
     if (packed && (bm == 64 || !vptr)) return TSP_EINVAL;
@@ -133,7 +133,7 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
     int nchunks = 0, cm = 0;
     if (!resolve_variant(bm, prec, colB_p, w, s, nchunks, tpw, order, cm)) return TSP_EINVAL;
     if (placement == kPlaceChunkXcd && (nchunks < 2 || kXcds % nchunks != 0)) return TSP_EINVAL;
-    const void *k = select_kernel(bm, prec, w, s, packed, lane_idx, sync != nullptr);
+    const void *k = select_kernel(bm, prec, w, s, packed, lane_idx, sync != nullptr, pair);
     if (!k) return TSP_EINVAL;
     const long long ranges = ((long long)ntasks + tpw - 1) / tpw;
     const long long waves = ranges * nchunks;

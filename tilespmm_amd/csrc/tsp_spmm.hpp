@@ -104,8 +104,12 @@ __device__ __forceinline__ int place_block(int b, int nb, int placement)
 // synchronised fp16 16-row and 8-row kernels with 128-column chunks
 // (configuration 4's) 5 waves in 96, the dense fp16 8-row kernel with
 // 256-column chunks 4 waves in 128; elsewhere the compiler decides.
-template <int BM, int W, int PREC, int S, bool PK, bool SY>
-constexpr int kMinWaves = BM == 64 && W == 64 && S == 1 && !SY                                      ? 3
+// With tile pairs, the synchronised 64-column kernels are held to 5 waves in
+// 96 registers (the compiler's own choice lands one register past it); the
+// 128-column pair kernels are limited to 4 waves by their LDS panels anyway.
+template <int BM, int W, int PREC, int S, bool PK, bool SY, bool PR>
+constexpr int kMinWaves = PR ? (SY && W == 64 && S == 1 ? 5 : 1)
+                          : BM == 64 && W == 64 && S == 1 && !SY                                      ? 3
                           : SY && PREC == TSP_PREC_FP16 && BM == 16 && W == 128 && S == 1 ? 5
                           : SY && PREC == TSP_PREC_FP16 && BM == 8 && W == 128 && S == 1  ? 5
                           : !SY && !PK && PREC == TSP_PREC_FP16 && BM == 8 && W == 256 && S == 1 ? 4
@@ -113,8 +117,15 @@ constexpr int kMinWaves = BM == 64 && W == 64 && S == 1 && !SY                  
 
 // SY: the panel-synchronised sweep (SyncArgs) is compiled in; without it the
 // kernel runs one generation and the sync arguments are ignored.
-template <int BM, int W, int PREC, int S, bool PK, bool LI, bool SY>
-__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(kMinWaves<BM, W, PREC, S, PK, SY>))) void spmm_kernel(
+// PR: tile pairs (fp16 tiles with BN = 16).  The wave's unit of work is two
+// consecutive tiles of one task, multiplied together as one 16 x 32 tile
+// with v_mfma_f32_16x16x32_f16 (MFMA K index 16 + k is the second tile's
+// column k); a task with an odd number of tiles ends with a unit whose
+// second half has zero A values and repeats the first tile's B rows.  Half
+// the MFMAs of the K = 16 form (which runs at half the fp16 rate), half the
+// loop iterations, and twice the B rows in flight per iteration.
+template <int BM, int W, int PREC, int S, bool PK, bool LI, bool SY, bool PR = false>
+__global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(kMinWaves<BM, W, PREC, S, PK, SY, PR>))) void spmm_kernel(
     int ntasks, int nchunks, int tasks_per_wave, int chunk_major, const void *__restrict__ val_,
     const uint64_t *__restrict__ bmp, const int *__restrict__ vptr,
     const unsigned *__restrict__ rows, const int *__restrict__ colstart,
@@ -134,10 +145,12 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     constexpr bool RND = PREC == TSP_PREC_TF32;
     auto rnd = [](uint32_t x) { return RND ? round_tf32_bits(x) : x; };
     constexpr int BN = tile_bn(BM, PREC);
+    static_assert(!PR || (F16 && BN == 16), "tile pairs: fp16 tiles 16 columns wide");
+    constexpr int BNU = PR ? 2 * BN : BN;    // B rows per unit of work (a tile or a pair)
     constexpr int VV = F16 ? 8 : 4;          // values per 16-byte vector
     constexpr int VPR = W / VV;              // vectors per panel row
-    constexpr int NV = BN * VPR / 64;        // vectors per lane per tile
-    static_assert(NV >= 1 && (BN * VPR) % 64 == 0, "panel does not tile the wave");
+    constexpr int NV = BNU * VPR / 64;       // vectors per lane per unit
+    static_assert(NV >= 1 && (BNU * VPR) % 64 == 0, "panel does not tile the wave");
     // LDS row stride: a multiple of the CB-value vectors the MFMA operand
     // reads use (up to 32 bytes), padded so consecutive rows shift banks
     constexpr int LDSW = W + 8;
@@ -150,17 +163,18 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     // registers feed the MFMAs directly and the panel never passes through
     // LDS.  Each load instruction still covers 4 whole 256-byte rows.
     constexpr bool DB = !F16 && VPR == 16 && NV == KS && CB == VV;
-    constexpr int AW = F16 ? (BN == 32 ? 4 : 2) : KS;   // A words per row group
+    constexpr int AW = F16 ? (BNU == 32 ? 4 : 2) : KS;   // A words per row group
     using VT = typename std::conditional<F16, _Float16, float>::type;
     using RV = VT __attribute__((ext_vector_type(CB)));     // CB values of one B row
     constexpr int PWD = PK ? BM * BN / 64 : 1;               // packed: bitmap words per tile
+    constexpr int NT = PR ? 2 : 1;                           // tiles per unit
     struct PMeta {
-        uint64_t bw[PWD];
-        int vbase;
+        uint64_t bw[NT][PWD];
+        int vbase[NT];
     };
     using FV = float __attribute__((ext_vector_type(CB)));  // CB output columns
 
-    __shared__ __attribute__((aligned(32))) VT lds_all[kWavesPerBlock][BN * LDSW];
+    __shared__ __attribute__((aligned(32))) VT lds_all[kWavesPerBlock][BNU * LDSW];
     // fp16 packed A: per wave, the v_perm_b32 byte selectors that expand a
     // lane's 4 raw values into its 4 operand slots, for each of the 16
     // occupancy patterns (slot j takes value rank_j = set bits below j, or 0)
@@ -282,11 +296,19 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         // Packed-format metadata of one tile (bitmap words, value offset): wave-
         // uniform scalar loads, prefetched S tiles ahead like the column indices
         // because the value addresses depend on them.
-        auto load_meta = [&](int t, PMeta &m) {
+        // With tile pairs, a unit without a second tile gets an empty bitmap
+        // (its values decode to zeros) and the first tile's value offset (a
+        // valid address).
+        auto load_meta = [&](int t, PMeta &m, bool two = false) {
             if constexpr (PK) {
 #pragma unroll
-                for (int w = 0; w < PWD; ++w) m.bw[w] = uload(bmp, (size_t)t * PWD + w);
-                m.vbase = uload(vptr, t);
+                for (int w = 0; w < PWD; ++w) m.bw[0][w] = uload(bmp, (size_t)t * PWD + w);
+                m.vbase[0] = uload(vptr, t);
+                if constexpr (PR) {
+#pragma unroll
+                    for (int w = 0; w < PWD; ++w) m.bw[1][w] = two ? uload(bmp, (size_t)(t + 1) * PWD + w) : 0ull;
+                    m.vbase[1] = two ? uload(vptr, t + 1) : m.vbase[0];
+                }
             }
         };
         // Packed A in two halves, so a wave never waits for a load it has just
@@ -304,10 +326,10 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         const int pword = pbit >> 6, poff = pbit & 63;
         const uint64_t below = (1ull << poff) - 1ull;
         const u2 *lut = lut_all[wid];
-        auto issue_a_packed = [&](const PMeta &m, VT (&raw)[NVAL], DecT &dec) {
+        auto issue_a_packed = [&](const PMeta &m, int h, VT (&raw)[NVAL], DecT &dec) {
             static_assert(!PK || BM <= 16, "packed tiles are 8- or 16-row");
             constexpr int WD = PWD;                  // bitmap words per tile
-            const uint64_t *bw = m.bw;
+            const uint64_t *bw = m.bw[h];
             if (BM == 8 && ln >= 8) {
 #pragma unroll
                 for (int j = 0; j < NVAL; ++j) raw[j] = (VT)0;
@@ -331,17 +353,18 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             const unsigned nib = (unsigned)(word >> poff) & ((1u << NVAL) - 1u);
             // the lane's values are consecutive in the packed stream (the value
             // array is padded, so reading NVAL of them is always in bounds)
-            const VT *pv = val + m.vbase + pre;
+            const VT *pv = val + m.vbase[h] + pre;
 #pragma unroll
             for (int j = 0; j < NVAL; ++j) raw[j] = pv[j];
             if constexpr (F16) dec = lut[nib];
             else dec = nib;
         };
-        auto finish_a_packed = [&](const VT (&v)[NVAL], const DecT &dec, uint32_t (&dst)[RG][AW]) {
+        // h: which tile of a pair (its words are MFMA K slots 16h .. 16h + 15)
+        auto finish_a_packed = [&](const VT (&v)[NVAL], const DecT &dec, uint32_t (&dst)[RG][AW], int h = 0) {
             if constexpr (F16) {
                 const u2 bits = __builtin_bit_cast(u2, h4{v[0], v[1], v[2], v[3]});
-                dst[0][0] = __builtin_amdgcn_perm(bits.y, bits.x, dec.x);
-                dst[0][1] = __builtin_amdgcn_perm(bits.y, bits.x, dec.y);
+                dst[0][2 * h] = __builtin_amdgcn_perm(bits.y, bits.x, dec.x);
+                dst[0][2 * h + 1] = __builtin_amdgcn_perm(bits.y, bits.x, dec.y);
             } else {
                 VT o[NVAL];
                 int idx = 0;
@@ -358,7 +381,9 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 for (int j = 0; j < NVAL; ++j) dst[0][j] = rnd(__float_as_uint(o[j]));
             }
         };
-        auto load_a = [&](int t, uint32_t (&dst)[RG][AW]) {
+        // dense A of tile t; with tile pairs (two: the unit holds tile t + 1
+        // too) the second tile's words follow as MFMA K slots 16 .. 31
+        auto load_a = [&](int t, uint32_t (&dst)[RG][AW], bool two = false) {
             const VT *tile = val + (size_t)t * (BM * BN);
 #pragma unroll
             for (int g = 0; g < RG; ++g) {
@@ -371,7 +396,11 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 if constexpr (F16) {
                     const u2 lo = *(const u2 *)(tile + r * BN + 4 * lq);
                     dst[g][0] = lo.x; dst[g][1] = lo.y;
-                    if constexpr (BN == 32) {
+                    if constexpr (PR) {
+                        u2 hi = u2{0u, 0u};
+                        if (two) hi = *(const u2 *)(tile + BM * BN + r * BN + 4 * lq);
+                        dst[g][2] = hi.x; dst[g][3] = hi.y;
+                    } else if constexpr (BN == 32) {
                         const u2 hi = *(const u2 *)(tile + r * BN + 16 + 4 * lq);
                         dst[g][2] = hi.x; dst[g][3] = hi.y;
                     }
@@ -398,10 +427,26 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         // indices of tile t+S are read S tiles before the B gathers that use them.
         constexpr int RPI = 64 / VPR;                // panel rows one vector instruction covers
         const int lrow = lane / VPR;
-        using CSV = int __attribute__((ext_vector_type(LI ? NV : BN)));
-        auto load_cs = [&](int t, CSV &cs) {
-            if constexpr (LI) cs = *(const CSV *)(colidx + (size_t)t * BN + lrow * NV);
-            else cs = *(cptr<CSV>)(colidx + (size_t)t * BN);
+        using CSV = int __attribute__((ext_vector_type(LI ? NV : BNU)));
+        // a unit's BNU indices: its tile's, then (tile pairs) the second
+        // tile's, or the first tile's again when the unit has no second tile
+        auto load_cs = [&](int t, CSV &cs, bool two = false) {
+            if constexpr (LI) {
+                int off = lrow * NV;
+                if (PR && !two && off >= BN) off -= BN;
+                cs = *(const CSV *)(colidx + (size_t)t * BN + off);
+            } else if constexpr (PR) {
+                using CSH = int __attribute__((ext_vector_type(BN)));
+                const CSH lo = *(cptr<CSH>)(colidx + (size_t)t * BN);
+                const CSH hi = *(cptr<CSH>)(colidx + (size_t)(two ? t + 1 : t) * BN);
+#pragma unroll
+                for (int j = 0; j < BN; ++j) {
+                    cs[j] = lo[j];
+                    cs[BN + j] = hi[j];
+                }
+            } else {
+                cs = *(cptr<CSV>)(colidx + (size_t)t * BN);
+            }
         };
         auto select_cid = [&](const CSV &cs, int (&dst)[NV]) {
 #pragma unroll
@@ -468,7 +513,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 // fp32 atomics are issued per lane: transpose each 8-row slab
                 // through the wave's (now idle) B panel in LDS so that every
                 // atomic instruction covers whole rows of consecutive columns
-                static_assert(BN * LDSW * sizeof(VT) >= 8 * W * sizeof(float), "panel too small for a slab");
+                static_assert(BNU * LDSW * sizeof(VT) >= 8 * W * sizeof(float), "panel too small for a slab");
                 float *tr = (float *)lds;
 #pragma unroll
                 for (int h = 0; h < BM / 8; ++h) {
@@ -523,7 +568,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
 #pragma unroll
                 for (int c = 0; c < CB; ++c) {
                     const h4 b0 = __builtin_bit_cast(h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4)(tb + 16 * c)));
-                    if constexpr (BN == 16) {
+                    if constexpr (BNU == 16) {
 #pragma unroll
                         for (int g = 0; g < RG; ++g) {
                             const h4 av = __builtin_bit_cast(h4, u2{a[g][0], a[g][1]});
@@ -542,17 +587,17 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 }
             } else if constexpr (F16) {
                 const VT *lb = lds + ln * CB;
-                constexpr int KR = BN == 16 ? 4 : 8;     // B rows of one lane
+                constexpr int KR = BNU == 16 ? 4 : 8;    // B rows of one lane
                 RV rv[KR];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) rv[j] = *(const RV *)(lb + (4 * lq + j) * LDSW);
-                if constexpr (BN == 32) {
+                if constexpr (BNU == 32) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) rv[4 + j] = *(const RV *)(lb + (16 + 4 * lq + j) * LDSW);
                 }
 #pragma unroll
                 for (int c = 0; c < CB; ++c) {
-                    if constexpr (BN == 16) {
+                    if constexpr (BNU == 16) {
                         const h4 b = h4{rv[0][c], rv[1][c], rv[2][c], rv[3][c]};
 #pragma unroll
                         for (int g = 0; g < RG; ++g) {
@@ -618,15 +663,128 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         // stream from HBM; one period is not enough to hide that latency).
         u4 bv[S][NV];
         uint32_t ar[S][RG][AW];          // dense A: operand words
-        VT araw[S][NVAL];                 // packed A: raw values and occupancy bits
-        DecT anib[S];
+        VT araw[S][NT][NVAL];             // packed A: raw values and occupancy bits
+        DecT anib[S][NT];
         CSV cs[S];
         PMeta pm[S];
         int cid[NV];
-        auto issue_a = [&](int t, int s) {
-            if constexpr (PK) issue_a_packed(pm[s], araw[s], anib[s]);
-            else load_a(t, ar[s]);
+        auto issue_a = [&](int t, int s, bool two = false) {
+            if constexpr (PK) {
+#pragma unroll
+                for (int h = 0; h < NT; ++h) issue_a_packed(pm[s], h, araw[s][h], anib[s][h]);
+            } else {
+                load_a(t, ar[s], two);
+            }
         };
+        auto take_a = [&](int s, uint32_t (&acur)[RG][AW]) {
+            if constexpr (PK) {
+#pragma unroll
+                for (int h = 0; h < NT; ++h) finish_a_packed(araw[s][h], anib[s][h], acur, h);
+            } else {
+#pragma unroll
+                for (int g = 0; g < RG; ++g)
+#pragma unroll
+                    for (int w = 0; w < AW; ++w) acur[g][w] = ar[s][g][w];
+            }
+        };
+        // Task bookkeeping when the compute front reaches tile t: at the end
+        // of task k, flush unless the next task continues the same row-block.
+        auto advance_task = [&](int t) {
+            if (t >= kend) {                 // task k is complete
+                int kn = k;
+                do kend = uload(colstart, ++kn + 1);
+                while (kend <= t);           // skip empty tasks
+                // the next task continues the same row-block: keep
+                // accumulating instead of flushing partial sums
+                const bool same = (uload(rows, kn) & 0x7fffffffu) == (uload(rows, k) & 0x7fffffffu);
+                if (!same) {
+                    flush(gfirst, k);
+                    gfirst = kn;
+                }
+                k = kn;
+            }
+        };
+        if constexpr (PR) {
+            // Units: two consecutive tiles of one task, or the last tile of a
+            // task with an odd count alone.  The unit cursor (ut, in task uk
+            // ending at ukend) runs 2S units ahead of the compute front; a
+            // slot's descriptors follow its unit from the index load (dI) to
+            // the B/A loads and the compute (dB).
+            int ut = tb, uk = k, ukend = kend;
+            auto next_unit = [&](int &first, bool &two) {
+                first = ut;
+                two = false;
+                if (ut >= te) return;
+                two = ut + 1 < ukend;
+                ut += two ? 2 : 1;
+                while (ut < te && ut >= ukend) ukend = uload(colstart, ++uk + 1);
+            };
+            int dIt[S], dBt[S];
+            bool dI2[S], dB2[S];
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                next_unit(dIt[s], dI2[s]);
+                if (dIt[s] < te) {
+                    load_cs(dIt[s], cs[s], dI2[s]);
+                    load_meta(dIt[s], pm[s], dI2[s]);
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                dBt[s] = dIt[s];
+                dB2[s] = dI2[s];
+                if (dBt[s] < te) {
+                    gate(__builtin_amdgcn_readfirstlane(cs[s][0]));
+                    select_cid(cs[s], cid);
+                    load_b(cid, bv[s]);
+                    issue_a(dBt[s], s, dB2[s]);
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                next_unit(dIt[s], dI2[s]);
+                if (dIt[s] < te) {
+                    load_cs(dIt[s], cs[s], dI2[s]);
+                    load_meta(dIt[s], pm[s], dI2[s]);
+                }
+            }
+            bool more = dBt[0] < te;
+            while (more) {
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    if (more && dBt[s] < te) {
+                        advance_task(dBt[s]);
+                        stage_b(bv[s]);
+                        u4 bcur[NV];
+#pragma unroll
+                        for (int i = 0; i < NV; ++i) bcur[i] = u4{0u, 0u, 0u, 0u};
+                        uint32_t acur[RG][AW];
+                        take_a(s, acur);
+                        if (dIt[s] < te) {
+                            gate(__builtin_amdgcn_readfirstlane(cs[s][0]));
+                            select_cid(cs[s], cid);
+                            load_b(cid, bv[s]);
+                            dBt[s] = dIt[s];
+                            dB2[s] = dI2[s];
+                            issue_a(dBt[s], s, dB2[s]);
+                            next_unit(dIt[s], dI2[s]);
+                            if (dIt[s] < te) {
+                                load_cs(dIt[s], cs[s], dI2[s]);
+                                load_meta(dIt[s], pm[s], dI2[s]);
+                            }
+                        } else {
+                            dBt[s] = te;
+                        }
+                        compute(acur, bcur);
+                    } else {
+                        more = false;
+                    }
+                }
+            }
+            flush(gfirst, k);
+            if (sync && lp < sy.npanels - 1) announce(g, lp + 1, sy.npanels - 1);
+            return;
+        }
 #pragma unroll
         for (int s = 0; s < S; ++s)
             if (tb + s < te) {
@@ -653,32 +811,13 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             for (int s = 0; s < S; ++s) {
                 const int t = t0 + s;
                 if (t < te) {
-                    if (t >= kend) {                 // task k is complete
-                        int kn = k;
-                        do kend = uload(colstart, ++kn + 1);
-                        while (kend <= t);           // skip empty tasks
-                        // the next task continues the same row-block: keep
-                        // accumulating instead of flushing partial sums
-                        const bool same = (uload(rows, kn) & 0x7fffffffu) == (uload(rows, k) & 0x7fffffffu);
-                        if (!same) {
-                            flush(gfirst, k);
-                            gfirst = kn;
-                        }
-                        k = kn;
-                    }
+                    advance_task(t);
                     stage_b(bv[s]);
                     u4 bcur[NV];
 #pragma unroll
                     for (int i = 0; i < NV; ++i) bcur[i] = DB ? bv[s][i] : u4{0u, 0u, 0u, 0u};
                     uint32_t acur[RG][AW];
-                    if constexpr (PK) {
-                        finish_a_packed(araw[s], anib[s], acur);
-                    } else {
-#pragma unroll
-                        for (int g = 0; g < RG; ++g)
-#pragma unroll
-                            for (int w = 0; w < AW; ++w) acur[g][w] = ar[s][g][w];
-                    }
+                    take_a(s, acur);
                     if (t + S < te) {
                         gate(__builtin_amdgcn_readfirstlane(cs[s][0]));
                         select_cid(cs[s], cid);
@@ -738,6 +877,14 @@ const void *pick_kernel(int prec)
     if (prec == TSP_PREC_FP16) return (const void *)&spmm_kernel<BM, W, TSP_PREC_FP16, S, PK, LI, SY>;
     if (prec == kPrecTf32Exact) return (const void *)&spmm_kernel<BM, W, kPrecTf32Exact, S, PK, LI, SY>;
     return (const void *)&spmm_kernel<BM, W, TSP_PREC_TF32, S, PK, LI, SY>;
+}
+
+// Tile-pair instantiations exist for fp16 only (nullptr for tf32).
+template <int BM, int W, int S, bool PK, bool LI, bool SY>
+const void *pick_pair_kernel(int prec)
+{
+    if (prec == TSP_PREC_FP16) return (const void *)&spmm_kernel<BM, W, TSP_PREC_FP16, S, PK, LI, SY, true>;
+    return nullptr;
 }
 
 }  // namespace tsp

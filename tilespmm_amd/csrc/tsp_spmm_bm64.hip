@@ -5,8 +5,9 @@
 
 namespace tsp {
 
-const void *select_kernel_bm64(int prec, int w, int s, bool packed, bool lane_idx, bool sync)
+const void *select_kernel_bm64(int prec, int w, int s, bool packed, bool lane_idx, bool sync, bool pair)
 {
+    if (pair) return nullptr;   // 64-row fp16 tiles are 32 wide already (K = 32)
 #define TSP_K(Wv, Sv, PKv, LIv, SYv)                                                  \
     if (w == Wv && s == Sv && packed == PKv && lane_idx == LIv && sync == SYv) \
         return pick_kernel<64, Wv, Sv, PKv, LIv, SYv>(prec);

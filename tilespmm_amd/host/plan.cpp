@@ -36,6 +36,7 @@ struct ClassDev {
     int ntasks = 0;
     int var_w = 0, var_s = 0, var_tpw = 0, var_order = 0;   // kernel variant, 0 = library default
     int var_li = 0;               // packed format: lane-loaded column indices (TSP_LAUNCH_LANE_INDICES)
+    int var_pr = 0;               // tile pairs (TSP_LAUNCH_TILE_PAIRS; fp16 8-/16-row, 64-/128-column chunks)
     int fmt = 1;                  // A format on the device: 1 dense tiles, 2 bitmap-packed
     bool pack_ok = false;         // packed format is worth trying (fewer bytes)
     void *d_pval = nullptr;       // packed values (+4 elements of padding)
@@ -220,11 +221,11 @@ static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
     if (!c.active() || c.ntasks == 0) return TSP_OK;
     const bool pk = c.fmt == 2;
     const int flags = (p->prec == TSP_PREC_TF32 ? TSP_LAUNCH_OPERANDS_TF32 : 0) |
-                      (pk && c.var_li ? TSP_LAUNCH_LANE_INDICES : 0);
+                      (pk && c.var_li ? TSP_LAUNCH_LANE_INDICES : 0) | (c.var_pr ? TSP_LAUNCH_TILE_PAIRS : 0);
     if (c.panel > 0) {
         // the counters are zeroed whenever the launch arguments change
         const std::vector<long long> sig{c.ntasks, c.var_w, c.var_s, c.var_tpw, c.var_order, c.place,
-                                         c.panel, c.panel_lag, p->colA, c.fmt};
+                                         c.panel, c.panel_lag, p->colA, c.fmt, c.var_pr};
         const int reset = sig != c.sync_sig ? TSP_LAUNCH_SYNC_RESET : 0;
         const int st = tsp_spmm_launch_panels(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val,
                                               pk ? c.d_bmp : nullptr, pk ? c.d_vptr : nullptr, c.d_rows,
@@ -332,6 +333,27 @@ extern "C" int tsp_plan_get_lane_indices(tsp_plan *p, int bm)
     if (!p) return -1;
     for (ClassDev &c : p->cls)
         if (c.bm == bm) return c.var_li;
+    return -1;
+}
+
+extern "C" int tsp_plan_set_pairs(tsp_plan *p, int bm, int on)
+{
+    if (p) ++p->version;          // any captured graph is stale now
+    if (!p || (on != 0 && on != 1)) return TSP_EINVAL;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) {
+            if (on && (p->prec != TSP_PREC_FP16 || bm == 64)) return TSP_EINVAL;
+            c.var_pr = on;
+            return TSP_OK;
+        }
+    return TSP_EINVAL;
+}
+
+extern "C" int tsp_plan_get_pairs(tsp_plan *p, int bm)
+{
+    if (!p) return -1;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) return c.var_pr;
     return -1;
 }
 
@@ -963,6 +985,7 @@ static int tune_time_step(tsp_plan *p, double min_ms, double *ms);
 static int tune_class(tsp_plan *p, ClassDev &c)
 {
     if (!c.active() || c.ntasks == 0 || c.var_w || c.var_order || c.var_tpw) return TSP_OK;
+    c.var_pr = 0;                 // steps 1-3 without tile pairs (step 4 tries them)
     tsp_kernel_info k;
     TSP_TRY(tsp_kernel_probe(c.bm, p->prec, p->colB_p, &k));
     const bool chunks = p->colB_p / k.cols_per_task >= 2;
@@ -1098,59 +1121,64 @@ static int tune_class(tsp_plan *p, ClassDev &c)
     //    depth 1 can lose once both are tuned); the rest as kept.  A deeper
     //    pipeline holds more B gathers in flight per wave but costs registers
     //    (occupancy); lane-loaded indices save the select chain for a vector
-    //    load.  The fastest option wins unless it is within 1% of step 3's
-    //    choice at depth 1 with scalar indices (comparing each option with
-    //    the best so far instead would make the pick depend on the order).
+    //    load.  fp16 8- and 16-row classes also try tile pairs (two tiles per
+    //    K = 32 MFMA) at 64- and 128-column chunks, with the same depths and
+    //    index modes (depth 1-2 on dense tiles).  The fastest option wins
+    //    unless it is within 1% of step 3's choice at depth 1 with scalar
+    //    indices (comparing each option with the best so far instead would
+    //    make the pick depend on the order).
+    struct DOpt {
+        int w, order, place, st, li, pr;
+        double ms;
+    };
     std::vector<WOpt> dw{{c.var_w, c.var_order, c.place}};
     if (runner.w >= 0) dw.push_back(runner);
     const int nli = c.fmt == 2 ? 2 : 1;
-    std::vector<std::array<std::array<double, 4>, 2>> sms(dw.size());
-    for (auto &t : sms)
-        for (auto &r : t) r.fill(1e30);
-    for (int round = 0; round < 2; ++round)
-        for (size_t d = 0; d < dw.size(); ++d)
-            for (int li = 0; li < nli; ++li) {
-                const int wd = dw[d].w ? dw[d].w : k.cols_per_task;
-                for (int st = 1; st <= (wd == 256 ? 2 : 3); ++st) {
-                    c.var_w = dw[d].w;
-                    c.var_order = dw[d].order;
-                    c.place = dw[d].place;
-                    c.var_s = st;
-                    c.var_li = li;
-                    double t = 0;
-                    TSP_TRY(tune_time_class(p, c.bm, &t));
-                    sms[d][li][st] = std::min(sms[d][li][st], t);
-                }
-            }
-    size_t db = 0;
-    int sb = 1, lb = 0;
-    for (size_t d = 0; d < dw.size(); ++d)
+    std::vector<DOpt> dopt;
+    for (const WOpt &d : dw) {
+        const int wd = d.w ? d.w : k.cols_per_task;
         for (int li = 0; li < nli; ++li)
-            for (int st = 1; st <= 3; ++st)
-                if (sms[d][li][st] < sms[db][lb][sb]) {
-                    db = d;
-                    sb = st;
-                    lb = li;
-                }
-    if (sms[db][lb][sb] > 0.99 * sms[0][0][1]) {
-        db = 0;
-        sb = 1;
-        lb = 0;
+            for (int st = 1; st <= (wd == 256 ? 2 : 3); ++st) dopt.push_back({d.w, d.order, d.place, st, li, 0, 1e30});
     }
-    c.var_w = dw[db].w;
-    c.var_order = dw[db].order;
-    c.place = dw[db].place;
-    c.var_s = sb;
-    c.var_li = lb;
-    if (log)
-        for (size_t d = 0; d < dw.size(); ++d)
+    if (p->prec == TSP_PREC_FP16 && c.bm != 64)
+        for (int w : {64, 128}) {
+            if (p->colB_p % w != 0) continue;
+            const int nch = p->colB_p / w;
+            // the kept order and placement, where this width allows them
+            int place = c.place, order = nch >= 2 ? (c.var_order ? c.var_order : 1) : 0;
+            if (place == TSP_PLACE_CHUNK_XCD && !(nch == 2 || nch == 4 || nch == 8)) place = TSP_PLACE_INTERLEAVED;
             for (int li = 0; li < nli; ++li)
-                for (int st = 1; st <= 3; ++st)
-                    fprintf(stderr, "tune bm=%d chunk width %d order=%d placement=%s stages %d %s indices: %.5f ms%s\n",
-                            c.bm, dw[d].w ? dw[d].w : k.cols_per_task, dw[d].order, place_name[dw[d].place], st,
-                            li ? "lane" : "scalar", sms[d][li][st],
-                            d == db && st == sb && li == lb ? "  <- kept" : "");
-    return tune_panels(p, c, sms[db][lb][sb]);
+                for (int st = 1; st <= (c.fmt == 2 ? 3 : 2); ++st) dopt.push_back({w, order, place, st, li, 1, 1e30});
+        }
+    for (int round = 0; round < 2; ++round)
+        for (DOpt &o : dopt) {
+            c.var_w = o.w;
+            c.var_order = o.order;
+            c.place = o.place;
+            c.var_s = o.st;
+            c.var_li = o.li;
+            c.var_pr = o.pr;
+            double t = 0;
+            TSP_TRY(tune_time_class(p, c.bm, &t));
+            o.ms = std::min(o.ms, t);
+        }
+    size_t db = 0;
+    for (size_t j = 1; j < dopt.size(); ++j)
+        if (dopt[j].ms < dopt[db].ms) db = j;
+    if (dopt[db].ms > 0.99 * dopt[0].ms) db = 0;     // dopt[0]: step 3's choice, depth 1, scalar indices
+    c.var_w = dopt[db].w;
+    c.var_order = dopt[db].order;
+    c.place = dopt[db].place;
+    c.var_s = dopt[db].st;
+    c.var_li = dopt[db].li;
+    c.var_pr = dopt[db].pr;
+    if (log)
+        for (size_t j = 0; j < dopt.size(); ++j)
+            fprintf(stderr, "tune bm=%d chunk width %d order=%d placement=%s stages %d %s indices%s: %.5f ms%s\n",
+                    c.bm, dopt[j].w ? dopt[j].w : k.cols_per_task, dopt[j].order, place_name[dopt[j].place],
+                    dopt[j].st, dopt[j].li ? "lane" : "scalar", dopt[j].pr ? " tile pairs" : "", dopt[j].ms,
+                    j == db ? "  <- kept" : "");
+    return tune_panels(p, c, dopt[db].ms);
 }
 
 // 5. The panel-synchronised sweep (tsp_spmm_launch_panels) on the dense
@@ -1165,21 +1193,23 @@ static int tune_panels(tsp_plan *p, ClassDev &c, double kept_ms)
 {
     if (c.fmt != 1 || (long long)c.ntasks * p->colB_p / 128 > 16384) return TSP_OK;
     const bool log = getenv("TSP_TUNE_LOG") != nullptr;
-    const int w0 = c.var_w, s0 = c.var_s, tpw0 = c.var_tpw, o0 = c.var_order, pl0 = c.place;
+    const int w0 = c.var_w, s0 = c.var_s, tpw0 = c.var_tpw, o0 = c.var_order, pl0 = c.place, pr0 = c.var_pr;
     const int vs = p->prec == TSP_PREC_FP16 ? 2 : 4;
     struct P {
-        int w, order, rows, lag, s;
+        int w, order, rows, lag, s, pr;
         double ms;
     };
     std::vector<P> opts;
+    const bool pairs = p->prec == TSP_PREC_FP16 && c.bm != 64;
     for (int w : {64, 128, 256}) {
         if (p->colB_p % w != 0 || (c.bm == 64 && w != 64)) continue;
-        for (int order = 1; order <= (p->colB_p / w >= 2 ? 2 : 1); ++order)
-            for (long long bytes : {1LL << 20, 2LL << 20}) {
-                int rows = 64;
-                while ((long long)rows * 2 * w * vs <= bytes) rows *= 2;
-                for (int lag : {2, 3, 4}) opts.push_back({w, order, rows, lag, 1, 1e30});
-            }
+        for (int pr = 0; pr <= (pairs && w <= 128 ? 1 : 0); ++pr)
+            for (int order = 1; order <= (p->colB_p / w >= 2 ? 2 : 1); ++order)
+                for (long long bytes : {1LL << 20, 2LL << 20}) {
+                    int rows = 64;
+                    while ((long long)rows * 2 * w * vs <= bytes) rows *= 2;
+                    for (int lag : {2, 3, 4}) opts.push_back({w, order, rows, lag, 1, pr, 1e30});
+                }
     }
     if (opts.empty()) return TSP_OK;
     const int place = pl0 == TSP_PLACE_CHUNK_XCD ? TSP_PLACE_INTERLEAVED : pl0;
@@ -1189,6 +1219,7 @@ static int tune_panels(tsp_plan *p, ClassDev &c, double kept_ms)
         c.var_tpw = 0;
         c.var_order = o.order;
         c.place = place;
+        c.var_pr = o.pr;
         TSP_TRY(tsp_plan_set_panels(p, c.bm, o.rows, o.lag));
         double t = 0;
         const int st = tune_time_class(p, c.bm, &t);
@@ -1211,15 +1242,16 @@ static int tune_panels(tsp_plan *p, ClassDev &c, double kept_ms)
     bool keep = opts[best].ms < 0.98 * kept_ms;
     if (log)
         for (size_t j = 0; j < opts.size(); ++j)
-            fprintf(stderr, "tune bm=%d panels of %d rows lead %d, chunk width %d order=%d stages %d: %.5f ms%s\n",
-                    c.bm, opts[j].rows, opts[j].lag, opts[j].w, opts[j].order, opts[j].s, opts[j].ms,
-                    keep && j == best ? "  <- kept" : "");
+            fprintf(stderr, "tune bm=%d panels of %d rows lead %d, chunk width %d order=%d stages %d%s: %.5f ms%s\n",
+                    c.bm, opts[j].rows, opts[j].lag, opts[j].w, opts[j].order, opts[j].s,
+                    opts[j].pr ? " tile pairs" : "", opts[j].ms, keep && j == best ? "  <- kept" : "");
     auto apply_best = [&]() -> int {
         c.var_w = opts[best].w;
         c.var_s = opts[best].s;
         c.var_tpw = 0;
         c.var_order = opts[best].order;
         c.place = place;
+        c.var_pr = opts[best].pr;
         return tsp_plan_set_panels(p, c.bm, opts[best].rows, opts[best].lag);
     };
     auto restore = [&]() -> int {
@@ -1228,6 +1260,7 @@ static int tune_panels(tsp_plan *p, ClassDev &c, double kept_ms)
         c.var_tpw = tpw0;
         c.var_order = o0;
         c.place = pl0;
+        c.var_pr = pr0;
         return tsp_plan_set_panels(p, c.bm, 0, 1);
     };
     // The capped grid assumes the device to itself: when other classes run
@@ -1381,7 +1414,7 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
         if (hot_tuning && !kept) {
             // the variants were tuned for the hot rows: tune them again without
             for (ClassDev &c : p->cls) {
-                c.var_w = c.var_s = c.var_tpw = c.var_order = c.var_li = 0;
+                c.var_w = c.var_s = c.var_tpw = c.var_order = c.var_li = c.var_pr = 0;
                 c.place = TSP_PLACE_CONTIGUOUS;
                 TSP_TRY(tsp_plan_set_panels(p, c.bm, 0, 1));
                 TSP_TRY(tune_class(p, c));
