@@ -245,6 +245,9 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         int kend = uload(colstart, k0 + 1);
         while (kend <= tb) kend = uload(colstart, ++k + 1);  // skip leading empty tasks
         int gfirst = k;                  // first task of the accumulation group
+        // the current task's schedule word (first row, split flag), read when
+        // the task starts so that a flush never waits for it
+        unsigned rwk = uload(rows, k);
         const int col0 = chunk * W;
         // Before the B loads of a tile whose first column is fc: announce its
         // panel q and wait (bounded) until every registered wave of this XCD
@@ -476,8 +479,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         // the tasks just before and after the group belong to other row-blocks,
         // this wave ran every task of it (a split row-block's tasks are
         // consecutive, as tile_pretreatment emits them).
-        auto flush = [&](int first, int last) {
-            const unsigned rw = uload(rows, last);
+        auto flush = [&](int first, int last, unsigned rw) {   // rw = rows[last]
             const int row0 = (int)(rw & 0x7fffffffu);
             bool split = (rw & 0x80000000u) != 0;
             if (split && first < last) {
@@ -696,12 +698,13 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 while (kend <= t);           // skip empty tasks
                 // the next task continues the same row-block: keep
                 // accumulating instead of flushing partial sums
-                const bool same = (uload(rows, kn) & 0x7fffffffu) == (uload(rows, k) & 0x7fffffffu);
-                if (!same) {
-                    flush(gfirst, k);
+                const unsigned rn = uload(rows, kn);
+                if ((rn & 0x7fffffffu) != (rwk & 0x7fffffffu)) {
+                    flush(gfirst, k, rwk);
                     gfirst = kn;
                 }
                 k = kn;
+                rwk = rn;
             }
         };
         if constexpr (PR) {
@@ -781,7 +784,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                     }
                 }
             }
-            flush(gfirst, k);
+            flush(gfirst, k, rwk);
             if (sync && lp < sy.npanels - 1) announce(g, lp + 1, sy.npanels - 1);
             return;
         }
@@ -832,7 +835,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 }
             }
         }
-        flush(gfirst, k);
+        flush(gfirst, k, rwk);
         if (sync && lp < sy.npanels - 1) announce(g, lp + 1, sy.npanels - 1);
     };
 

@@ -185,6 +185,34 @@ def corpus(which):
             ("powerlaw_2^20_m16_a2.5", lambda: gen_powerlaw(rng, 1 << 20, 16, 2.5)),
             ("rmat_20_ef16", lambda: gen_rmat(rng, 20, 16)),
         ]
+    if which == "extra":
+        # neighbours of the matrices a leave-one-matrix-out refit served worst
+        # (block-sparse families, small uniform matrices), more RMAT scales and
+        # power-law exponents, and other band widths.  Each matrix draws from
+        # its own generator, seeded from its name, so any subset (--only)
+        # generates the same instances
+        def seeded(name, make):
+            return name, lambda: make(np.random.default_rng(int(hashlib.sha1(name.encode()).hexdigest()[:8], 16)))
+        extra = [
+            ("blocks32_2^15_d2", lambda rng: gen_blocks(rng, 1 << 15, 32, 0.02)),
+            ("blocks32_2^13_d8", lambda rng: gen_blocks(rng, 1 << 13, 32, 0.08)),
+            ("blocks16_2^14_d4", lambda rng: gen_blocks(rng, 1 << 14, 16, 0.04)),
+            ("blocks64_2^14_d2", lambda rng: gen_blocks(rng, 1 << 14, 64, 0.02)),
+            ("blocks8_2^14_d2", lambda rng: gen_blocks(rng, 1 << 14, 8, 0.02)),
+            ("blocks8_2^16_d05", lambda rng: gen_blocks(rng, 1 << 16, 8, 0.005, 1e-5)),
+            ("uniform_2^13_k8", lambda rng: gen_uniform(rng, 1 << 13, 8)),
+            ("uniform_2^12_k16", lambda rng: gen_uniform(rng, 1 << 12, 16)),
+            ("uniform_2^15_k32", lambda rng: gen_uniform(rng, 1 << 15, 32)),
+            ("uniform_2^17_k24", lambda rng: gen_uniform(rng, 1 << 17, 24)),
+            ("rmat_17_ef16", lambda rng: gen_rmat(rng, 17, 16)),
+            ("rmat_19_ef8", lambda rng: gen_rmat(rng, 19, 8)),
+            ("powerlaw_2^19_m12_a2.1", lambda rng: gen_powerlaw(rng, 1 << 19, 12, 2.1)),
+            ("banded_2^16_bw128_k16", lambda rng: gen_banded(rng, 1 << 16, 128, 16)),
+            ("blocks64_2^15_d1", lambda rng: gen_blocks(rng, 1 << 15, 64, 0.01)),
+            ("blocks64_2^13_d4", lambda rng: gen_blocks(rng, 1 << 13, 64, 0.04, 1e-4)),
+            ("blocks48_2^14_d2", lambda rng: gen_blocks(rng, 3 << 13, 48, 0.02)),
+        ]
+        items += [seeded(n, mk) for n, mk in extra]
     return items
 
 
@@ -221,6 +249,7 @@ def sweep_matrix(name, A, colB, reps, out, tune=False):
         sig = hashlib.sha1(cls.tobytes()).hexdigest()
         if sig not in seen:
             seen[sig] = time_candidate(A, B, colB, cbp, g, d, reps, tune)
+            print(f"   ({g:.2f},{d:.2f}): {seen[sig][0]:.4f} ms, tiles {seen[sig][2]}", flush=True)
         times.append(seen[sig][0])
     best = int(np.argmin(times))
     rec = {"matrix": name, "prec": A.prec, "colB": colB, "features": f.tolist(), "times_ms": times,
@@ -654,7 +683,7 @@ def main():
     tf.add_argument("--per-group", action="store_true", help="one weight pair per (class, prec, width)")
     s = sub.add_parser("sweep")
     s.add_argument("--configs", type=int, nargs="*", default=[])
-    s.add_argument("--corpus", choices=["small", "full"], default=None)
+    s.add_argument("--corpus", choices=["small", "full", "extra"], default=None)
     s.add_argument("--precs", type=int, nargs="*", default=[0, 1])
     s.add_argument("--colBs", type=int, nargs="*", default=[32, 128])
     s.add_argument("--reps", type=int, default=30)
