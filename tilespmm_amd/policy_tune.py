@@ -293,22 +293,27 @@ def cmd_sweep(args):
 # ---------------------------------------------------------------------------
 # fit + export
 # ---------------------------------------------------------------------------
-def load_results(path):
-    recs = [json.loads(l) for l in open(path) if l.strip()]
+def load_results(paths):
+    """Sweep records from one file or several."""
+    recs = []
+    for path in ([paths] if isinstance(paths, str) else paths):
+        recs += [json.loads(l) for l in open(path) if l.strip()]
     return [r for r in recs if "times_ms" in r]
 
 
-def fit_tree(recs, max_depth, min_leaf):
-    """Greedy binary tree over features; leaf = candidate with the lowest mean
-    normalised time among its matrices; splits maximise the drop in summed
-    regret."""
+def fit_tree(recs, max_depth, min_leaf, worst_weight=0.0):
+    """Greedy binary tree over features; leaf = candidate with the lowest
+    summed normalised time (time / best time of the case) over its cases,
+    plus worst_weight x cases x the worst of them (a robust leaf: a case
+    that is far off in a leaf counts beyond its share); splits maximise the
+    drop in that cost."""
     X = np.array([[r["features"][i + 2] for i in range(9)] for r in recs], dtype=np.float64)
     T = np.array([np.array(r["times_ms"]) / r["best_ms"] for r in recs], dtype=np.float64)
 
     def leaf_cost(idx):
-        m = T[idx].mean(axis=0)
-        a = int(np.argmin(m))
-        return a, float(T[idx, a].sum())
+        c = T[idx].sum(axis=0) + worst_weight * len(idx) * T[idx].max(axis=0)
+        a = int(np.argmin(c))
+        return a, float(c[a])
 
     nodes = []
 
@@ -443,7 +448,7 @@ def cmd_fit(args):
     roots, allnodes = [], []
     for prec in (0, 1):
         rs = [r for r in recs if r["prec"] == prec] or recs
-        root, nodes = fit_tree(rs, args.depth, args.min_leaf)
+        root, nodes = fit_tree(rs, args.depth, args.min_leaf, args.worst_weight)
         off = len(allnodes)
 
         def shift(x):
@@ -452,7 +457,8 @@ def cmd_fit(args):
             allnodes.append({"feature": n["feature"], "cut": n["cut"], "left": shift(n["left"]),
                              "right": shift(n["right"])})
         roots.append(shift(root))
-    note = f"{len(recs)} swept (matrix, colB, precision) cases, depth <= {args.depth}"
+    note = (f"{len(recs)} swept (matrix, colB, precision) cases, depth <= {args.depth}, at least {args.min_leaf} "
+            f"cases per leaf, worst-case weight {args.worst_weight}")
     if args.lomo:
         # leave one matrix out: refit without it, score its cases
         def walk(root, nodes, f):
@@ -464,10 +470,11 @@ def cmd_fit(args):
         reg, insample = [], []
         for prec in (0, 1):
             rs = [r for r in recs if r["prec"] == prec]
-            root, nodes = fit_tree(rs, args.depth, args.min_leaf)
+            root, nodes = fit_tree(rs, args.depth, args.min_leaf, args.worst_weight)
             insample += [r["times_ms"][walk(root, nodes, r["features"])] / r["best_ms"] for r in rs]
             for m in sorted(set(r["matrix"] for r in rs)):
-                root, nodes = fit_tree([r for r in rs if r["matrix"] != m], args.depth, args.min_leaf)
+                root, nodes = fit_tree([r for r in rs if r["matrix"] != m], args.depth, args.min_leaf,
+                                       args.worst_weight)
                 reg += [r["times_ms"][walk(root, nodes, r["features"])] / r["best_ms"]
                         for r in rs if r["matrix"] == m]
         note += (f"; in-sample mean x{np.mean(insample):.3f} worst x{np.max(insample):.3f}, "
@@ -691,13 +698,15 @@ def main():
     s.add_argument("--only", nargs="*", default=None, help="substrings of matrix names to keep")
     s.add_argument("--out", required=True)
     f = sub.add_parser("fit")
-    f.add_argument("--inp", required=True)
+    f.add_argument("--inp", required=True, nargs="+")
     f.add_argument("--header", default=os.path.join(HERE, "host", "model.h"))
     f.add_argument("--depth", type=int, default=4)
     f.add_argument("--min-leaf", type=int, default=3)
+    f.add_argument("--worst-weight", type=float, default=0.0,
+                   help="leaf cost = summed regret + this x cases x worst regret (robust leaves)")
     f.add_argument("--lomo", action="store_true", help="also report leave-one-matrix-out regret")
     c = sub.add_parser("check")
-    c.add_argument("--inp", required=True)
+    c.add_argument("--inp", required=True, nargs="+")
     e = sub.add_parser("export")
     e.add_argument("--header", default=os.path.join(HERE, "host", "model.h"),
                    help="the fitted table whose model_tree.json is read")
