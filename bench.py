@@ -619,7 +619,7 @@ def main():
     ap.add_argument("--lane-idx", type=ints3, default=None,
                     help="pin lane-loaded column indices per class 64,16,8 (1 off, 2 on, 0 keep)")
     ap.add_argument("--pairs", type=ints3, default=None,
-                    help="pin tile pairs per class 64,16,8 (1 off, 2 on, 0 keep; fp16 8-/16-row classes)")
+                    help="pin tile pairs per class 64,16,8 (1 off, 2 on, 0 keep; fp16 8-/16-row classes, tf32 8-row class)")
     ap.add_argument("--panels", type=ints3, default=None,
                     help="pin the panel-synchronised sweep per class: B rows per panel (0 = off)")
     ap.add_argument("--panel-lag", type=ints3, default=None,

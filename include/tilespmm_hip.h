@@ -202,11 +202,17 @@ int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const 
  * per class (faster on the gather-bound RMAT and power-law fp16 classes,
  * slower on banded and block-sparse ones). */
 #define TSP_LAUNCH_LANE_INDICES 2
-/* TSP_LAUNCH_TILE_PAIRS (fp16 8- and 16-row tiles, chunk width w 64 or 128,
- * given explicitly): each wave multiplies two consecutive tiles of a task at
- * a time, as one 16 x 32 tile on v_mfma_f32_16x16x32_f16 (the K = 16 form
- * runs at half the fp16 rate); a task with an odd tile count ends with a
- * single tile.  Same products, accumulated in another order (fp32).
+/* TSP_LAUNCH_TILE_PAIRS (fp16 8- and 16-row tiles, chunk width w 64 or 128;
+ * tf32 8-row tiles, w 64): each wave multiplies two consecutive tiles of a
+ * task at a time; a task with an odd tile count ends with a single tile.
+ * fp16: one 16 x 32 tile on v_mfma_f32_16x16x32_f16 (the K = 16 form runs at
+ * half the fp16 rate).  tf32 (needs TSP_LAUNCH_OPERANDS_TF32): split-bf16
+ * products on v_mfma_f32_16x16x32_bf16 -- the high and low bf16 halves of
+ * each A value in MFMA rows 0-7 and 8-15, each B value as the split word of
+ * tsp_split_bf16_device, so d_B must hold those words (B values as split
+ * words, same layout); every product is exact, as in the fp32 MFMA path
+ * (but for values below 2^-116, whose low halves lose bits).
+ * Same products, accumulated in another order (fp32).
  * tsp_pairs_supported(bm, prec, w) says whether a launch with chunk width w
  * may pass it (a launch given w <= 0 checks its default width).  No
  * counterpart in the reference (its 16-row kernel covers both k-halves of
@@ -278,6 +284,18 @@ int tsp_round_tf32_bits(const uint32_t *in, uint32_t *out, size_t n);
 /* The same rounding in place over n fp32 values in device memory,
  * asynchronous on `stream`. */
 int tsp_round_tf32_device(void *d_x, size_t n, void *stream);
+
+/* tf32 values as split-bf16 words: high half = the value truncated to bf16,
+ * low half = the rest, exact for magnitudes of at least 2^-116 (below, the
+ * rest is an fp32 subnormal truncated to 16 bits: error < 2^-126); these are
+ * the words the tf32 tile-pair kernels read as B.  Inf keeps a zero low
+ * half, NaN becomes a quiet NaN in both halves.
+ * Inputs must be tf32 values (e.g. after tsp_round_tf32_device).  The host
+ * form converts n values; the device form converts n values of d_src into
+ * d_dst (may be equal), asynchronously on `stream`.  No counterpart in the
+ * reference (its tensor cores take tf32 operands directly). */
+int tsp_split_bf16_bits(const uint32_t *in, uint32_t *out, size_t n);
+int tsp_split_bf16_device(const void *d_src, void *d_dst, size_t n, void *stream);
 
 /* A plain streaming copy kernel (dst = src, 16-byte vectors), used to
  * calibrate HBM byte counters and the achievable copy bandwidth. */

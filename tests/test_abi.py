@@ -99,7 +99,9 @@ def test_error_strings_and_arg_checks(tsp):
     _, host = tsp.load()
     # tile pairs: fp16 8- and 16-row tiles at 64- or 128-column chunks only
     assert [hip.tsp_pairs_supported(bm, pr, w) for bm, pr, w in
-            ((16, 0, 64), (8, 0, 128), (16, 1, 64), (64, 0, 64), (8, 0, 32), (16, 0, 256))] == [1, 1, 0, 0, 0, 0]
+            ((16, 0, 64), (8, 0, 128), (8, 1, 64), (16, 1, 64), (8, 1, 128), (64, 0, 64), (8, 0, 32),
+             (16, 0, 256))] == [1, 1, 1, 0, 0, 0, 0, 0]
+    assert hip.tsp_split_bf16_bits(None, None, 1) == hip.tsp_split_bf16_device(None, None, 1, None) == 1001
     assert host.tsp_plan_set_pairs(None, 16, 1) == 1001 and host.tsp_plan_get_pairs(None, 16) == -1
     assert host.tsp_plan_graph_capture(None, 1) == 1001
     assert host.tsp_plan_graph_run(None, 1) == 1001

@@ -158,8 +158,8 @@ def test_tile_pairs(gpu, orc):
     tasks per wave, order and placement gives the oracle's result, with
     thresholds that leave tasks of odd and even tile counts (the last unit of
     an odd task holds one tile) and split tasks; the panel sweep with pairs
-    is bit-identical to the unsynchronised pair launch.  tf32 plans and other
-    chunk widths refuse pairs."""
+    is bit-identical to the unsynchronised pair launch.  Chunk widths without
+    pair kernels refuse them."""
     tsp = gpu
     prec = 0
     rng = np.random.default_rng(91)
@@ -222,6 +222,143 @@ def test_tile_pairs(gpu, orc):
             plan.set_pairs(bm, 0)
         finally:
             plan.close()
+
+
+def test_tile_pairs_tf32(gpu, orc):
+    """tf32 tile pairs (8-row tiles, 64-column chunks): split-bf16 products on
+    v_mfma_f32_16x16x32_bf16 against B in split words.  Every depth, format,
+    index mode, tasks per wave, order and placement gives the oracle's
+    result within the tf32 tolerance, with odd and even task lengths and
+    split tasks, and with hot B rows (the plan refills the split form's hot
+    slots); the split form converts back exactly."""
+    tsp = gpu
+    hip = tsp.load()[0]
+    prec = 1
+    rng = np.random.default_rng(93)
+    A = random_matrix(tsp, rng, 613, 509, 45, prec, heavy_rows=4)
+    colB = 128
+    B, cbp = random_b(tsp, rng, A.cols, colB, prec)
+    Cref, Cabs = reference(orc, A, B, colB)
+    subs = tsp.matrix_split(A, 5.0, 3.0)
+    tiles = [tsp.tile_create(sb, A.cols, b, prec) for sb, b in zip(subs, (64, 16, 8))]
+    plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
+    try:
+        with pytest.raises(tsp.TspError):
+            plan.set_pairs(16, 1)                       # tf32 pairs: 8-row tiles only
+        for hot in (0, 1 << 16):
+            plan.set_hot_rows(hot)
+            for th in ((3, 3, 3), (8, 8, 8), (4096, 4096, 4096)):
+                plan.set_th(*th)
+                for fmt in (1, 2):
+                    plan.set_format(8, fmt)
+                    for st, li in [(st, li) for st in ((1, 2, 3) if fmt == 2 else (1, 2))
+                                   for li in ((0, 1) if fmt == 2 else (0,))]:
+                        for tpw, order in ((1, 1), (3, 2)):
+                            for place in (0, 1, 2):
+                                tag = (f"tf32 pairs hot={hot} th={th[0]} fmt={fmt} s={st} lane_idx={li} tpw={tpw} "
+                                       f"order={order} place={place}")
+                                say(tag)
+                                plan.set_variant(8, 64, st, tpw, order)
+                                plan.set_lane_indices(8, li)
+                                plan.set_placement(8, place)
+                                plan.set_pairs(8, 1)
+                                plan.run(zero_c=True)
+                                Cg = plan.download_c()
+                                assert_close(Cg[:, :colB], Cref, Cabs, prec, tag)
+                                plan.set_pairs(8, 0)
+        plan.set_variant(8, 128, 1, 1, 1)
+        plan.set_pairs(8, 1)
+        with pytest.raises(tsp.TspError):
+            plan.run(zero_c=True)                       # 128-column chunks have no tf32 pair kernel
+    finally:
+        plan.close()
+    # the split words: host and device conversions agree and sum back exactly
+    bits = np.concatenate([np.frombuffer(np.float32(rng.uniform(-1e3, 1e3, 4000)).tobytes(), np.uint32),
+                           np.array([0x7F800000, 0xFF800000, 0x7F800001, 0x7FFFFFFF, 0, 0x80000000], np.uint32)])
+    tf = np.zeros_like(bits)
+    assert hip.tsp_round_tf32_bits(bits.ctypes.data, tf.ctypes.data, bits.size) == 0
+    host = np.zeros_like(tf)
+    assert hip.tsp_split_bf16_bits(tf.ctypes.data, host.ctypes.data, tf.size) == 0
+    d = tsp._DevBuf(tf)
+    try:
+        assert hip.tsp_split_bf16_device(d.p, d.p, tf.size, None) == 0
+        assert np.array_equal(tsp._d2h(d.p, tf.size, np.uint32), host)
+    finally:
+        d.free()
+    hi = (host & 0xFFFF0000).view(np.float32).astype(np.float64)
+    lo = (host << 16).view(np.float32).astype(np.float64)
+    fin = np.isfinite(tf.view(np.float32))
+    assert np.array_equal(hi[fin] + lo[fin], tf.view(np.float32)[fin].astype(np.float64))
+    assert np.isposinf(hi[-6]) and lo[-6] == 0 and np.isneginf(hi[-5]) and lo[-5] == 0
+    assert np.isnan(hi[-4]) and np.isnan(lo[-4]) and np.isnan(hi[-3]) and np.isnan(lo[-3])
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+def test_nan_and_inf_propagate_with_tile_pairs(gpu, prec):
+    """NaN and Inf propagate through the tile-pair kernels exactly as through
+    the single-tile ones (every row in the 8-row class, 64-column chunks;
+    tf32 through the split words), with tasks of odd tile counts (whose last
+    unit has no second tile), even counts and split tasks: a NaN in A reaches
+    its row; a NaN / +Inf in a B row reaches, as NaN / +Inf, the rows whose
+    CSR rows hold it and, as NaN, the other rows of the row-blocks whose
+    tiles gather it; a -Inf in A meets finite B values as -Inf; every other
+    entry stays finite."""
+    tsp = gpu
+    rng = np.random.default_rng(19)
+    rows, cols, colB = 256, 128, 64
+    rp = np.concatenate([[0], np.cumsum(np.full(rows, 4))]).astype(np.int32)
+    ci = np.concatenate([np.sort(rng.choice(cols, 4, replace=False)) for _ in range(rows)]).astype(np.int32)
+    v = rng.uniform(0.5, 1, rp[-1]).astype(np.float32)
+    bv = rng.uniform(0.5, 1, (cols, colB)).astype(np.float32)
+    if prec == 0:
+        val, B = v.astype(np.float16).view(np.uint16), bv.astype(np.float16).view(np.uint16)
+        nan_a, ninf_a, nan_b, inf_b = np.uint16(0x7E01), np.uint16(0xFC00), np.uint16(0x7C01), np.uint16(0x7C00)
+    else:
+        val, B = v.copy(), bv.copy()
+        nan_a, ninf_a = np.uint32(0x7FFFFFFF), np.uint32(0xFF800000)
+        nan_b, inf_b = np.uint32(0x7F800001), np.uint32(0x7F800000)
+    bits = np.uint16 if prec == 0 else np.uint32
+    val.view(bits)[rp[10] + 1] = nan_a
+    val.view(bits)[rp[100] + 2] = ninf_a
+    cnan, cinf = 77, 91
+    B.view(bits)[cnan, 5] = nan_b
+    B.view(bits)[cinf, 9] = inf_b
+    A = tsp.Csr(rows, cols, rp, ci, val, prec)
+    subs = tsp.matrix_split(A, 5.0, 3.0)
+    assert [s.rows for s in subs] == [0, 0, rows]
+    tiles = [tsp.tile_create(s, A.cols, b, prec) for s, b in zip(subs, (64, 16, 8))]
+    plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, colB, prec, B)
+    has = lambda c: np.array([c in ci[rp[r]:rp[r + 1]] for r in range(rows)])
+    block = lambda c: np.repeat([has(c)[i:i + 8].any() for i in range(0, rows, 8)], 8)
+    a_inf = ci[rp[100] + 2]                     # the B row the -Inf of row 100 meets
+    try:
+        for th in (1, 3, 8, 4096):
+            plan.set_th(0, 0, th)
+            plan.set_variant(8, 64, 1, 1, 1)
+            plan.set_pairs(8, 0)
+            plan.run(zero_c=True)
+            C1 = plan.download_c()[:, :colB]
+            plan.set_pairs(8, 1)
+            plan.run(zero_c=True)
+            C = plan.download_c()[:, :colB]
+            tag = f"prec={prec} th={th}"
+            assert np.array_equal(np.isnan(C), np.isnan(C1)), tag
+            assert np.array_equal(np.isposinf(C), np.isposinf(C1)), tag
+            assert np.array_equal(np.isneginf(C), np.isneginf(C1)), tag
+            other = np.ones(rows, bool)
+            other[[10, 100]] = False
+            assert np.isnan(C[10]).all(), tag
+            assert np.isnan(C[has(cnan) & other, 5]).all(), tag
+            assert np.isposinf(C[has(cinf) & other, 9]).all(), tag
+            assert np.isnan(C[block(cinf) & ~has(cinf) & other, 9]).all(), tag
+            rest = np.delete(np.arange(colB), [5, 9])
+            assert np.isneginf(C[100, rest]).all(), tag
+            assert np.isfinite(C[other][:, rest]).all(), tag
+            assert np.isfinite(C[~block(cnan) & other, 5]).all(), tag
+            assert np.isfinite(C[~block(cinf) & other, 9]).all(), tag
+            assert a_inf not in (cnan, cinf)
+    finally:
+        plan.close()
 
 
 @pytest.mark.parametrize("prec", [0, 1])

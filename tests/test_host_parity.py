@@ -328,6 +328,49 @@ def test_gen_c4_blocksparse(tsp):
     assert abs(nnz - (335544 * 256 + 429497 * 0.98)) < 1000
 
 
+def test_split_bf16_bits(tsp):
+    """The split form the tf32 tile-pair kernels read B in
+    (tsp_split_bf16_bits): the high bf16 half is the value's top 16 bits, the
+    low half is the remainder, so hi + lo == x exactly for every tf32 value
+    of magnitude at least 2^-116 (the remainder has at most 3 significant
+    bits and the sign of x); below that the remainder is an fp32 subnormal,
+    truncated to its top 16 bits, and hi + lo is within 2^-126 of x.  Inf
+    keeps a zero low half and every NaN becomes a NaN pair.  Checked against
+    the definition on random values of every exponent, the extremes and the
+    specials."""
+    hip = tsp.load()[0]
+    rng = np.random.default_rng(5)
+    raw = rng.integers(0, 1 << 32, 200000, dtype=np.uint64).astype(np.uint32)
+    ex = (raw >> 23) & 0xFF
+    raw = raw[(ex > 0) & (ex < 255)]                      # normal numbers
+    x = np.concatenate([raw, np.array([0x3F800000, 0x7F7FE000, 0xFF7FE000, 0x00800000, 0x80800000, 0, 0x80000000,
+                                       0x7F800000, 0xFF800000, 0x7F800001, 0x7FFFFFFF, 0xFFC00000], np.uint32)])
+    tf = np.zeros_like(x)
+    assert hip.tsp_round_tf32_bits(x.ctypes.data_as(C.c_void_p), tf.ctypes.data_as(C.c_void_p), x.size) == 0
+    out = np.zeros_like(tf)
+    assert hip.tsp_split_bf16_bits(tf.ctypes.data_as(C.c_void_p), out.ctypes.data_as(C.c_void_p), tf.size) == 0
+    hi_bits = out & np.uint32(0xFFFF0000)
+    lo_bits = (out << np.uint32(16)).astype(np.uint32)
+    hi, lo = hi_bits.view(np.float32), lo_bits.view(np.float32)
+    f = tf.view(np.float32)
+    fin = np.isfinite(f)
+    assert np.array_equal(hi_bits[fin], tf[fin] & np.uint32(0xFFFF0000))
+    with np.errstate(invalid="ignore"):
+        err = np.abs(hi.astype(np.float64) + lo.astype(np.float64) - f.astype(np.float64))
+    big = fin & (((tf >> np.uint32(23)) & np.uint32(0xFF)) >= 11)       # |x| >= 2^-116
+    assert big.sum() > 190000
+    assert (err[big] == 0).all()
+    assert (err[fin & ~big] < 2.0 ** -126).all()
+    nz = big & (lo != 0)
+    assert np.array_equal(np.signbit(lo[nz]), np.signbit(f[nz]))
+    # at most 3 significant bits below the high half's 8
+    assert ((lo_bits[nz] & np.uint32(0x001F0000)) == 0).all()
+    inf = np.isinf(f)
+    assert np.array_equal(hi_bits[inf], tf[inf]) and (lo_bits[inf] == 0).all()
+    nan = np.isnan(f)
+    assert nan.sum() == 3 and (out[nan] == np.uint32(0x7FC07FC0)).all()
+
+
 def test_round_tf32_bits_special_values(tsp, orc):
     """The kernels' tf32 operand rounding (tsp_round_tf32_bits, the same
     function the device code calls) equals the oracle's nearest-even rounding

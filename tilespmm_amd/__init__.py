@@ -173,6 +173,8 @@ HIP_SYMBOLS = {
                                          C.c_int, _P, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                                          C.c_int, C.c_int, C.c_int, _P, C.c_longlong]),
     "tsp_pairs_supported": (C.c_int, [C.c_int, C.c_int, C.c_int]),
+    "tsp_split_bf16_bits": (C.c_int, [_P, _P, C.c_size_t]),
+    "tsp_split_bf16_device": (C.c_int, [_P, _P, C.c_size_t, _P]),
     "tsp_switch_v64": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v16": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v8": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),

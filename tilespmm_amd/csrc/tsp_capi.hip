@@ -295,6 +295,7 @@ int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const 
 
 int tsp_pairs_supported(int bm, int prec, int w)
 {
+    if (prec == TSP_PREC_TF32) return bm == 8 && w == 64;
     return prec == TSP_PREC_FP16 && (bm == 8 || bm == 16) && (w == 64 || w == 128);
 }
 
@@ -306,7 +307,9 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
 {
     if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES | TSP_LAUNCH_TILE_PAIRS)) return TSP_EINVAL;
     if ((flags & TSP_LAUNCH_LANE_INDICES) && !d_bitmap) return TSP_EINVAL;
-    if ((flags & TSP_LAUNCH_TILE_PAIRS) && !tsp_pairs_supported(bm, prec, w > 0 ? w : tsp::default_chunk_width(bm, colB_p)))
+    if ((flags & TSP_LAUNCH_TILE_PAIRS) &&
+        (!tsp_pairs_supported(bm, prec, w > 0 ? w : tsp::default_chunk_width(bm, colB_p)) ||
+         (prec == TSP_PREC_TF32 && !(flags & TSP_LAUNCH_OPERANDS_TF32))))
         return TSP_EINVAL;
     if (bm != 64 && bm != 16 && bm != 8) return TSP_EINVAL;
     if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
@@ -335,7 +338,9 @@ int tsp_spmm_launch_panels(int bm, int prec, int rowblkblock, int colB_p, const 
     if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES | TSP_LAUNCH_SYNC_RESET | TSP_LAUNCH_TILE_PAIRS))
         return TSP_EINVAL;
     if ((flags & TSP_LAUNCH_LANE_INDICES) && !d_bitmap) return TSP_EINVAL;
-    if ((flags & TSP_LAUNCH_TILE_PAIRS) && !tsp_pairs_supported(bm, prec, w > 0 ? w : tsp::default_chunk_width(bm, colB_p)))
+    if ((flags & TSP_LAUNCH_TILE_PAIRS) &&
+        (!tsp_pairs_supported(bm, prec, w > 0 ? w : tsp::default_chunk_width(bm, colB_p)) ||
+         (prec == TSP_PREC_TF32 && !(flags & TSP_LAUNCH_OPERANDS_TF32))))
         return TSP_EINVAL;
     if (bm != 64 && bm != 16 && bm != 8) return TSP_EINVAL;
     if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
@@ -399,7 +404,30 @@ __global__ __launch_bounds__(256) void round_tf32_kernel(uint32_t *__restrict__ 
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) x[i] = round_tf32_bits(x[i]);
 }
+__global__ __launch_bounds__(256) void split_bf16_kernel(const uint32_t *__restrict__ x, uint32_t *__restrict__ y,
+                                                        size_t n)
+{
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) y[i] = split_bf16_bits(x[i]);
+}
 }  // namespace tsp
+
+int tsp_split_bf16_device(const void *d_src, void *d_dst, size_t n, void *stream)
+{
+    if (n && (!d_src || !d_dst)) return TSP_EINVAL;
+    if (n == 0) return TSP_OK;
+    const size_t b = (n + 255) / 256;
+    tsp::split_bf16_kernel<<<(unsigned)(b < 16384 ? b : 16384), 256, 0, (hipStream_t)stream>>>(
+        (const uint32_t *)d_src, (uint32_t *)d_dst, n);
+    return (int)hipGetLastError();
+}
+
+int tsp_split_bf16_bits(const uint32_t *in, uint32_t *out, size_t n)
+{
+    if (n && (!in || !out)) return TSP_EINVAL;
+    for (size_t i = 0; i < n; ++i) out[i] = tsp::split_bf16_bits(in[i]);
+    return TSP_OK;
+}
 
 int tsp_round_tf32_device(void *d_x, size_t n, void *stream)
 {

@@ -33,6 +33,27 @@ __host__ __device__ inline uint32_t round_tf32_bits(uint32_t x)
     return (x & 0x7f800000u) == 0x7f800000u ? x : r;
 }
 
+// A tf32 value split into two bf16 halves that sum to it exactly, packed in
+// one 32-bit word: high half = the value truncated to bf16 (its top 16
+// bits), low half = the rest (at most 3 significant bits, so exact in
+// bf16).  The tile-pair tf32 kernels multiply such words on bf16 MFMAs.
+// Inf keeps its high half and gets a zero low half; NaN becomes a quiet NaN
+// in both halves (a payload only in the low bits would otherwise leave an
+// Inf high half).  The input must be a tf32 value (low 13 mantissa bits
+// zero), as the plan's rounded copies are.
+__host__ __device__ inline uint32_t split_bf16_bits(uint32_t x)
+{
+    if ((x & 0x7f800000u) == 0x7f800000u) return (x & 0x007fffffu) ? 0x7fc07fc0u : (x & 0xffff0000u);
+    const uint32_t hi = x & 0xffff0000u;
+    float fx, fh;
+    __builtin_memcpy(&fx, &x, 4);
+    __builtin_memcpy(&fh, &hi, 4);
+    const float lo = fx - fh;
+    uint32_t lb;
+    __builtin_memcpy(&lb, &lo, 4);
+    return hi | (lb >> 16);
+}
+
 // Placement of a launch's workgroups on the XCDs.  The hardware deals
 // workgroups to the XCDs round-robin (workgroup b -> XCD b % kXcds), and each
 // XCD has its own L2.  kPlaceContiguous gives each XCD one contiguous eighth

@@ -121,7 +121,7 @@ constexpr int kMinWaves = PR ? (SY && W == 64 && S == 1 ? 5 : 1)
 // consecutive tiles of one task, multiplied together as one 16 x 32 tile
 // with v_mfma_f32_16x16x32_f16 (MFMA K index 16 + k is the second tile's
 // column k); a task with an odd number of tiles ends with a unit whose
-// second half has zero A values and repeats the first tile's B rows.  Half
+// second half has zero A values and zeroed B rows.  Half
 // the MFMAs of the K = 16 form (which runs at half the fp16 rate), half the
 // loop iterations, and twice the B rows in flight per iteration.
 template <int BM, int W, int PREC, int S, bool PK, bool LI, bool SY, bool PR = false>
@@ -145,7 +145,11 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     constexpr bool RND = PREC == TSP_PREC_TF32;
     auto rnd = [](uint32_t x) { return RND ? round_tf32_bits(x) : x; };
     constexpr int BN = tile_bn(BM, PREC);
-    static_assert(!PR || (F16 && BN == 16), "tile pairs: fp16 tiles 16 columns wide");
+    static_assert(!PR || (F16 && BN == 16) || (PREC == kPrecTf32Exact && BM == 8 && W == 64 && !SY),
+                  "tile pairs: fp16 tiles 16 columns wide, or tf32 8-row tiles at 64-column chunks");
+    // tf32 tile pairs: split-bf16 products (v_mfma_f32_16x16x32_bf16) on B
+    // words in the split form of split_bf16_bits
+    constexpr bool SPL = PR && !F16;
     constexpr int BNU = PR ? 2 * BN : BN;    // B rows per unit of work (a tile or a pair)
     constexpr int VV = F16 ? 8 : 4;          // values per 16-byte vector
     constexpr int VPR = W / VV;              // vectors per panel row
@@ -162,8 +166,8 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     // MFMA step i (CB = 4 adjacent columns of row KS*q + i), so the gathered
     // registers feed the MFMAs directly and the panel never passes through
     // LDS.  Each load instruction still covers 4 whole 256-byte rows.
-    constexpr bool DB = !F16 && VPR == 16 && NV == KS && CB == VV;
-    constexpr int AW = F16 ? (BNU == 32 ? 4 : 2) : KS;   // A words per row group
+    constexpr bool DB = !F16 && VPR == 16 && CB == VV && (SPL ? NV == 4 : NV == KS);
+    constexpr int AW = F16 ? (BNU == 32 ? 4 : 2) : SPL ? 4 : KS;   // A words per row group
     using VT = typename std::conditional<F16, _Float16, float>::type;
     using RV = VT __attribute__((ext_vector_type(CB)));     // CB values of one B row
     constexpr int PWD = PK ? BM * BN / 64 : 1;               // packed: bitmap words per tile
@@ -321,7 +325,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         // byte selectors of its occupancy pattern; tf32: the occupancy bits);
         // finish_a_packed (just before the tile's MFMAs) expands them into
         // operand registers.
-        constexpr int NVAL = F16 ? 4 : KS;           // packed: operand values per lane
+        constexpr int NVAL = F16 || SPL ? 4 : KS;    // packed: operand values per lane
         using DecT = typename std::conditional<F16, u2, uint32_t>::type;
         // the lane's first slot bit, the bitmap word holding its NVAL bits
         // (NVAL-bit groups never straddle words) and the bits below it there
@@ -363,6 +367,39 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             else dec = nib;
         };
         // h: which tile of a pair (its words are MFMA K slots 16h .. 16h + 15)
+        // Split-bf16 A (tf32 tile pairs): lane (ln, lq) holds row ln & 7 of
+        // tile lq >> 1 of the pair, columns 4 (lq & 1) .. +3 -- the high bf16
+        // halves in MFMA rows 0-7, the low halves in rows 8-15, each value
+        // doubled into a bf16 pair so that it multiplies both halves of a B
+        // split word (K slots 2d, 2d + 1 of lane group lq are B row 4 lq + d
+        // of the pair's 16 rows, which is tile column 4 (lq & 1) + d).
+        const int sbit = (ln & 7) * 8 + 4 * (lq & 1);
+        const uint64_t sbelow = (1ull << sbit) - 1ull;
+        const uint32_t ssel = ln < 8 ? 0x07060706u : 0x05040504u;
+        // an infinite A value keeps its high half only in the K slot of the B
+        // high halves (slot 2d + 1), so that it never meets a zero low half
+        // of a finite B value (Inf * 0 would turn its row's product into NaN)
+        const uint32_t sinf = (ssel & 0xffff0000u) | 0x0c0cu;
+        auto issue_a_split = [&](const PMeta &m, VT (&raw)[NVAL], DecT &dec) {
+            if constexpr (SPL && PK) {
+                const uint64_t word = lq >= 2 ? m.bw[1][0] : m.bw[0][0];
+                const int vb = lq >= 2 ? m.vbase[1] : m.vbase[0];
+                const int pre = __popcll(word & sbelow);
+                dec = (uint32_t)(word >> sbit) & 15u;
+                const VT *pv = val + vb + pre;       // padded: 4 values are always readable
+#pragma unroll
+                for (int j = 0; j < NVAL; ++j) raw[j] = pv[j];
+            }
+        };
+        // values (fp32 bits, tf32) -> operand words: dst[0][j] is the lane's
+        // half of value j, doubled
+        auto split_words = [&](const uint32_t (&v)[4], uint32_t (&dst)[RG][AW]) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t w = split_bf16_bits(v[j]);
+                dst[0][j] = __builtin_amdgcn_perm(w, w, (v[j] & 0x7fffffffu) == 0x7f800000u ? sinf : ssel);
+            }
+        };
         auto finish_a_packed = [&](const VT (&v)[NVAL], const DecT &dec, uint32_t (&dst)[RG][AW], int h = 0) {
             if constexpr (F16) {
                 const u2 bits = __builtin_bit_cast(u2, h4{v[0], v[1], v[2], v[3]});
@@ -391,7 +428,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
 #pragma unroll
             for (int g = 0; g < RG; ++g) {
                 const int r = 16 * g + ln;
-                if (BM == 8 && ln >= 8) {
+                if (BM == 8 && ln >= 8 && !SPL) {
 #pragma unroll
                     for (int w = 0; w < AW; ++w) dst[g][w] = 0u;
                     continue;
@@ -407,6 +444,11 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                         const u2 hi = *(const u2 *)(tile + r * BN + 16 + 4 * lq);
                         dst[g][2] = hi.x; dst[g][3] = hi.y;
                     }
+                } else if constexpr (SPL) {
+                    // raw values of tile t + (lq >> 1), row ln & 7, columns 4 (lq & 1) .. +3
+                    u4 x = u4{0u, 0u, 0u, 0u};
+                    if (lq < 2 || two) x = *(const u4 *)(tile + (lq >> 1) * (BM * BN) + (ln & 7) * BN + 4 * (lq & 1));
+                    dst[g][0] = x.x; dst[g][1] = x.y; dst[g][2] = x.z; dst[g][3] = x.w;
                 } else {
                     const float *p = tile + r * BN + KS * lq;
                     if constexpr (KS == 2) {
@@ -459,7 +501,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 } else {
                     // the lane's row: i*RPI + lrow, or KS*lrow + i when the
                     // gathered registers are the MFMA operands
-                    auto row = [&](int r) { return DB ? KS * r + i : i * RPI + r; };
+                    auto row = [&](int r) { return DB ? NV * r + i : i * RPI + r; };
                     int v = cs[row(0)];
 #pragma unroll
                     for (int r = 1; r < RPI; ++r) v = lrow == r ? cs[row(r)] : v;
@@ -480,6 +522,21 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         // this wave ran every task of it (a split row-block's tasks are
         // consecutive, as tile_pretreatment emits them).
         auto flush = [&](int first, int last, unsigned rw) {   // rw = rows[last]
+            if constexpr (SPL) {
+                // rows 8-15 of each MFMA block hold the low-half products of
+                // rows 0-7: lane l (< 32) adds lane l + 32's sums.  Where an
+                // infinite B value meets a zero low half of A, the low-half sum
+                // is NaN (0 * Inf) while the high-half sum holds the row's true
+                // infinite result (a zero A value makes the high half NaN too):
+                // an infinite high-half sum is the result.
+#pragma unroll
+                for (int c = 0; c < CB; ++c)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float o = __shfl_xor(acc[0][c][j], 32);
+                        acc[0][c][j] = __builtin_isinf(acc[0][c][j]) ? acc[0][c][j] : acc[0][c][j] + o;
+                    }
+            }
             const int row0 = (int)(rw & 0x7fffffffu);
             bool split = (rw & 0x80000000u) != 0;
             if (split && first < last) {
@@ -615,6 +672,17 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                         }
                     }
                 }
+            } else if constexpr (SPL) {
+                // block c: the split words of the lane's 4 B rows at chunk
+                // column 4 ln + c (its gathered registers), one K = 32 bf16
+                // MFMA covering both tiles of the unit
+                typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+                const bf8 av = __builtin_bit_cast(bf8, u4{a[0][0], a[0][1], a[0][2], a[0][3]});
+#pragma unroll
+                for (int c = 0; c < CB; ++c) {
+                    const bf8 bt = __builtin_bit_cast(bf8, u4{bd[0][c], bd[1][c], bd[2][c], bd[3][c]});
+                    acc[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bt, acc[0][c], 0, 0, 0);
+                }
             } else {
                 const VT *lb = lds + ln * CB;
 #pragma unroll
@@ -671,7 +739,9 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         PMeta pm[S];
         int cid[NV];
         auto issue_a = [&](int t, int s, bool two = false) {
-            if constexpr (PK) {
+            if constexpr (SPL && PK) {
+                issue_a_split(pm[s], araw[s][0], anib[s][0]);
+            } else if constexpr (PK) {
 #pragma unroll
                 for (int h = 0; h < NT; ++h) issue_a_packed(pm[s], h, araw[s][h], anib[s][h]);
             } else {
@@ -679,7 +749,17 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             }
         };
         auto take_a = [&](int s, uint32_t (&acur)[RG][AW]) {
-            if constexpr (PK) {
+            if constexpr (SPL) {
+                uint32_t raw4[RG][AW];
+                if constexpr (PK) {
+                    finish_a_packed(araw[s][0], anib[s][0], raw4);
+                } else {
+#pragma unroll
+                    for (int w = 0; w < AW; ++w) raw4[0][w] = ar[s][0][w];
+                }
+                const uint32_t v[4] = {raw4[0][0], raw4[0][1], raw4[0][2], raw4[0][3]};
+                split_words(v, acur);
+            } else if constexpr (PK) {
 #pragma unroll
                 for (int h = 0; h < NT; ++h) finish_a_packed(araw[s][h], anib[s][h], acur, h);
             } else {
@@ -757,10 +837,18 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 for (int s = 0; s < S; ++s) {
                     if (more && dBt[s] < te) {
                         advance_task(dBt[s]);
+                        if (!dB2[s]) {
+                            // a unit without a second tile gathered the first
+                            // tile's B rows again for its second half: zero them,
+                            // so that its zero A values meet no Inf or NaN
+#pragma unroll
+                            for (int i = 0; i < NV; ++i)
+                                if (prow[i] >= BN) bv[s][i] = u4{0u, 0u, 0u, 0u};
+                        }
                         stage_b(bv[s]);
                         u4 bcur[NV];
 #pragma unroll
-                        for (int i = 0; i < NV; ++i) bcur[i] = u4{0u, 0u, 0u, 0u};
+                        for (int i = 0; i < NV; ++i) bcur[i] = DB ? bv[s][i] : u4{0u, 0u, 0u, 0u};
                         uint32_t acur[RG][AW];
                         take_a(s, acur);
                         if (dIt[s] < te) {
@@ -882,11 +970,14 @@ const void *pick_kernel(int prec)
     return (const void *)&spmm_kernel<BM, W, TSP_PREC_TF32, S, PK, LI, SY>;
 }
 
-// Tile-pair instantiations exist for fp16 only (nullptr for tf32).
+// Tile-pair instantiations: fp16, and tf32 operands that are tf32 values
+// already for 8-row tiles at 64-column chunks (nullptr otherwise).
 template <int BM, int W, int S, bool PK, bool LI, bool SY>
 const void *pick_pair_kernel(int prec)
 {
     if (prec == TSP_PREC_FP16) return (const void *)&spmm_kernel<BM, W, TSP_PREC_FP16, S, PK, LI, SY, true>;
+    if constexpr (BM == 8 && W == 64 && !SY)
+        if (prec == kPrecTf32Exact) return (const void *)&spmm_kernel<BM, W, kPrecTf32Exact, S, PK, LI, SY, true>;
     return nullptr;
 }
 

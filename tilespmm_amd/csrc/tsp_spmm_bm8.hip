@@ -1,7 +1,8 @@
 // tsp_spmm_bm8.hip -- the 8-row instantiations of spmm_kernel (tsp_spmm.hpp):
 // the (chunk width, pipeline depth) pairs of the dense A format and of both
 // packed forms (scalar and lane-loaded column indices), plus the
-// panel-synchronised dense sweep, and the fp16 tile-pair forms of each.
+// panel-synchronised dense sweep, and the tile-pair forms (fp16; tf32 at
+// 64-column chunks).
 #include "tsp_spmm.hpp"
 
 namespace tsp {
@@ -9,7 +10,7 @@ namespace tsp {
 const void *select_kernel_bm8(int prec, int w, int s, bool packed, bool lane_idx, bool sync, bool pair)
 {
     if (pair) {
-        // tile pairs (fp16): 64- and 128-column chunks
+        // tile pairs: fp16 at 64- and 128-column chunks, tf32 at 64
 #define TSP_P(Wv, Sv, PKv, LIv, SYv)                                                  \
     if (w == Wv && s == Sv && packed == PKv && lane_idx == LIv && sync == SYv) \
         return pick_pair_kernel<8, Wv, Sv, PKv, LIv, SYv>(prec);

@@ -76,6 +76,8 @@ double now_ms()
 struct tsp_plan {
     int dev = 0, prec = 0, rowA = 0, colA = 0, colB_p = 0;
     void *d_B = nullptr;          // colA rows of B, then hot_cap spare rows for hot-row copies
+    void *d_Bs = nullptr;         // tf32 plans: the same rows as split-bf16 words, made when a class first
+                                  // uses tile pairs (their kernels read B in that form)
     int hot_cap = 0;              // spare rows after row colA
     int nhot = 0;                 // hot slots in use: row colA + s copies B row d_hot[s]
     int *d_hot = nullptr;
@@ -215,6 +217,12 @@ static int upload_dense(tsp_plan *p, ClassDev &c)
     return round_tf32_copy(p, c.d_val, c.m->dnssize);
 }
 
+// A class reads B as split-bf16 words (tf32 tile pairs) or as values.
+static bool reads_split_b(const tsp_plan *p, const ClassDev &c)
+{
+    return p->prec == TSP_PREC_TF32 && c.var_pr;
+}
+
 // Launch one class on `stream` (its own stream unless given another).
 static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
 {
@@ -237,7 +245,8 @@ static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
         return st;
     }
     return tsp_spmm_launch_ex(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val, pk ? c.d_bmp : nullptr,
-                              pk ? c.d_vptr : nullptr, c.d_rows, c.d_colstart, p->d_B, p->d_C, c.d_colidx, p->rowA,
+                              pk ? c.d_vptr : nullptr, c.d_rows, c.d_colstart, reads_split_b(p, c) ? p->d_Bs : p->d_B,
+                              p->d_C, c.d_colidx, p->rowA,
                               stream ? stream : c.stream, c.var_w, c.var_s, c.var_tpw, c.var_order, c.place, flags);
 }
 
@@ -336,13 +345,30 @@ extern "C" int tsp_plan_get_lane_indices(tsp_plan *p, int bm)
     return -1;
 }
 
+// The split-bf16 form of a tf32 plan's B (tf32 tile pairs read it): its
+// canonical rows, converted once, and the spare hot-row slots, which every
+// step refills from those rows.
+static int ensure_split_b(tsp_plan *p)
+{
+    if (p->d_Bs) return TSP_OK;
+    const size_t n = ((size_t)p->colA + (size_t)p->hot_cap) * (size_t)p->colB_p;
+    TSP_TRY(tsp_device_sync());
+    TSP_TRY(tsp_malloc(&p->d_Bs, n * sizeof(float)));
+    TSP_TRY(tsp_split_bf16_device(p->d_B, p->d_Bs, (size_t)p->colA * (size_t)p->colB_p, nullptr));
+    if (p->nhot)
+        TSP_TRY(tsp_hot_rows_gather(p->d_Bs, p->colA, (long long)sizeof(float) * p->colB_p, p->d_hot, p->nhot,
+                                    nullptr));
+    return tsp_device_sync();
+}
+
 extern "C" int tsp_plan_set_pairs(tsp_plan *p, int bm, int on)
 {
     if (p) ++p->version;          // any captured graph is stale now
     if (!p || (on != 0 && on != 1)) return TSP_EINVAL;
     for (ClassDev &c : p->cls)
         if (c.bm == bm) {
-            if (on && (p->prec != TSP_PREC_FP16 || bm == 64)) return TSP_EINVAL;
+            if (on && (bm == 64 || (p->prec == TSP_PREC_TF32 && bm != 8))) return TSP_EINVAL;
+            if (on && p->prec == TSP_PREC_TF32) TSP_TRY(ensure_split_b(p));
             c.var_pr = on;
             return TSP_OK;
         }
@@ -411,6 +437,7 @@ extern "C" int tsp_plan_destroy(tsp_plan *p)
         if (c.dev_built) tsp_tile_destroy(&c.own);
     }
     tsp_free(p->d_B);
+    tsp_free(p->d_Bs);
     tsp_free(p->d_hot);
     tsp_free(p->d_flush);
     tsp_free(p->d_C);
@@ -633,9 +660,19 @@ static ClassDev *only_class(tsp_plan *p)
 static long long b_row_bytes(const tsp_plan *p) { return (long long)tsph::val_size(p->prec) * p->colB_p; }
 
 // Copy the hot B rows into their slots (on main, ahead of the class kernels).
+// Hot-row copies into the spare rows of each form of B that an active class
+// reads.
 static int hot_gather(tsp_plan *p)
 {
-    return p->nhot ? tsp_hot_rows_gather(p->d_B, p->colA, b_row_bytes(p), p->d_hot, p->nhot, p->main) : TSP_OK;
+    if (!p->nhot) return TSP_OK;
+    bool plain = false, split = false;
+    for (const ClassDev &c : p->cls)
+        if (c.active() && c.ntasks > 0) (reads_split_b(p, c) ? split : plain) = true;
+    if (plain || !split)
+        TSP_TRY(tsp_hot_rows_gather(p->d_B, p->colA, b_row_bytes(p), p->d_hot, p->nhot, p->main));
+    if (split && p->d_Bs)
+        TSP_TRY(tsp_hot_rows_gather(p->d_Bs, p->colA, b_row_bytes(p), p->d_hot, p->nhot, p->main));
+    return TSP_OK;
 }
 
 static int fork_join_once(tsp_plan *p, int reps)
@@ -1122,8 +1159,9 @@ static int tune_class(tsp_plan *p, ClassDev &c)
     //    pipeline holds more B gathers in flight per wave but costs registers
     //    (occupancy); lane-loaded indices save the select chain for a vector
     //    load.  fp16 8- and 16-row classes also try tile pairs (two tiles per
-    //    K = 32 MFMA) at 64- and 128-column chunks, with the same depths and
-    //    index modes (depth 1-2 on dense tiles).  The fastest option wins
+    //    K = 32 MFMA) at 64- and 128-column chunks, tf32 8-row classes at 64
+    //    (split-bf16 products), with the same depths and index modes (depth
+    //    1-2 on dense tiles).  The fastest option wins
     //    unless it is within 1% of step 3's choice at depth 1 with scalar
     //    indices (comparing each option with the best so far instead would
     //    make the pick depend on the order).
@@ -1140,9 +1178,11 @@ static int tune_class(tsp_plan *p, ClassDev &c)
         for (int li = 0; li < nli; ++li)
             for (int st = 1; st <= (wd == 256 ? 2 : 3); ++st) dopt.push_back({d.w, d.order, d.place, st, li, 0, 1e30});
     }
-    if (p->prec == TSP_PREC_FP16 && c.bm != 64)
+    const bool pair_ok = p->prec == TSP_PREC_FP16 ? c.bm != 64 : c.bm == 8;
+    if (pair_ok && p->prec == TSP_PREC_TF32) TSP_TRY(ensure_split_b(p));
+    if (pair_ok)
         for (int w : {64, 128}) {
-            if (p->colB_p % w != 0) continue;
+            if (p->colB_p % w != 0 || !tsp_pairs_supported(c.bm, p->prec, w)) continue;
             const int nch = p->colB_p / w;
             // the kept order and placement, where this width allows them
             int place = c.place, order = nch >= 2 ? (c.var_order ? c.var_order : 1) : 0;
@@ -1419,6 +1459,14 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
                 TSP_TRY(tsp_plan_set_panels(p, c.bm, 0, 1));
                 TSP_TRY(tune_class(p, c));
             }
+        }
+        // the split form of B stays only if a tuned class reads it
+        bool split = false;
+        for (ClassDev &c : p->cls) split |= c.active() && reads_split_b(p, c);
+        if (p->d_Bs && !split) {
+            TSP_TRY(tsp_device_sync());
+            TSP_TRY(tsp_free(p->d_Bs));
+            p->d_Bs = nullptr;
         }
         t3 = now_ms();
     }
