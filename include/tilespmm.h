@@ -210,9 +210,12 @@ int tsp_plan_get_variant(tsp_plan *plan, int bm, int *w, int *stages, int *tasks
 /* Workgroup placement of one class on the XCDs (TSP_PLACE_CONTIGUOUS or
  * TSP_PLACE_INTERLEAVED, see tsp_spmm_launch_placed); tsp_plan_tune times
  * both.  get returns -1 on a bad argument. */
-/* Lane-loaded column indices (TSP_LAUNCH_LANE_INDICES) for a class on the
- * packed format: 1 on, 0 off (64-row classes: off only); tsp_plan_tune picks.
- * get returns -1 on a bad argument. */
+/* Lane-loaded column indices (TSP_LAUNCH_LANE_INDICES) for a class: 1 on,
+ * 0 off (64-row classes: off only); tsp_plan_tune picks.  The setting applies
+ * to the launches that have a lane-loaded kernel: every packed-format
+ * variant, and dense variants at chunks of up to 128 columns without tile
+ * pairs or the panel sweep.  get returns whether the class's launches load
+ * indices per lane (1 / 0), or -1 on a bad argument. */
 int tsp_plan_set_lane_indices(tsp_plan *plan, int bm, int on);
 int tsp_plan_get_lane_indices(tsp_plan *plan, int bm);
 /* Tile pairs (TSP_LAUNCH_TILE_PAIRS) for one class: 1 on, 0 off; fp16 8- and

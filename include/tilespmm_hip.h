@@ -195,12 +195,15 @@ int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const 
  * The plan rounds its copies of A and B once when they enter it and
  * launches this way.  No counterpart in the reference. */
 #define TSP_LAUNCH_OPERANDS_TF32 1
-/* TSP_LAUNCH_LANE_INDICES (packed A format only): each lane reads the
- * column indices of its B rows with one vector load instead of the scalar
- * loads plus a per-lane select chain; same result, fewer VALU instructions
- * per tile, one more vector memory instruction.  The plan's tuning picks
- * per class (faster on the gather-bound RMAT and power-law fp16 classes,
- * slower on banded and block-sparse ones). */
+/* TSP_LAUNCH_LANE_INDICES (8- and 16-row classes: every packed-format
+ * variant; dense tiles at chunk widths up to 128, without tile pairs or the
+ * panel sweep): each lane reads the column indices of its B rows with one
+ * vector load instead of the scalar loads plus a per-lane select chain; same
+ * result, fewer VALU instructions per tile, one more vector memory
+ * instruction.  The plan's tuning picks per class (faster on the
+ * gather-bound RMAT and power-law fp16 classes and on small launch-bound
+ * plans, slower on banded and block-sparse ones).  Other launches with the
+ * flag fail with TSP_EINVAL. */
 #define TSP_LAUNCH_LANE_INDICES 2
 /* TSP_LAUNCH_TILE_PAIRS (fp16 8- and 16-row tiles, chunk width w 64 or 128;
  * tf32 8-row tiles, w 64): each wave multiplies two consecutive tiles of a

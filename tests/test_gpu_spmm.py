@@ -115,9 +115,9 @@ def test_random_all_classes(gpu, orc, prec, colB):
 @pytest.mark.parametrize("prec", [0, 1])
 def test_every_kernel_variant(gpu, orc, prec):
     """Every (chunk width, pipeline depth, tasks per wave, scalar or
-    lane-loaded column indices on the packed format) variant of every class,
-    with every XCD placement its chunk count allows, gives the oracle's
-    result, split tasks included."""
+    lane-loaded column indices) variant of every class and A format, with
+    every XCD placement its chunk count allows, gives the oracle's result,
+    split tasks included."""
     tsp = gpu
     rng = np.random.default_rng(50 + prec)
     A = random_matrix(tsp, rng, 611, 509, 45, prec, heavy_rows=4)
@@ -134,7 +134,7 @@ def test_every_kernel_variant(gpu, orc, prec):
                 plan.set_format(bm, fmt)
                 assert plan.get_format(bm) == fmt
                 for w in ((32, 64) if bm == 64 else (32, 64, 128)):
-                    for s, li in [(s, li) for s in (1, 2, 3) for li in ((0, 1) if fmt == 2 else (0,))]:
+                    for s, li in [(s, li) for s in (1, 2, 3) for li in ((0,) if bm == 64 else (0, 1))]:
                         for tpw, order in ((1, 1), (3, 2), (0, 0)):
                             for place in ((0, 1, 2) if cbp // w in (2, 4, 8) else (0, 1)):
                                 tag = (f"prec={prec} bm={bm} fmt={fmt} w={w} s={s} lane_idx={li} tpw={tpw} "
@@ -953,9 +953,18 @@ def test_tf32_prerounded_launch_matches_rounding_launch(gpu, orc, bm):
         ok[row3] = False
         Cref, Cabs = reference(orc, A, B, colB)
         assert_close(c1[ok, :colB], Cref[ok], Cabs[ok], 1, f"bm {bm}")
-        # an unknown flag is refused before any launch
+        # an unknown flag is refused before any launch, and so are lane-loaded
+        # indices where no kernel has them (64-row tiles)
         assert hip.tsp_spmm_launch_ex(bm, 1, len(rows), cbp, bufs["valr"], None, None, bufs["rows"], bufs["cs"],
-                                      bufs["Br"], bufs["C2"], bufs["col"], A.rows, None, 0, 0, 0, 0, 0, 2) != 0
+                                      bufs["Br"], bufs["C2"], bufs["col"], A.rows, None, 0, 0, 0, 0, 0, 64) != 0
+        li = hip.tsp_spmm_launch_ex(bm, 1, len(rows), cbp, bufs["valr"], None, None, bufs["rows"], bufs["cs"],
+                                    bufs["Br"], bufs["C2"], bufs["col"], A.rows, None, 0, 0, 0, 0, 0, 3)
+        if bm == 64:
+            assert li != 0
+        else:
+            # dense tiles with lane-loaded indices: the same result bit for bit
+            assert li == 0 and hip.tsp_device_sync() == 0
+            assert np.array_equal(down("C2", Cz).view(np.uint32), c1.view(np.uint32))
         if bm != 64:
             # packed A with lane-loaded indices and 64-column chunks (the
             # gathered B registers are the MFMA operands, no LDS panel): the

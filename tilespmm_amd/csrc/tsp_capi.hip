@@ -306,7 +306,6 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
                        int placement, int flags)
 {
     if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES | TSP_LAUNCH_TILE_PAIRS)) return TSP_EINVAL;
-    if ((flags & TSP_LAUNCH_LANE_INDICES) && !d_bitmap) return TSP_EINVAL;
     if ((flags & TSP_LAUNCH_TILE_PAIRS) &&
         (!tsp_pairs_supported(bm, prec, w > 0 ? w : tsp::default_chunk_width(bm, colB_p)) ||
          (prec == TSP_PREC_TF32 && !(flags & TSP_LAUNCH_OPERANDS_TF32))))
@@ -337,7 +336,6 @@ int tsp_spmm_launch_panels(int bm, int prec, int rowblkblock, int colB_p, const 
 {
     if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES | TSP_LAUNCH_SYNC_RESET | TSP_LAUNCH_TILE_PAIRS))
         return TSP_EINVAL;
-    if ((flags & TSP_LAUNCH_LANE_INDICES) && !d_bitmap) return TSP_EINVAL;
     if ((flags & TSP_LAUNCH_TILE_PAIRS) &&
         (!tsp_pairs_supported(bm, prec, w > 0 ? w : tsp::default_chunk_width(bm, colB_p)) ||
          (prec == TSP_PREC_TF32 && !(flags & TSP_LAUNCH_OPERANDS_TF32))))

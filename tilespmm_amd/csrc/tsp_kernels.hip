@@ -127,7 +127,6 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
 {
     const bool packed = bmp != nullptr;
     if (packed && (bm == 64 || !vptr)) return TSP_EINVAL;
-    if (lane_idx && !packed) return TSP_EINVAL;          // lane-loaded indices: packed kernels only
     if (placement != kPlaceContiguous && placement != kPlaceInterleaved && placement != kPlaceChunkXcd)
         return TSP_EINVAL;
     int nchunks = 0, cm = 0;

@@ -203,7 +203,11 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             lut_all[wid][lane] = u2{sel[0] | sel[1] << 16, sel[2] | sel[3] << 16};
         }
     }
-    const long long nranges = ((long long)ntasks + tasks_per_wave - 1) / tasks_per_wave;
+    // (one task per wave and one chunk, the common launch of small plans,
+    // skip the 64-bit divisions: each costs dozens of scalar instructions,
+    // which a launch-bound kernel pays in full)
+    const long long nranges =
+        tasks_per_wave == 1 ? (long long)ntasks : ((long long)ntasks + tasks_per_wave - 1) / tasks_per_wave;
     const bool sync = SY && sy.cnt != nullptr;
     const int xcd = blockIdx.x % kXcds;
     // Counters of generation g on this XCD: the waves registered for it, then
@@ -240,18 +244,27 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         int lp = -1;                     // last panel this wave announced (sync)
         const int k0 = range * tasks_per_wave;
         const int k1 = min(ntasks, k0 + tasks_per_wave);
+        // One batch of scalar loads: the range's tile bounds, the first task's
+        // end and its schedule word (first row, split flag; a task's word is
+        // read when the task starts, so that a flush never waits for it).
         const int tb = uload(colstart, k0), te = uload(colstart, k1);
+        int kend = uload(colstart, k0 + 1);
+        unsigned rwk = uload(rows, k0);
         if (tb >= te) return;                        // every task of the range is empty
         // a wave waits only for the waves that registered before it looks, so
         // a wave that is not resident (yet) holds nobody back
         if (sync && lane == 0) bump(g, 0);
         int k = k0;
-        int kend = uload(colstart, k0 + 1);
-        while (kend <= tb) kend = uload(colstart, ++k + 1);  // skip leading empty tasks
-        int gfirst = k;                  // first task of the accumulation group
-        // the current task's schedule word (first row, split flag), read when
-        // the task starts so that a flush never waits for it
-        unsigned rwk = uload(rows, k);
+        int gfirst = k0;                 // first task of the accumulation group
+        // Skip leading empty tasks.  Called once the first column-index loads
+        // are in flight, so that the common case (none) adds no round trip
+        // before them.
+        auto skip_empty = [&]() {
+            if (kend > tb) return;
+            while (kend <= tb) kend = uload(colstart, ++k + 1);
+            gfirst = k;
+            rwk = uload(rows, k);
+        };
         const int col0 = chunk * W;
         // Before the B loads of a tile whose first column is fc: announce its
         // panel q and wait (bounded) until every registered wave of this XCD
@@ -793,6 +806,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
             // ending at ukend) runs 2S units ahead of the compute front; a
             // slot's descriptors follow its unit from the index load (dI) to
             // the B/A loads and the compute (dB).
+            skip_empty();
             int ut = tb, uk = k, ukend = kend;
             auto next_unit = [&](int &first, bool &two) {
                 first = ut;
@@ -882,6 +896,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 load_cs(tb + s, cs[s]);
                 load_meta(tb + s, pm[s]);
             }
+        skip_empty();
 #pragma unroll
         for (int s = 0; s < S; ++s)
             if (tb + s < te) {
@@ -951,8 +966,12 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                 // (the live B working set of a phase is one chunk's columns);
                 // otherwise the chunks of one range are neighbours (the A
                 // tiles are reused from L2).
-                r = chunk_major ? gw % nranges : gw / nchunks;
-                chunk = chunk_major ? (int)(gw / nranges) : (int)(gw - r * nchunks);
+                if (nchunks == 1) {
+                    r = gw;
+                } else {
+                    r = chunk_major ? gw % nranges : gw / nchunks;
+                    chunk = chunk_major ? (int)(gw / nranges) : (int)(gw - r * nchunks);
+                }
             }
         }
         if (r >= 0) run(g, (int)r, chunk);

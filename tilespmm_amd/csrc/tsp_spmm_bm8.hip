@@ -1,6 +1,7 @@
 // tsp_spmm_bm8.hip -- the 8-row instantiations of spmm_kernel (tsp_spmm.hpp):
-// the (chunk width, pipeline depth) pairs of the dense A format and of both
-// packed forms (scalar and lane-loaded column indices), plus the
+// the (chunk width, pipeline depth) pairs of the dense A format and of the
+// packed format, each with scalar or lane-loaded column indices (dense: at
+// chunks of up to 128 columns), plus the
 // panel-synchronised dense sweep, and the tile-pair forms (fp16; tf32 at
 // 64-column chunks).
 #include "tsp_spmm.hpp"
@@ -28,6 +29,10 @@ const void *select_kernel_bm8(int prec, int w, int s, bool packed, bool lane_idx
         return pick_kernel<8, Wv, Sv, PKv, LIv, SYv>(prec);
 #define X(Wv, Sv) TSP_K(Wv, Sv, false, false, false)
     X(32, 1) X(32, 2) X(32, 3) X(64, 1) X(64, 2) X(64, 3) X(128, 1) X(128, 2) X(128, 3) X(256, 1) X(256, 2)
+#undef X
+    // dense tiles with lane-loaded column indices (chunks of up to 128 columns)
+#define X(Wv, Sv) TSP_K(Wv, Sv, false, true, false)
+    X(32, 1) X(32, 2) X(32, 3) X(64, 1) X(64, 2) X(64, 3) X(128, 1) X(128, 2) X(128, 3)
 #undef X
 #define X(Wv, Sv) TSP_K(Wv, Sv, true, false, false) TSP_K(Wv, Sv, true, true, false)
     X(32, 1) X(32, 2) X(32, 3) X(64, 1) X(64, 2) X(64, 3) X(128, 1) X(128, 2) X(128, 3) X(256, 1) X(256, 2)

@@ -35,7 +35,8 @@ struct ClassDev {
     int th = 0;
     int ntasks = 0;
     int var_w = 0, var_s = 0, var_tpw = 0, var_order = 0;   // kernel variant, 0 = library default
-    int var_li = 0;               // packed format: lane-loaded column indices (TSP_LAUNCH_LANE_INDICES)
+    int var_li = 0;               // lane-loaded column indices (TSP_LAUNCH_LANE_INDICES), where a kernel has them
+    int wdef = 0;                 // the library's default chunk width for this class
     int var_pr = 0;               // tile pairs (TSP_LAUNCH_TILE_PAIRS; fp16 8-/16-row, 64-/128-column chunks)
     int fmt = 1;                  // A format on the device: 1 dense tiles, 2 bitmap-packed
     bool pack_ok = false;         // packed format is worth trying (fewer bytes)
@@ -223,13 +224,22 @@ static bool reads_split_b(const tsp_plan *p, const ClassDev &c)
     return p->prec == TSP_PREC_TF32 && c.var_pr;
 }
 
+// The class's launches load column indices per lane: asked for, and a
+// lane-loaded kernel exists for the variant (every packed one; dense ones at
+// chunks of up to 128 columns, without tile pairs or the panel sweep).
+static bool lane_indices_on(const ClassDev &c)
+{
+    if (!c.var_li || c.bm == 64) return false;
+    return c.fmt == 2 || ((c.var_w ? c.var_w : c.wdef) <= 128 && !c.var_pr && c.panel == 0);
+}
+
 // Launch one class on `stream` (its own stream unless given another).
 static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
 {
     if (!c.active() || c.ntasks == 0) return TSP_OK;
     const bool pk = c.fmt == 2;
     const int flags = (p->prec == TSP_PREC_TF32 ? TSP_LAUNCH_OPERANDS_TF32 : 0) |
-                      (pk && c.var_li ? TSP_LAUNCH_LANE_INDICES : 0) | (c.var_pr ? TSP_LAUNCH_TILE_PAIRS : 0);
+                      (lane_indices_on(c) ? TSP_LAUNCH_LANE_INDICES : 0) | (c.var_pr ? TSP_LAUNCH_TILE_PAIRS : 0);
     if (c.panel > 0) {
         // the counters are zeroed whenever the launch arguments change
         const std::vector<long long> sig{c.ntasks, c.var_w, c.var_s, c.var_tpw, c.var_order, c.place,
@@ -341,7 +351,7 @@ extern "C" int tsp_plan_get_lane_indices(tsp_plan *p, int bm)
 {
     if (!p) return -1;
     for (ClassDev &c : p->cls)
-        if (c.bm == bm) return c.var_li;
+        if (c.bm == bm) return lane_indices_on(c) ? 1 : 0;
     return -1;
 }
 
@@ -479,8 +489,11 @@ static int plan_begin(std::unique_ptr<tsp_plan> &p, int device_id, int rowA, int
 
 // Per active class: schedule buffers (a row-block splits into at most its
 // tile count of tasks) and the class stream.
-static int class_finish(ClassDev &c)
+static int class_finish(tsp_plan *p, ClassDev &c)
 {
+    tsp_kernel_info k;
+    TSP_TRY(tsp_kernel_probe(c.bm, p->prec, p->colB_p, &k));
+    c.wdef = k.cols_per_task;
     c.cap_tasks = (long long)c.m->tilem + c.m->tilenum;
     TSP_TRY(tsp_malloc((void **)&c.d_rows, sizeof(unsigned) * (size_t)c.cap_tasks));
     TSP_TRY(tsp_malloc((void **)&c.d_colstart, sizeof(int) * ((size_t)c.cap_tasks + 1)));
@@ -528,7 +541,7 @@ extern "C" int tsp_plan_create(tsp_plan **out, int device_id, Tile_matrix *m64, 
         if ((st = upload_dense(p.get(), c))) return fail(st);
         if ((st = tsp_malloc((void **)&c.d_colidx, sizeof(int) * nt * c.m->bn))) return fail(st);
         if ((st = tsp_memcpy_h2d(c.d_colidx, c.m->tile_colidx, sizeof(int) * nt * c.m->bn))) return fail(st);
-        if ((st = class_finish(c))) return fail(st);
+        if ((st = class_finish(p.get(), c))) return fail(st);
     }
     if ((st = plan_end(p.get()))) return fail(st);
     *out = p.release();
@@ -618,7 +631,7 @@ extern "C" int tsp_plan_create_csr(tsp_plan **out, int device_id, const tsp_sub_
         ClassDev &c = p->cls[i];
         c.bm = bms[i];
         if ((st = class_from_csr(p.get(), c, ss[i]))) return fail(st);
-        if (c.active() && (st = class_finish(c))) return fail(st);
+        if (c.active() && (st = class_finish(p.get(), c))) return fail(st);
     }
     if (tile_ms) *tile_ms = now_ms() - t0;
     if ((st = plan_end(p.get()))) return fail(st);
@@ -1152,8 +1165,9 @@ static int tune_class(tsp_plan *p, ClassDev &c)
                         place_name[wo[j].place], wms[j], j == bw ? "  <- kept" : "");
     }
 
-    // 4. pipeline depth (1-3 tiles in flight per wave) x, on the packed
-    //    format, scalar or lane-loaded column indices, for step 3's choice and
+    // 4. pipeline depth (1-3 tiles in flight per wave) x scalar or
+    //    lane-loaded column indices (packed format, or dense tiles at chunks
+    //    of up to 128 columns), for step 3's choice and
     //    for its runner-up when that was within 3% (a width that wins at
     //    depth 1 can lose once both are tuned); the rest as kept.  A deeper
     //    pipeline holds more B gathers in flight per wave but costs registers
@@ -1175,7 +1189,7 @@ static int tune_class(tsp_plan *p, ClassDev &c)
     std::vector<DOpt> dopt;
     for (const WOpt &d : dw) {
         const int wd = d.w ? d.w : k.cols_per_task;
-        for (int li = 0; li < nli; ++li)
+        for (int li = 0; li < (c.fmt == 2 || (wd <= 128 && c.bm != 64) ? 2 : 1); ++li)
             for (int st = 1; st <= (wd == 256 ? 2 : 3); ++st) dopt.push_back({d.w, d.order, d.place, st, li, 0, 1e30});
     }
     const bool pair_ok = p->prec == TSP_PREC_FP16 ? c.bm != 64 : c.bm == 8;
