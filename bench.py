@@ -363,7 +363,7 @@ def measure(tsp, hip, config, prec, colB, args, headline):
     hip.tsp_device_sync()
     # a cross-check over a long window (at least 200 ms)
     long_reps = int(min(100000, max(args.steps, np.ceil(200.0 / max(ms, 1e-4)))))
-    ms_long = plan.time(long_reps)
+    ms_long, submit_long = plan.time_ex(long_reps)
     tflops = 2.0 * A.nnz * colB / (ms * 1e-3) / 1e12
 
     # per-class kernel time, each class alone on the stream a step launches it on
@@ -440,7 +440,10 @@ def measure(tsp, hip, config, prec, colB, args, headline):
            "th": list(th), "tilenum": tilenum, "hot_rows": hot_n, "hot_bytes": hot_b,
            "ms_per_step": ms, "tflops": tflops, "steps": args.steps, "window_ms": ms * args.steps,
            "long_window": {"steps": long_reps, "ms_per_step": round(ms_long, 6),
-                           "tflops": round(2.0 * A.nnz * colB / (ms_long * 1e-3) / 1e12, 4)},
+                           "tflops": round(2.0 * A.nnz * colB / (ms_long * 1e-3) / 1e12, 4),
+                           # host wall time per step to submit the launches: about
+                           # ms_per_step when the steps are bound by the launch rate
+                           "host_submit_ms_per_step": round(submit_long, 6)},
            "warmup_clock": {"steps": wit, "gfx_mhz": mhz},
            "roofline": roof, "classes": cls, "pre_ms": pre,
            "replay": pins_of(plan, th, cls)}

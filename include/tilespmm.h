@@ -276,6 +276,12 @@ int tsp_plan_warmup_clock(tsp_plan *plan, int max_iters, int *iters_run, unsigne
 int tsp_plan_warmup(tsp_plan *plan, int max_iters);
 /* Time `reps` back-to-back runs bracketed by events on the plan's main stream. */
 int tsp_plan_time(tsp_plan *plan, int reps, double *ms_per_iter);
+/* The same, plus *submit_ms_per_iter (may be NULL): the host's wall time per
+ * run to submit the runs, until the last launch call returns.  When it is
+ * about the event time per run, the runs are bound by the host's launch
+ * rate (a few microseconds per HIP launch) rather than by the kernels.  No
+ * counterpart in the reference. */
+int tsp_plan_time_ex(tsp_plan *plan, int reps, double *ms_per_iter, double *submit_ms_per_iter);
 /* Steps replayed from a HIP graph.  No counterpart in the reference, which
  * launches every kernel from the host; for callers that repeat the product
  * many times (iterative methods, serving), where steps of a few

@@ -606,6 +606,30 @@ def test_tuned_plan_and_determinism(gpu, orc):
     assert np.array_equal(C2, C3)
 
 
+def test_time_ex_reports_host_submission(gpu):
+    """tsp_plan_time_ex: the event time per step and the host's submission
+    time per step, both positive; the host cannot finish submitting much
+    later than the GPU finishes running what it submitted, and a step's
+    submission stays within a launch's few microseconds (the plan adds no
+    host work of its own per step)."""
+    tsp = gpu
+    A, B, colB, cbp = tsp.gen_config(1)
+    subs = tsp.matrix_split(A, 5.0, 3.0)
+    tiles = [tsp.tile_create(s, A.cols, b, 0) for s, b in zip(subs, (64, 16, 8))]
+    plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, 0, B)
+    try:
+        plan.set_th(8, 8, 8)
+        plan.run(zero_c=True)
+        ms, sub = plan.time_ex(500)
+        assert plan.time(10) > 0
+        say(f"C1 step {ms * 1e3:.2f} us, host submission {sub * 1e3:.2f} us")
+        assert ms > 0 and sub > 0
+        assert sub < 1.5 * ms + 0.002
+        assert sub < 0.05
+    finally:
+        plan.close()
+
+
 @pytest.mark.parametrize("config", [2, 3])
 def test_config_full_parity(gpu, orc, config):
     tsp = gpu

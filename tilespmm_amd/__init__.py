@@ -255,6 +255,7 @@ HOST_SYMBOLS = {
     "tsp_plan_warmup": (C.c_int, [_P, C.c_int]),
     "tsp_plan_warmup_clock": (C.c_int, [_P, C.c_int, _IP, C.POINTER(C.c_uint)]),
     "tsp_plan_time": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double)]),
+    "tsp_plan_time_ex": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "tsp_plan_graph_capture": (C.c_int, [_P, C.c_int]),
     "tsp_plan_graph_run": (C.c_int, [_P, C.c_int]),
     "tsp_plan_graph_time": (C.c_int, [_P, C.c_int, C.POINTER(C.c_double)]),
@@ -742,6 +743,12 @@ class Plan:
         ms = C.c_double()
         _check("tsp_plan_time", load()[1].tsp_plan_time(self.p, reps, C.byref(ms)))
         return ms.value
+
+    def time_ex(self, reps: int):
+        """(ms per step from events, host ms per step to submit the steps)."""
+        ms, sub = C.c_double(), C.c_double()
+        _check("tsp_plan_time_ex", load()[1].tsp_plan_time_ex(self.p, reps, C.byref(ms), C.byref(sub)))
+        return ms.value, sub.value
 
     def graph_capture(self, steps: int) -> None:
         """Capture `steps` steps into a HIP graph (tsp_plan_graph_capture)."""

@@ -803,17 +803,28 @@ extern "C" int tsp_plan_run(tsp_plan *p, int zero_c)
 // the three class streams between two events, src/csr2tile.h:1043-1055).
 extern "C" int tsp_plan_time(tsp_plan *p, int reps, double *ms)
 {
+    return tsp_plan_time_ex(p, reps, ms, nullptr);
+}
+
+// The same, plus the host's wall time to submit the steps (until the last
+// launch call returns): when it is about the event time per step, the steps
+// are bound by the host's launch rate rather than by the kernels.
+extern "C" int tsp_plan_time_ex(tsp_plan *p, int reps, double *ms, double *submit_ms)
+{
     if (!p || reps <= 0 || !ms) return TSP_EINVAL;
     void *start = nullptr;
     TSP_TRY(tsp_event_create(&start));
     std::unique_ptr<void, int (*)(void *)> guard(start, tsp_event_destroy);
     TSP_TRY(tsp_event_record(start, p->main));
+    const double t0 = now_ms();
     TSP_TRY(fork_join(p, reps));
+    const double t1 = now_ms();
     TSP_TRY(tsp_event_record(p->ev1, p->main));
     TSP_TRY(tsp_event_sync(p->ev1));
     float t = 0.f;
     TSP_TRY(tsp_event_elapsed_ms(&t, start, p->ev1));
     *ms = (double)t / reps;
+    if (submit_ms) *submit_ms = (t1 - t0) / reps;
     return TSP_OK;
 }
 
