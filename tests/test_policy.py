@@ -115,7 +115,7 @@ def all_records():
 
 def test_policy_against_exhaustive_tuning(tsp):
     """On its training sweeps (344 cases, 43 matrices) the shipped tree is
-    x1.007 of the exhaustive optimum on average and x1.22 at worst; the
+    x1.010 of the exhaustive optimum on average and x1.23 at worst; the
     provisional single-leaf table (candidate 24) is x1.14 (worst x2.79)."""
     g, d = tsp.policy_candidates()
     slow = []
@@ -126,18 +126,20 @@ def test_policy_against_exhaustive_tuning(tsp):
         a = [i for i in range(len(g)) if g[i] == np.float32(pg) and d[i] == np.float32(pd)]
         assert a, (pg, pd)
         slow.append(r["times_ms"][a[0]] / r["best_ms"])
-    assert np.mean(slow) <= 1.01 and max(slow) <= 1.22, (np.mean(slow), max(slow))
+    assert np.mean(slow) <= 1.011 and max(slow) <= 1.23, (np.mean(slow), max(slow))
     prov = [r["times_ms"][24] / r["best_ms"] for r in recs]
     assert np.mean(slow) < np.mean(prov)
 
 
 def test_policy_leave_one_matrix_out():
     """The fit generalises to matrices it has not seen: refitting without
-    each matrix in turn (policy_tune's fit, depth 5, at least 4 cases per
-    leaf) and scoring the held-out matrix's cases gives x1.025 on average,
-    with 86% of the cases within x1.05.  The worst held-out cases (x1.64,
-    x1.56) are the 64-row-block matrices, whose best split the 11 policy
-    features cannot tell from the 16- and 32-row-block ones."""
+    each matrix in turn (policy_tune's fit as shipped: depth 3, at least 4
+    cases per leaf, robust leaves with worst-case weight 0.05) and scoring
+    the held-out matrix's cases gives x1.025 on average, with 87% of the
+    cases within x1.05 and x1.46 at worst (small fp16 matrices, whose steps
+    of a few microseconds pay for every extra class launch).  The deeper
+    tree without robust leaves (depth 5) has the same mean but x1.64 at
+    worst, on a 64-row-block matrix."""
     import importlib.util
     spec = importlib.util.spec_from_file_location("policy_tune", os.path.join(ROOT, "tilespmm_amd", "policy_tune.py"))
     pt = importlib.util.module_from_spec(spec)
@@ -154,11 +156,11 @@ def test_policy_leave_one_matrix_out():
     for prec in (0, 1):
         rs = [r for r in recs if r["prec"] == prec]
         for m in sorted({r["matrix"] for r in rs}):
-            root, nodes = pt.fit_tree([r for r in rs if r["matrix"] != m], 5, 4)
+            root, nodes = pt.fit_tree([r for r in rs if r["matrix"] != m], 3, 4, 0.05)
             held += [r["times_ms"][walk(root, nodes, r["features"])] / r["best_ms"] for r in rs if r["matrix"] == m]
     held = np.array(held)
     assert held.size == 344
-    assert held.mean() <= 1.03 and (held <= 1.05).mean() >= 0.85 and held.max() <= 1.65, \
+    assert held.mean() <= 1.03 and (held <= 1.05).mean() >= 0.86 and held.max() <= 1.47, \
         (held.mean(), (held <= 1.05).mean(), held.max())
 
 
