@@ -13,6 +13,11 @@ line.
   python bench.py [--steps K] [--warmup W] [--config 1..5] [--prec fp16|tf32]
                   [--colB N] [--targets 3,5] [--no-cpu] [--no-vendor]
                   [--cold-reps N] [--gpus 1]
+
+Experiments (other JSON lines): --gather (gather bandwidth by row size and
+table size), --copy-bytes N (copy calibration), --hub-split H (the hub-row
+experiment), --gather-stream (the gathers of the workload's own B-row index
+stream alone, against its tuned step), --sweep (variant sweep).
 """
 import argparse
 import json
@@ -587,6 +592,75 @@ def hub_split(tsp, hip, args):
     hip.tsp_free(mark_dst)
 
 
+def gather_stream(tsp, hip, args):
+    """The gather floor of a workload's own B-row stream: the tile column
+    indices of every class of the policy split, in tile order, gathered
+    (tsp_gather_index_stream: one colB_p-wide row per index, 8 loads in
+    flight per lane, nothing else in the loop) from B's rows in place and
+    with the hot rows the tuned plan copies (the most gathered columns that
+    fill its budget, at rows colA + slot).  Beside it, the tuned plan's step
+    time: their ratio is how close the kernels run to the rate at which the
+    memory system serves their gathers.  One JSON line."""
+    import ctypes as C
+    prec = {"fp16": 0, "tf32": 1, None: -1}[args.prec]
+    A, B, colB, cbp = tsp.gen_config(args.config, prec, args.colB)
+    prec = A.prec
+    g, d = tsp.predict(tsp.features(A, 9.5, colB), prec)
+    subs = tsp.matrix_split(A, g, d)
+    plan = tsp.Plan.from_csr(subs, A.rows, A.cols, cbp, prec, B)
+    plan.tune(True)
+    plan.warmup(300)
+    plan.run(zero_c=True)
+    step_ms = plan.time(args.steps)
+    hot_tuned = plan.get_hot_rows()[0]
+    plan.close()
+    del B
+    stream = np.concatenate([tsp.tile_create(sb, A.cols, bm, prec).arrays()["tile_colidx"].astype(np.int32)
+                             for sb, bm in zip(subs, (64, 16, 8)) if sb.rows > 0])
+    row_bytes = cbp * (2 if prec == 0 else 4)
+    cnt = np.bincount(stream, minlength=A.cols)
+    H = min(int((16 << 20) // row_bytes), int((cnt >= 4).sum()))
+    order = np.argsort(-cnt, kind="stable")[:H]
+    slot = np.full(A.cols, -1, np.int64)
+    slot[order] = np.arange(H)
+    hot = np.where(slot[stream] >= 0, A.cols + slot[stream], stream).astype(np.int32)
+    nrows = A.cols + H
+    tab, sink, didx = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    if (hip.tsp_malloc(C.byref(tab), nrows * row_bytes) or hip.tsp_malloc(C.byref(sink), 1024)
+            or hip.tsp_malloc(C.byref(didx), stream.nbytes)):
+        raise SystemExit("bench.py: cannot allocate the gather stream probe")
+    e0, e1 = C.c_void_p(), C.c_void_p()
+    hip.tsp_event_create(C.byref(e0))
+    hip.tsp_event_create(C.byref(e1))
+    out = {}
+    try:
+        hip.tsp_memset(tab, 1, nrows * row_bytes)
+        for name, idx in (("canonical", stream), ("hot_rows", hot)):
+            assert hip.tsp_memcpy_h2d(didx, idx.ctypes.data_as(C.c_void_p), idx.nbytes) == 0
+            assert hip.tsp_gather_index_stream(tab, nrows, row_bytes, didx, idx.size, sink, None) == 0
+            reps = 5
+            hip.tsp_event_record(e0, None)
+            for _ in range(reps):
+                hip.tsp_gather_index_stream(tab, nrows, row_bytes, didx, idx.size, sink, None)
+            hip.tsp_event_record(e1, None)
+            hip.tsp_event_sync(e1)
+            ms = C.c_float()
+            hip.tsp_event_elapsed_ms(C.byref(ms), e0, e1)
+            t = ms.value / reps
+            out[name] = {"ms": round(t, 5), "g_rows_per_s": round(idx.size / (t * 1e-3) / 1e9, 2)}
+    finally:
+        hip.tsp_event_destroy(e0)
+        hip.tsp_event_destroy(e1)
+        for p in (tab, sink, didx):
+            hip.tsp_free(p)
+    out["hot_rows"]["rows"] = H
+    best = min(out["canonical"]["ms"], out["hot_rows"]["ms"])
+    print(json.dumps({"gather_stream": NAMES[args.config], "prec": prec, "colB": colB, "row_bytes": row_bytes,
+                      "indices": int(stream.size), "hot_share_of_gathers": round(float(cnt[order].sum() / stream.size), 4),
+                      "tuned_step_ms": round(step_ms, 5), "tuned_hot_rows": hot_tuned, **out,
+                      "gather_floor_over_step": round(best / step_ms, 4)}), flush=True)
+
+
 TARGETS = {3: "T3", 5: "T5"}
 
 
@@ -645,6 +719,8 @@ def main():
                     help="only run the random row-gather probe (gather bandwidth ceiling)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="only run the plain copy kernel on this many bytes (counter calibration)")
+    ap.add_argument("--gather-stream", action="store_true",
+                    help="only time the gathers of the workload's own B-row index stream against its tuned step")
     ap.add_argument("--hub-split", type=lambda v: [int(x) for x in v.split(",")], default=None,
                     help="only run the hub-row experiment for these hub set sizes (columns), e.g. 16384")
     args = ap.parse_args()
@@ -665,6 +741,9 @@ def main():
         return
     if args.hub_split:
         hub_split(tsp, hip, args)
+        return
+    if args.gather_stream:
+        gather_stream(tsp, hip, args)
         return
 
     prec = {"fp16": 0, "tf32": 1, None: -1}[args.prec]

@@ -311,6 +311,16 @@ int tsp_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
  * bandwidth ceiling; no reference counterpart. */
 int tsp_gather_kernel(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed,
                       void *sink, void *stream);
+/* Row gathers in the order of an index stream: reads row d_idx[i] (row_bytes
+ * 64, 128, 256 or 512, 16 bytes per lane) of a table of table_rows rows for
+ * i = 0..n-1, the stream cut into contiguous pieces, one per wave, with 8
+ * loads in flight per lane; indices outside the table are clamped to it.
+ * Nothing is written unless an improbable bit pattern is read (d_sink, 256
+ * words).  Given a class's tile column indices it measures the gather rate
+ * of the kernels' own B-row stream with no other work; no reference
+ * counterpart. */
+int tsp_gather_index_stream(const void *d_table, long long table_rows, int row_bytes, const int *d_idx, long long n,
+                            void *d_sink, void *stream);
 
 /* ---- Hot B rows ------------------------------------------------------------
  * B is allocated with spare rows after row colA; hot slot s is row colA + s

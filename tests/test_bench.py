@@ -106,3 +106,22 @@ def test_bench_hub_split(tsp):
     assert s["hub_split_summary"] == 256 and 0 < s["hub_share_of_nnz"] < 1
     assert lines[1]["nnz"] + lines[2]["nnz"] == lines[0]["nnz"] == 32768
     assert s["hub_plus_cold_ms"] == pytest.approx(s["hub_ms"] + s["cold_ms"], abs=2e-5)
+
+
+@pytest.mark.gpu
+def test_bench_gather_stream(tsp):
+    """bench.py --gather-stream: the workload's own B-row index stream (every
+    class's tile column indices) gathered alone, in place and with the hot
+    rows, beside the tuned step; on configuration 1 (fp16, colB 32: 64-byte
+    rows) every index is a gather of 4096 rows."""
+    if not tsp.device_available():
+        pytest.fail("no gfx950 device: GPU tests need an MI355X")
+    print("bench.py --config 1 --gather-stream --steps 20", flush=True)
+    r = subprocess.run([sys.executable, "-u", BENCH, "--config", "1", "--gather-stream", "--steps", "20"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    j = json.loads(r.stdout.strip().splitlines()[-1])
+    assert j["row_bytes"] == 64 and j["indices"] % 16 == 0 and j["indices"] >= 32768
+    for k in ("canonical", "hot_rows"):
+        assert j[k]["ms"] > 0 and j[k]["g_rows_per_s"] > 0
+    assert 0 <= j["hot_share_of_gathers"] <= 1 and j["tuned_step_ms"] > 0

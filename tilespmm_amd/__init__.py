@@ -185,6 +185,7 @@ HIP_SYMBOLS = {
     "tsp_round_tf32_device": (C.c_int, [_P, C.c_size_t, _P]),
     "tsp_copy_kernel": (C.c_int, [_P, _P, C.c_size_t, _P]),
     "tsp_gather_kernel": (C.c_int, [_P, C.c_size_t, C.c_int, C.c_int, C.c_uint, _P, _P]),
+    "tsp_gather_index_stream": (C.c_int, [_P, C.c_longlong, C.c_int, _P, C.c_longlong, _P, _P]),
     "tsp_colidx_count": (C.c_int, [_P, C.c_longlong, C.c_int, _P, C.c_int, _P, _P]),
     "tsp_colidx_remap": (C.c_int, [_P, C.c_longlong, C.c_int, _P, C.c_int, _P, _P]),
     "tsp_hot_rows_gather": (C.c_int, [_P, C.c_int, C.c_longlong, _P, C.c_int, _P]),

@@ -460,4 +460,13 @@ int tsp_gather_kernel(const void *table, size_t table_bytes, int row_bytes, int 
     return tsp::launch_gather(table, table_bytes, row_bytes, iters, seed, sink, (hipStream_t)stream);
 }
 
+int tsp_gather_index_stream(const void *d_table, long long table_rows, int row_bytes, const int *d_idx, long long n,
+                            void *d_sink, void *stream)
+{
+    const bool rb_ok = row_bytes == 64 || row_bytes == 128 || row_bytes == 256 || row_bytes == 512;
+    if (!rb_ok || n < 0 || (n > 0 && (!d_table || !d_idx || !d_sink || table_rows <= 0))) return TSP_EINVAL;
+    if ((uintptr_t)d_table & 15) return TSP_EINVAL;
+    return tsp::launch_stream_gather(d_table, table_rows, row_bytes, d_idx, n, d_sink, (hipStream_t)stream);
+}
+
 }  // extern "C"

@@ -129,6 +129,8 @@ int launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
 constexpr int kGatherBlocks = 8192;      // gather probe grid: 8192 x 256 threads
 int launch_gather(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed, void *sink,
                   hipStream_t s);
+int launch_stream_gather(const void *table, long long nrows, int row_bytes, const int *idx, long long n, void *sink,
+                         hipStream_t s);
 
 // Address of the allocation-free entry points' `scratch` array on the current
 // device (looked up once per device; tsp_device_init calls it).

@@ -233,6 +233,55 @@ int launch_gather(const void *table, size_t table_bytes, int row_bytes, int iter
     return (int)hipGetLastError();
 }
 
+// Row gathers in the order of a given index stream (a class's tile column
+// indices, canonical or hot-remapped): wave w reads rows idx[w*per_wave ..],
+// each group of ROWB/16 lanes one row (16 bytes per lane), 8 loads in flight
+// per lane.  Indices are clamped to the table.  Measures the gather rate of
+// the kernels' own B-row stream with nothing else in the loop.
+template <int ROWB>
+__global__ __launch_bounds__(256) void stream_gather_kernel(const u4 *__restrict__ tab, long long nrows,
+                                                            const int *__restrict__ idx, long long n,
+                                                            long long per_wave, uint32_t *__restrict__ sink)
+{
+    constexpr int RL = ROWB / 16, RPW = 64 / RL;   // lanes per row, rows per wave instruction
+    const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63, q = lane / RL, sub = lane % RL;
+    const long long b = wave * per_wave, e = min(b + per_wave, n);
+    u4 acc = {0u, 0u, 0u, 0u};
+    for (long long i = b; i < e; i += 8 * RPW) {
+        u4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const long long j = i + (long long)u * RPW + q;
+            long long r = j < e ? (long long)idx[j] : 0;
+            r = r < 0 ? 0 : (r >= nrows ? nrows - 1 : r);
+            v[u] = j < e ? tab[(size_t)r * RL + sub] : u4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc ^= v[u];
+    }
+    if ((acc.x & 0xfffffu) == 0x12345u) sink[threadIdx.x] = acc.x ^ acc.y ^ acc.z ^ acc.w;
+}
+
+int launch_stream_gather(const void *table, long long nrows, int row_bytes, const int *idx, long long n, void *sink,
+                         hipStream_t s)
+{
+    if (n <= 0) return 0;
+    const u4 *t = (const u4 *)table;
+    uint32_t *k = (uint32_t *)sink;
+    const long long waves = (long long)kGatherBlocks * 4;
+    const int rpw = 64 / (row_bytes / 16);
+    const long long per = ((n + waves - 1) / waves + 8 * rpw - 1) / (8 * rpw) * (8 * rpw);
+    switch (row_bytes) {
+    case 64: stream_gather_kernel<64><<<kGatherBlocks, 256, 0, s>>>(t, nrows, idx, n, per, k); break;
+    case 128: stream_gather_kernel<128><<<kGatherBlocks, 256, 0, s>>>(t, nrows, idx, n, per, k); break;
+    case 256: stream_gather_kernel<256><<<kGatherBlocks, 256, 0, s>>>(t, nrows, idx, n, per, k); break;
+    case 512: stream_gather_kernel<512><<<kGatherBlocks, 256, 0, s>>>(t, nrows, idx, n, per, k); break;
+    default: return TSP_EINVAL;
+    }
+    return (int)hipGetLastError();
+}
+
 int launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s)
 {
     const size_t n = bytes / 16;
