@@ -592,29 +592,15 @@ def hub_split(tsp, hip, args):
     hip.tsp_free(mark_dst)
 
 
-def gather_stream(tsp, hip, args):
-    """The gather floor of a workload's own B-row stream: the tile column
-    indices of every class of the policy split, in tile order, gathered
+def stream_floor(tsp, hip, A, subs, prec, cbp):
+    """Gathers the B rows of every tile column index of every class of the
+    split `subs`, in tile order, with nothing else in the loop
     (tsp_gather_index_stream: one colB_p-wide row per index, 8 loads in
-    flight per lane, nothing else in the loop) from B's rows in place and
-    with the hot rows the tuned plan copies (the most gathered columns that
-    fill its budget, at rows colA + slot).  Beside it, the tuned plan's step
-    time: their ratio is how close the kernels run to the rate at which the
-    memory system serves their gathers.  One JSON line."""
+    flight per lane), once from B's rows in place and once with the hot rows
+    a plan copies (the most gathered columns gathered at least 4 times, up to
+    16 MB, at rows colA + slot).  The faster of the two is the floor of the
+    step's own gathers."""
     import ctypes as C
-    prec = {"fp16": 0, "tf32": 1, None: -1}[args.prec]
-    A, B, colB, cbp = tsp.gen_config(args.config, prec, args.colB)
-    prec = A.prec
-    g, d = tsp.predict(tsp.features(A, 9.5, colB), prec)
-    subs = tsp.matrix_split(A, g, d)
-    plan = tsp.Plan.from_csr(subs, A.rows, A.cols, cbp, prec, B)
-    plan.tune(True)
-    plan.warmup(300)
-    plan.run(zero_c=True)
-    step_ms = plan.time(args.steps)
-    hot_tuned = plan.get_hot_rows()[0]
-    plan.close()
-    del B
     stream = np.concatenate([tsp.tile_create(sb, A.cols, bm, prec).arrays()["tile_colidx"].astype(np.int32)
                              for sb, bm in zip(subs, (64, 16, 8)) if sb.rows > 0])
     row_bytes = cbp * (2 if prec == 0 else 4)
@@ -623,7 +609,6 @@ def gather_stream(tsp, hip, args):
     order = np.argsort(-cnt, kind="stable")[:H]
     slot = np.full(A.cols, -1, np.int64)
     slot[order] = np.arange(H)
-    hot = np.where(slot[stream] >= 0, A.cols + slot[stream], stream).astype(np.int32)
     nrows = A.cols + H
     tab, sink, didx = C.c_void_p(), C.c_void_p(), C.c_void_p()
     if (hip.tsp_malloc(C.byref(tab), nrows * row_bytes) or hip.tsp_malloc(C.byref(sink), 1024)
@@ -632,10 +617,13 @@ def gather_stream(tsp, hip, args):
     e0, e1 = C.c_void_p(), C.c_void_p()
     hip.tsp_event_create(C.byref(e0))
     hip.tsp_event_create(C.byref(e1))
-    out = {}
+    out = {"row_bytes": row_bytes, "indices": int(stream.size),
+           "hot_share_of_gathers": round(float(cnt[order].sum() / max(stream.size, 1)), 4)}
     try:
         hip.tsp_memset(tab, 1, nrows * row_bytes)
-        for name, idx in (("canonical", stream), ("hot_rows", hot)):
+        for name in ("canonical", "hot_rows"):
+            idx = stream if name == "canonical" else np.where(slot[stream] >= 0, A.cols + slot[stream],
+                                                              stream).astype(np.int32)
             assert hip.tsp_memcpy_h2d(didx, idx.ctypes.data_as(C.c_void_p), idx.nbytes) == 0
             assert hip.tsp_gather_index_stream(tab, nrows, row_bytes, didx, idx.size, sink, None) == 0
             reps = 5
@@ -654,11 +642,32 @@ def gather_stream(tsp, hip, args):
         for p in (tab, sink, didx):
             hip.tsp_free(p)
     out["hot_rows"]["rows"] = H
-    best = min(out["canonical"]["ms"], out["hot_rows"]["ms"])
-    print(json.dumps({"gather_stream": NAMES[args.config], "prec": prec, "colB": colB, "row_bytes": row_bytes,
-                      "indices": int(stream.size), "hot_share_of_gathers": round(float(cnt[order].sum() / stream.size), 4),
+    out["floor_ms"] = min(out["canonical"]["ms"], out["hot_rows"]["ms"])
+    return out
+
+
+def gather_stream(tsp, hip, args):
+    """The gather floor of a workload's own B-row stream (stream_floor) beside
+    the tuned plan's step time: their ratio is how close the kernels run to
+    the rate at which the memory system serves their gathers.  One JSON
+    line."""
+    prec = {"fp16": 0, "tf32": 1, None: -1}[args.prec]
+    A, B, colB, cbp = tsp.gen_config(args.config, prec, args.colB)
+    prec = A.prec
+    g, d = tsp.predict(tsp.features(A, 9.5, colB), prec)
+    subs = tsp.matrix_split(A, g, d)
+    plan = tsp.Plan.from_csr(subs, A.rows, A.cols, cbp, prec, B)
+    plan.tune(True)
+    plan.warmup(300)
+    plan.run(zero_c=True)
+    step_ms = plan.time(args.steps)
+    hot_tuned = plan.get_hot_rows()[0]
+    plan.close()
+    del B
+    out = stream_floor(tsp, hip, A, subs, prec, cbp)
+    print(json.dumps({"gather_stream": NAMES[args.config], "prec": prec, "colB": colB,
                       "tuned_step_ms": round(step_ms, 5), "tuned_hot_rows": hot_tuned, **out,
-                      "gather_floor_over_step": round(best / step_ms, 4)}), flush=True)
+                      "gather_floor_over_step": round(out["floor_ms"] / step_ms, 4)}), flush=True)
 
 
 TARGETS = {3: "T3", 5: "T5"}
@@ -756,6 +765,10 @@ def main():
         plan.close()
         return
     plan.close()
+    # the floor of the headline step's own B-row gathers (stream_floor)
+    floor = stream_floor(tsp, hip, A, subs, A.prec, rec["colB_padded"])
+    floor["floor_over_step"] = round(floor["floor_ms"] / rec["ms_per_step"], 4)
+    rec["gather_floor"] = floor
     del A, subs
     ceiling = gather_ceiling(hip)
     # the measured copy-bandwidth peak (a 512 MB copy back to back, read plus
@@ -811,6 +824,7 @@ def main():
         "roofline": rec["roofline"],
         "cpu_baseline": rec.get("cpu_baseline"),
         "gather": gather_stats(rec),
+        "gather_floor": rec.get("gather_floor"),
         "targets": targets,
         "window_ms": round(rec["window_ms"], 3),
         "long_window": rec["long_window"],

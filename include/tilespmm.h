@@ -191,8 +191,12 @@ int tsp_plan_create_csr(tsp_plan **plan, int device_id, const tsp_sub_csr *s64,
  * current one). */
 int tsp_plan_set_th(tsp_plan *plan, int th64, int th16, int th8);
 /* Cost-model top-4 per class, then runtime tuning over the cross product
- * (5 untimed + 10 timed runs each, src/csr2tile.h:962-1014).  Leaves the best
- * schedule installed; outputs the thresholds and the two timing parts. */
+ * (5 untimed + 10 timed runs each, src/csr2tile.h:962-1014).  With tune != 0
+ * it then tunes each class's kernel variant (A format, chunk order and
+ * width, tasks per wave, XCD placement, pipeline depth, index loads, tile
+ * pairs, panel sweep), the hot B rows, and each class's threshold once more
+ * with its tuned variant.  Leaves the best schedule installed; outputs the
+ * thresholds and the two timing parts. */
 int tsp_plan_tune(tsp_plan *plan, int tune, int th_out[3], double *model_ms, double *tune_ms);
 /* Pin the kernel variant one class launches with (see
  * tsp_spmm_launch_variant); zeros restore the library default. */

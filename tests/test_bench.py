@@ -81,6 +81,10 @@ def test_bench_json_line(tsp):
         assert roof["kernel_ms"] <= d["ms_per_step"] * 1.05
     assert d["warmup_clock"]["steps"] >= 1 and d["long_window"]["steps"] >= 20
     assert d["gather"]["ceiling_glines_per_s"] > 0
+    # the floor of the headline's own B-row gathers, beside its step
+    fl = d["gather_floor"]
+    assert fl["row_bytes"] == 64 and fl["indices"] >= 32768 and fl["floor_ms"] > 0
+    assert fl["floor_over_step"] == pytest.approx(fl["floor_ms"] / d["ms_per_step"], rel=1e-2, abs=1e-3)
     # the fp16 / colB 128 target record of the same run
     t = d["targets"]["C1"]
     assert "fp16, colB 128" in t["workload"] and t["tflops"] > 0

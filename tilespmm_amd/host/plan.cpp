@@ -1485,6 +1485,40 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
                 TSP_TRY(tune_class(p, c));
             }
         }
+        // The thresholds again, with the tuned variants: the cross product
+        // above timed them with the library's default variants, and a
+        // class's best threshold can move with its variant (configuration 5
+        // in fp16 at colB 128 kept 8 with the defaults and then ran 5% slower
+        // than at 16 with its tuned variant).  One class at a time over its
+        // cost-model candidates, the others as kept; whole steps of at least
+        // 20 ms, best of two interleaved rounds; the cross product's pick
+        // stays unless another is 1% faster.
+        const bool log = getenv("TSP_TUNE_LOG") != nullptr;
+        for (int i = 0; i < 3; ++i) {
+            if (opts[i].size() < 2 || !p->cls[i].active()) continue;
+            std::vector<double> ms(opts[i].size(), 1e30);
+            for (int round = 0; round < 2; ++round)
+                for (size_t j = 0; j < opts[i].size(); ++j) {
+                    int th[3] = {best[0], best[1], best[2]};
+                    th[i] = opts[i][j];
+                    TSP_TRY(tsp_plan_set_th(p, th[0], th[1], th[2]));
+                    double t = 0;
+                    TSP_TRY(tune_time_step(p, 20.0, &t));
+                    ms[j] = std::min(ms[j], t);
+                }
+            size_t bj = 0, kj = 0;
+            for (size_t j = 0; j < opts[i].size(); ++j) {
+                if (ms[j] < ms[bj]) bj = j;
+                if (opts[i][j] == best[i]) kj = j;
+            }
+            if (ms[bj] > 0.99 * ms[kj]) bj = kj;
+            if (log)
+                for (size_t j = 0; j < opts[i].size(); ++j)
+                    fprintf(stderr, "tune bm=%d threshold %d with the tuned variant: %.5f ms%s\n", p->cls[i].bm,
+                            opts[i][j], ms[j], j == bj ? "  <- kept" : "");
+            best[i] = opts[i][bj];
+        }
+        TSP_TRY(tsp_plan_set_th(p, best[0], best[1], best[2]));
         // the split form of B stays only if a tuned class reads it
         bool split = false;
         for (ClassDev &c : p->cls) split |= c.active() && reads_split_b(p, c);
