@@ -155,7 +155,11 @@ int tsp_malloc(void **ptr, size_t bytes)
     if (!ptr) return TSP_EINVAL;
     *ptr = nullptr;
     if (bytes == 0) return TSP_OK;
-    return (int)hipMalloc(ptr, bytes);
+    const hipError_t e = hipMalloc(ptr, bytes);
+    // a failed allocation must not surface later as the error of an
+    // unrelated launch (launches report hipGetLastError)
+    if (e != hipSuccess) (void)hipGetLastError();
+    return (int)e;
 }
 int tsp_free(void *ptr) { return ptr ? (int)hipFree(ptr) : TSP_OK; }
 int tsp_memcpy_h2d(void *dst, const void *src, size_t bytes)

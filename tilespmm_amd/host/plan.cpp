@@ -363,12 +363,18 @@ static int ensure_split_b(tsp_plan *p)
     if (p->d_Bs) return TSP_OK;
     const size_t n = ((size_t)p->colA + (size_t)p->hot_cap) * (size_t)p->colB_p;
     TSP_TRY(tsp_device_sync());
-    TSP_TRY(tsp_malloc(&p->d_Bs, n * sizeof(float)));
-    TSP_TRY(tsp_split_bf16_device(p->d_B, p->d_Bs, (size_t)p->colA * (size_t)p->colB_p, nullptr));
-    if (p->nhot)
-        TSP_TRY(tsp_hot_rows_gather(p->d_Bs, p->colA, (long long)sizeof(float) * p->colB_p, p->d_hot, p->nhot,
-                                    nullptr));
-    return tsp_device_sync();
+    void *bs = nullptr;
+    TSP_TRY(tsp_malloc(&bs, n * sizeof(float)));
+    int st = tsp_split_bf16_device(p->d_B, bs, (size_t)p->colA * (size_t)p->colB_p, nullptr);
+    if (st == TSP_OK && p->nhot)
+        st = tsp_hot_rows_gather(bs, p->colA, (long long)sizeof(float) * p->colB_p, p->d_hot, p->nhot, nullptr);
+    if (st == TSP_OK) st = tsp_device_sync();
+    if (st != TSP_OK) {               // never keep a half-made copy
+        tsp_free(bs);
+        return st;
+    }
+    p->d_Bs = bs;
+    return TSP_OK;
 }
 
 extern "C" int tsp_plan_set_pairs(tsp_plan *p, int bm, int on)
@@ -1203,8 +1209,9 @@ static int tune_class(tsp_plan *p, ClassDev &c)
         for (int li = 0; li < (c.fmt == 2 || (wd <= 128 && c.bm != 64) ? 2 : 1); ++li)
             for (int st = 1; st <= (wd == 256 ? 2 : 3); ++st) dopt.push_back({d.w, d.order, d.place, st, li, 0, 1e30});
     }
-    const bool pair_ok = p->prec == TSP_PREC_FP16 ? c.bm != 64 : c.bm == 8;
-    if (pair_ok && p->prec == TSP_PREC_TF32) TSP_TRY(ensure_split_b(p));
+    bool pair_ok = p->prec == TSP_PREC_FP16 ? c.bm != 64 : c.bm == 8;
+    // tf32 pairs read a split copy of B; without room for it they are not tried
+    if (pair_ok && p->prec == TSP_PREC_TF32 && ensure_split_b(p) != TSP_OK) pair_ok = false;
     if (pair_ok)
         for (int w : {64, 128}) {
             if (p->colB_p % w != 0 || !tsp_pairs_supported(c.bm, p->prec, w)) continue;
