@@ -117,13 +117,15 @@ constexpr int kMinWaves = PR ? (SY && W == 64 && S == 1 ? 5 : 1)
 
 // SY: the panel-synchronised sweep (SyncArgs) is compiled in; without it the
 // kernel runs one generation and the sync arguments are ignored.
-// PR: tile pairs (fp16 tiles with BN = 16).  The wave's unit of work is two
-// consecutive tiles of one task, multiplied together as one 16 x 32 tile
+// PR: tile pairs.  The wave's unit of work is two consecutive tiles of one
+// task.  fp16 tiles with BN = 16 are multiplied together as one 16 x 32 tile
 // with v_mfma_f32_16x16x32_f16 (MFMA K index 16 + k is the second tile's
-// column k); a task with an odd number of tiles ends with a unit whose
-// second half has zero A values and zeroed B rows.  Half
-// the MFMAs of the K = 16 form (which runs at half the fp16 rate), half the
-// loop iterations, and twice the B rows in flight per iteration.
+// column k): half the MFMAs of the K = 16 form (which runs at half the fp16
+// rate), half the loop iterations, and twice the B rows in flight per
+// iteration.  tf32 8-row tiles (BN = 8, operands already tf32 values) use
+// split-bf16 products on v_mfma_f32_16x16x32_bf16 (SPL below).  A task with
+// an odd number of tiles ends with a unit whose second half has zero A
+// values and zeroed B rows.
 template <int BM, int W, int PREC, int S, bool PK, bool LI, bool SY, bool PR = false>
 __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(kMinWaves<BM, W, PREC, S, PK, SY, PR>))) void spmm_kernel(
     int ntasks, int nchunks, int tasks_per_wave, int chunk_major, const void *__restrict__ val_,
