@@ -599,7 +599,9 @@ def stream_floor(tsp, hip, A, subs, prec, cbp):
     flight per lane), once from B's rows in place and once with the hot rows
     a plan copies (the most gathered columns gathered at least 4 times, up to
     16 MB, at rows colA + slot).  The faster of the two is the floor of the
-    step's own gathers."""
+    step's own gathers.  Beside it, the time to write C once (rows x colB_p
+    fp32, a memset of that size): the other compulsory stream of a step,
+    which shares the memory system with the gathers."""
     import ctypes as C
     stream = np.concatenate([tsp.tile_create(sb, A.cols, bm, prec).arrays()["tile_colidx"].astype(np.int32)
                              for sb, bm in zip(subs, (64, 16, 8)) if sb.rows > 0])
@@ -643,6 +645,27 @@ def stream_floor(tsp, hip, A, subs, prec, cbp):
             hip.tsp_free(p)
     out["hot_rows"]["rows"] = H
     out["floor_ms"] = min(out["canonical"]["ms"], out["hot_rows"]["ms"])
+    cbytes = A.rows * cbp * 4
+    cbuf = C.c_void_p()
+    if hip.tsp_malloc(C.byref(cbuf), cbytes) == 0:
+        try:
+            hip.tsp_event_create(C.byref(e0))
+            hip.tsp_event_create(C.byref(e1))
+            hip.tsp_memset_async(cbuf, 0, cbytes, None)
+            reps = 5
+            hip.tsp_event_record(e0, None)
+            for _ in range(reps):
+                hip.tsp_memset_async(cbuf, 0, cbytes, None)
+            hip.tsp_event_record(e1, None)
+            hip.tsp_event_sync(e1)
+            ms = C.c_float()
+            hip.tsp_event_elapsed_ms(C.byref(ms), e0, e1)
+            out["c_write_ms"] = round(ms.value / reps, 5)
+            out["floor_plus_c_write_ms"] = round(out["floor_ms"] + out["c_write_ms"], 5)
+        finally:
+            hip.tsp_event_destroy(e0)
+            hip.tsp_event_destroy(e1)
+            hip.tsp_free(cbuf)
     return out
 
 
@@ -667,7 +690,9 @@ def gather_stream(tsp, hip, args):
     out = stream_floor(tsp, hip, A, subs, prec, cbp)
     print(json.dumps({"gather_stream": NAMES[args.config], "prec": prec, "colB": colB,
                       "tuned_step_ms": round(step_ms, 5), "tuned_hot_rows": hot_tuned, **out,
-                      "gather_floor_over_step": round(out["floor_ms"] / step_ms, 4)}), flush=True)
+                      "gather_floor_over_step": round(out["floor_ms"] / step_ms, 4),
+                      "floor_plus_c_write_over_step": round(out.get("floor_plus_c_write_ms", 0.0) / step_ms, 4)}),
+          flush=True)
 
 
 TARGETS = {3: "T3", 5: "T5"}
@@ -768,6 +793,8 @@ def main():
     # the floor of the headline step's own B-row gathers (stream_floor)
     floor = stream_floor(tsp, hip, A, subs, A.prec, rec["colB_padded"])
     floor["floor_over_step"] = round(floor["floor_ms"] / rec["ms_per_step"], 4)
+    if "floor_plus_c_write_ms" in floor:
+        floor["floor_plus_c_write_over_step"] = round(floor["floor_plus_c_write_ms"] / rec["ms_per_step"], 4)
     rec["gather_floor"] = floor
     del A, subs
     ceiling = gather_ceiling(hip)
