@@ -107,39 +107,39 @@ def test_table_is_a_model_so_drop_in(tsp):
 
 
 EXTRA = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra.jsonl")
+EXTRA2 = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra2.jsonl")
 
 
 def all_records():
-    return records() + [json.loads(l) for l in open(EXTRA) if l.strip()]
+    return records() + [json.loads(l) for f in (EXTRA, EXTRA2) for l in open(f) if l.strip()]
 
 
 def test_policy_against_exhaustive_tuning(tsp):
-    """On its training sweeps (344 cases, 43 matrices) the shipped tree is
-    x1.010 of the exhaustive optimum on average and x1.23 at worst; the
-    provisional single-leaf table (candidate 24) is x1.14 (worst x2.79)."""
+    """On its training sweeps (408 cases, 51 matrices) the shipped tree is
+    x1.007 of the exhaustive optimum on average and x1.22 at worst; the
+    provisional single-leaf table (candidate 24) is x1.13 (worst x2.79)."""
     g, d = tsp.policy_candidates()
     slow = []
     recs = all_records()
-    assert len(recs) == 344 and len({r["matrix"] for r in recs}) == 43
+    assert len(recs) == 408 and len({r["matrix"] for r in recs}) == 51
     for r in recs:
         pg, pd = tsp.predict(np.array(r["features"]), r["prec"])
         a = [i for i in range(len(g)) if g[i] == np.float32(pg) and d[i] == np.float32(pd)]
         assert a, (pg, pd)
         slow.append(r["times_ms"][a[0]] / r["best_ms"])
-    assert np.mean(slow) <= 1.011 and max(slow) <= 1.23, (np.mean(slow), max(slow))
+    assert np.mean(slow) <= 1.008 and max(slow) <= 1.22, (np.mean(slow), max(slow))
     prov = [r["times_ms"][24] / r["best_ms"] for r in recs]
     assert np.mean(slow) < np.mean(prov)
 
 
 def test_policy_leave_one_matrix_out():
     """The fit generalises to matrices it has not seen: refitting without
-    each matrix in turn (policy_tune's fit as shipped: depth 3, at least 4
-    cases per leaf, robust leaves with worst-case weight 0.05) and scoring
-    the held-out matrix's cases gives x1.025 on average, with 87% of the
-    cases within x1.05 and x1.46 at worst (small fp16 matrices, whose steps
-    of a few microseconds pay for every extra class launch).  The deeper
-    tree without robust leaves (depth 5) has the same mean but x1.64 at
-    worst, on a 64-row-block matrix."""
+    each matrix in turn (policy_tune's fit as shipped: depth 4, at least 8
+    cases per leaf) and scoring the held-out matrix's cases gives x1.019 on
+    average, with 90% of the cases within x1.05.  The worst held-out cases
+    (x1.76, x1.56 at colB 32) are a small 64-row-block matrix, whose best
+    split (all 64-row tiles) the 11 policy features cannot tell from the
+    16- and 32-row-block matrices, which want 16-row tiles."""
     import importlib.util
     spec = importlib.util.spec_from_file_location("policy_tune", os.path.join(ROOT, "tilespmm_amd", "policy_tune.py"))
     pt = importlib.util.module_from_spec(spec)
@@ -156,11 +156,11 @@ def test_policy_leave_one_matrix_out():
     for prec in (0, 1):
         rs = [r for r in recs if r["prec"] == prec]
         for m in sorted({r["matrix"] for r in rs}):
-            root, nodes = pt.fit_tree([r for r in rs if r["matrix"] != m], 3, 4, 0.05)
+            root, nodes = pt.fit_tree([r for r in rs if r["matrix"] != m], 4, 8, 0.0)
             held += [r["times_ms"][walk(root, nodes, r["features"])] / r["best_ms"] for r in rs if r["matrix"] == m]
     held = np.array(held)
-    assert held.size == 344
-    assert held.mean() <= 1.03 and (held <= 1.05).mean() >= 0.86 and held.max() <= 1.47, \
+    assert held.size == 408
+    assert held.mean() <= 1.02 and (held <= 1.05).mean() >= 0.89 and held.max() <= 1.77, \
         (held.mean(), (held <= 1.05).mean(), held.max())
 
 

@@ -157,6 +157,12 @@ def gen_rmat(rng, scale, ef, a=0.57, b=0.19, c=0.19):
 def corpus(which):
     rng = np.random.default_rng(20260777)
     items = []
+
+    # the extra corpora: each matrix draws from its own generator, seeded
+    # from its name, so any subset (--only) generates the same instances
+    def seeded(name, make):
+        return name, lambda: make(np.random.default_rng(int(hashlib.sha1(name.encode()).hexdigest()[:8], 16)))
+
     if which in ("small", "full"):
         items += [
             ("uniform_2^16_k4", lambda: gen_uniform(rng, 1 << 16, 4)),
@@ -188,11 +194,7 @@ def corpus(which):
     if which == "extra":
         # neighbours of the matrices a leave-one-matrix-out refit served worst
         # (block-sparse families, small uniform matrices), more RMAT scales and
-        # power-law exponents, and other band widths.  Each matrix draws from
-        # its own generator, seeded from its name, so any subset (--only)
-        # generates the same instances
-        def seeded(name, make):
-            return name, lambda: make(np.random.default_rng(int(hashlib.sha1(name.encode()).hexdigest()[:8], 16)))
+        # power-law exponents, and other band widths
         extra = [
             ("blocks32_2^15_d2", lambda rng: gen_blocks(rng, 1 << 15, 32, 0.02)),
             ("blocks32_2^13_d8", lambda rng: gen_blocks(rng, 1 << 13, 32, 0.08)),
@@ -213,6 +215,21 @@ def corpus(which):
             ("blocks48_2^14_d2", lambda rng: gen_blocks(rng, 3 << 13, 48, 0.02)),
         ]
         items += [seeded(n, mk) for n, mk in extra]
+    if which == "extra2":
+        # small matrices beside the ones a depth-3 leave-one-matrix-out refit
+        # served worst (small uniform and 8-row-block matrices, whose steps of
+        # a few microseconds pay for every extra class launch)
+        extra2 = [
+            ("uniform_2^12_k8", lambda rng: gen_uniform(rng, 1 << 12, 8)),
+            ("uniform_2^12_k32", lambda rng: gen_uniform(rng, 1 << 12, 32)),
+            ("uniform_2^13_k16", lambda rng: gen_uniform(rng, 1 << 13, 16)),
+            ("uniform_2^14_k16", lambda rng: gen_uniform(rng, 1 << 14, 16)),
+            ("uniform_2^16_k16", lambda rng: gen_uniform(rng, 1 << 16, 16)),
+            ("blocks8_2^13_d2", lambda rng: gen_blocks(rng, 1 << 13, 8, 0.02)),
+            ("blocks8_2^14_d4", lambda rng: gen_blocks(rng, 1 << 14, 8, 0.04)),
+            ("blocks8_2^15_d2", lambda rng: gen_blocks(rng, 1 << 15, 8, 0.02)),
+        ]
+        items += [seeded(n, mk) for n, mk in extra2]
     return items
 
 
@@ -690,7 +707,7 @@ def main():
     tf.add_argument("--per-group", action="store_true", help="one weight pair per (class, prec, width)")
     s = sub.add_parser("sweep")
     s.add_argument("--configs", type=int, nargs="*", default=[])
-    s.add_argument("--corpus", choices=["small", "full", "extra"], default=None)
+    s.add_argument("--corpus", choices=["small", "full", "extra", "extra2"], default=None)
     s.add_argument("--precs", type=int, nargs="*", default=[0, 1])
     s.add_argument("--colBs", type=int, nargs="*", default=[32, 128])
     s.add_argument("--reps", type=int, default=30)
