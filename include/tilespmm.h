@@ -308,7 +308,12 @@ int tsp_plan_graph_free(tsp_plan *plan);
    its own stream, or the main stream when it is the plan's only class. */
 int tsp_plan_time_class(tsp_plan *plan, int bm, int reps, double *ms_per_launch);
 int tsp_plan_download_c(tsp_plan *plan, float *h_C);
-/* Device pointers of the plan (for external drivers). */
+/* Device pointers of the plan (for external drivers).  A plan's C is zeroed
+ * when the plan is made and written only by the plan's launches, which
+ * therefore skip storing results that are exact zeros (empty rows of a
+ * row-block cost no write; TSP_LAUNCH_SKIP_ZERO_STORES).  Once the caller
+ * has taken C's device pointer it may write into C, so from then on the
+ * plan stores every result (and a graph captured before is stale). */
 int tsp_plan_device_c(tsp_plan *plan, float **d_C);
 int tsp_plan_destroy(tsp_plan *plan);
 

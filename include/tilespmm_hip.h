@@ -221,6 +221,13 @@ int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const 
  * counterpart in the reference (its 16-row kernel covers both k-halves of
  * one 16 x 16 tile with two m16n8k16 steps). */
 #define TSP_LAUNCH_TILE_PAIRS 8
+/* TSP_LAUNCH_SKIP_ZERO_STORES: the caller guarantees that C already holds
+ * zero wherever the launch's result is an exact zero (a zero-filled C that
+ * only launches of the same matrix and B write, as a plan's is); the kernels
+ * then skip storing (and atomically adding) exact zeros -- a row-block's
+ * empty rows, for instance, cost no write.  NaN is stored.  No counterpart
+ * in the reference, whose kernels store every row of every tile. */
+#define TSP_LAUNCH_SKIP_ZERO_STORES 16
 int tsp_pairs_supported(int bm, int prec, int w);
 int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
                        const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,

@@ -362,6 +362,57 @@ def test_nan_and_inf_propagate_with_tile_pairs(gpu, prec):
 
 
 @pytest.mark.parametrize("prec", [0, 1])
+def test_zero_results_not_stored_until_c_is_shared(gpu, orc, prec):
+    """A plan's launches skip storing exact-zero results: its C starts at zero
+    and only its launches write it, so empty rows and B's padded columns stay
+    zero and every other entry is right, step after step (split tasks, whose
+    atomic adds accumulate across steps, with C zeroed before each).  Once the caller takes C's device pointer the plan stores
+    every result again: garbage written into C is overwritten by the next
+    step wherever a row-block has tiles (rows of row-blocks without any tile
+    are written by no step, as in the reference)."""
+    import ctypes as C
+    tsp = gpu
+    hip, host = tsp.load()
+    rng = np.random.default_rng(123 + prec)
+    A = random_matrix(tsp, rng, 700, 509, 30, prec, empty_frac=0.4, heavy_rows=2)
+    colB = 100
+    B, cbp = random_b(tsp, rng, A.cols, colB, prec)
+    Cref, Cabs = reference(orc, A, B, colB)
+    subs = tsp.matrix_split(A, 2.0, 1.5)
+    tiles = [tsp.tile_create(sb, A.cols, bm, prec) for sb, bm in zip(subs, (64, 16, 8))]
+    plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, prec, B)
+    empty = np.diff(A.rowptr) == 0
+    assert empty.sum() > 100
+    written = np.zeros(A.rows, bool)               # rows of row-blocks that have tiles
+    for sb, bm in zip(subs, (64, 16, 8)):
+        lens = np.diff(sb.rowptr) if sb.rows else np.zeros(0)
+        for b0 in range(0, sb.rows, bm):
+            if lens[b0:b0 + bm].any():
+                written[sb.orig_row[b0:b0 + bm]] = True
+    try:
+        for th in ((1 << 20,) * 3, (8, 8, 8)):
+            plan.set_th(*th)
+            for rep in range(2):
+                plan.run(zero_c=th[0] == 8)
+                Cg = plan.download_c()
+                tag = f"prec={prec} th={th[0]} rep={rep}"
+                assert_close(Cg[:, :colB], Cref, Cabs, prec, tag)
+                assert (Cg[:, colB:] == 0).all() and (Cg[empty] == 0).all(), tag
+        plan.set_th(*((1 << 20,) * 3))
+        plan.run(zero_c=True)
+        C0 = plan.download_c()
+        dc = C.c_void_p()
+        assert host.tsp_plan_device_c(plan.p, C.byref(dc)) == 0
+        assert hip.tsp_memset(dc, 0x7f, A.rows * cbp * 4) == 0      # 0x7f7f7f7f: a large finite value
+        plan.run(zero_c=False)
+        C1 = plan.download_c()
+        assert np.array_equal(C1[written].view(np.uint32), C0[written].view(np.uint32))
+        assert (C1[~written].view(np.uint32) == 0x7f7f7f7f).all()
+    finally:
+        plan.close()
+
+
+@pytest.mark.parametrize("prec", [0, 1])
 def test_panel_sweep_and_wide_chunks(gpu, orc, prec):
     """The panel-synchronised sweep (tsp_plan_set_panels, dense format) and
     the 256-column chunks: every class, chunk width, depth, order, placement
@@ -989,6 +1040,18 @@ def test_tf32_prerounded_launch_matches_rounding_launch(gpu, orc, bm):
             # dense tiles with lane-loaded indices: the same result bit for bit
             assert li == 0 and hip.tsp_device_sync() == 0
             assert np.array_equal(down("C2", Cz).view(np.uint32), c1.view(np.uint32))
+        # TSP_LAUNCH_SKIP_ZERO_STORES (16): exact-zero results are not stored,
+        # so a C full of garbage keeps it exactly there (NaN is stored)
+        junk = np.full_like(Cz, 0).view(np.uint32)
+        junk[:] = 0x7f7f7f7f
+        up("C3", junk.view(np.float32))
+        assert hip.tsp_spmm_launch_ex(bm, 1, len(rows), cbp, bufs["valr"], None, None, bufs["rows"], bufs["cs"],
+                                      bufs["Br"], bufs["C3"], bufs["col"], A.rows, None, 0, 0, 0, 0, 0, 1 | 16) == 0
+        assert hip.tsp_device_sync() == 0
+        c3 = down("C3", Cz).view(np.uint32)
+        zero = c1.view(np.uint32) == 0
+        assert (~zero).any()
+        assert (c3[zero] == 0x7f7f7f7f).all() and np.array_equal(c3[~zero], c1.view(np.uint32)[~zero])
         if bm != 64:
             # packed A with lane-loaded indices and 64-column chunks (the
             # gathered B registers are the MFMA operands, no LDS panel): the

@@ -309,7 +309,9 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
                        int c_rows, void *stream, int w, int stages, int tasks_per_wave, int order,
                        int placement, int flags)
 {
-    if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES | TSP_LAUNCH_TILE_PAIRS)) return TSP_EINVAL;
+    if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES | TSP_LAUNCH_TILE_PAIRS |
+                  TSP_LAUNCH_SKIP_ZERO_STORES))
+        return TSP_EINVAL;
     if ((flags & TSP_LAUNCH_TILE_PAIRS) &&
         (!tsp_pairs_supported(bm, prec, w > 0 ? w : tsp::default_chunk_width(bm, colB_p)) ||
          (prec == TSP_PREC_TF32 && !(flags & TSP_LAUNCH_OPERANDS_TF32))))
@@ -328,7 +330,8 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
     return tsp::launch(bm, kprec, rowblkblock, colB_p, d_val, d_bitmap, d_vptr, d_rows, d_colstart, d_B,
                        d_C, d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave, order,
                        placement, (flags & TSP_LAUNCH_LANE_INDICES) != 0, 0, 0, 1, nullptr, 0, false,
-                       (flags & TSP_LAUNCH_TILE_PAIRS) != 0);
+                       (flags & TSP_LAUNCH_TILE_PAIRS) != 0,
+                       (flags & TSP_LAUNCH_SKIP_ZERO_STORES) ? tsp::kOptSkipZeroStores : 0);
 }
 
 int tsp_spmm_launch_panels(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
@@ -338,7 +341,8 @@ int tsp_spmm_launch_panels(int bm, int prec, int rowblkblock, int colB_p, const 
                            int placement, int flags, int b_rows, int panel_rows, int panel_lag, int *d_sync,
                            long long sync_ints)
 {
-    if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES | TSP_LAUNCH_SYNC_RESET | TSP_LAUNCH_TILE_PAIRS))
+    if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES | TSP_LAUNCH_SYNC_RESET | TSP_LAUNCH_TILE_PAIRS |
+                  TSP_LAUNCH_SKIP_ZERO_STORES))
         return TSP_EINVAL;
     if ((flags & TSP_LAUNCH_TILE_PAIRS) &&
         (!tsp_pairs_supported(bm, prec, w > 0 ? w : tsp::default_chunk_width(bm, colB_p)) ||
@@ -358,7 +362,8 @@ int tsp_spmm_launch_panels(int bm, int prec, int rowblkblock, int colB_p, const 
     return tsp::launch(bm, kprec, rowblkblock, colB_p, d_val, d_bitmap, d_vptr, d_rows, d_colstart, d_B,
                        d_C, d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave, order,
                        placement, (flags & TSP_LAUNCH_LANE_INDICES) != 0, b_rows, panel_rows, panel_lag, d_sync,
-                       sync_ints, (flags & TSP_LAUNCH_SYNC_RESET) != 0, (flags & TSP_LAUNCH_TILE_PAIRS) != 0);
+                       sync_ints, (flags & TSP_LAUNCH_SYNC_RESET) != 0, (flags & TSP_LAUNCH_TILE_PAIRS) != 0,
+                       (flags & TSP_LAUNCH_SKIP_ZERO_STORES) ? tsp::kOptSkipZeroStores : 0);
 }
 
 int tsp_spmm_launch_variant(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,

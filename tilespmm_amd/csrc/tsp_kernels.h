@@ -71,6 +71,9 @@ constexpr int kPlaceContiguous = 0;
 constexpr int kPlaceInterleaved = 1;
 constexpr int kPlaceChunkXcd = 2;
 
+// Kernel option bits (the `opts` argument).
+constexpr int kOptSkipZeroStores = 1;   // do not store exact-zero results (C holds them already)
+
 // Panel-synchronised sweep (optional).  The B rows are cut into panels of
 // 2^pshift rows; the waves that one XCD runs in one generation of the grid
 // step through the panels together, so the B rows they gather stay in that
@@ -108,7 +111,8 @@ const void *select_kernel(int bm, int prec, int w, int s, bool packed, bool lane
 // The instantiations of one row-block class (tsp_spmm_bm{64,16,8}.hip);
 // nullptr for a variant that is not built.  prec: TSP_PREC_FP16,
 // TSP_PREC_TF32 or kPrecTf32Exact.  pair: the tile-pair form (fp16 8- and
-// 16-row tiles, 64- and 128-column chunks).
+// 16-row tiles at 64- and 128-column chunks; kPrecTf32Exact 8-row tiles at
+// 64-column chunks).
 const void *select_kernel_bm64(int prec, int w, int s, bool packed, bool lane_idx, bool sync, bool pair);
 const void *select_kernel_bm16(int prec, int w, int s, bool packed, bool lane_idx, bool sync, bool pair);
 const void *select_kernel_bm8(int prec, int w, int s, bool packed, bool lane_idx, bool sync, bool pair);
@@ -118,13 +122,13 @@ const void *select_kernel_bm8(int prec, int w, int s, bool packed, bool lane_idx
 // b_rows, panel_rows, panel_lag, sync, sync_ints, sync_reset: the
 // panel-synchronised sweep (sync != nullptr; see SyncArgs) with a buffer of
 // sync_ints counters, zeroed first when sync_reset is set.  pair: tile pairs
-// (TSP_LAUNCH_TILE_PAIRS).
+// (TSP_LAUNCH_TILE_PAIRS).  opts: kOpt* bits.
 int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint64_t *bmp,
            const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
            const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order,
            int placement = kPlaceContiguous, bool lane_idx = false, int b_rows = 0, int panel_rows = 0,
            int panel_lag = 1, int *sync = nullptr, long long sync_ints = 0, bool sync_reset = false,
-           bool pair = false);
+           bool pair = false, int opts = 0);
 int launch_copy(void *dst, const void *src, size_t bytes, hipStream_t s);
 constexpr int kGatherBlocks = 8192;      // gather probe grid: 8192 x 256 threads
 int launch_gather(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed, void *sink,

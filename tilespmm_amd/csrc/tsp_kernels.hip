@@ -123,7 +123,7 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
            const int *vptr, const unsigned *rows, const int *colstart, const void *B, float *C,
            const int *colidx, int c_rows, hipStream_t st, int w, int s, int tpw, int order,
            int placement, bool lane_idx, int b_rows, int panel_rows, int panel_lag, int *sync, long long sync_ints,
-           bool sync_reset, bool pair)
+           bool sync_reset, bool pair, int opts)
 {
     const bool packed = bmp != nullptr;
     if (packed && (bm == 64 || !vptr)) return TSP_EINVAL;
@@ -180,7 +180,7 @@ int launch(int bm, int prec, int ntasks, int colB_p, const void *val, const uint
     if (blocks > 0x7fffffffLL) return TSP_EINVAL;
     const int ld = colB_p;
     void *args[] = {&ntasks, &nchunks, &tpw, &cm, &val, &bmp, &vptr, &rows, &colstart, &B, &C, &colidx, (void *)&ld,
-                    &c_rows, &placement, &sy};
+                    &c_rows, &placement, &opts, &sy};
     const hipError_t e = hipLaunchKernel(k, dim3((unsigned)blocks), dim3(kBlockThreads), args, 0, st);
     return e != hipSuccess ? (int)e : (int)hipGetLastError();
 }

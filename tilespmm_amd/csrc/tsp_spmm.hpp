@@ -132,7 +132,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     const uint64_t *__restrict__ bmp, const int *__restrict__ vptr,
     const unsigned *__restrict__ rows, const int *__restrict__ colstart,
     const void *__restrict__ B_, float *__restrict__ C, const int *__restrict__ colidx, int ld,
-    int c_rows, int placement, SyncArgs sy)
+    int c_rows, int placement, int opts, SyncArgs sy)
 {
     constexpr bool F16 = PREC == TSP_PREC_FP16;
     // fp16 dense tiles read their B operands with LDS transpose reads and
@@ -536,6 +536,13 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         // the tasks just before and after the group belong to other row-blocks,
         // this wave ran every task of it (a split row-block's tasks are
         // consecutive, as tile_pretreatment emits them).
+        // kOptSkipZeroStores: C already holds zero (or this same result)
+        // wherever the launch would store an exact zero -- a plan's own C,
+        // zeroed when the plan is made and written only by its launches --
+        // so those stores are skipped (a row-block's empty rows, 43% of the
+        // RMAT matrices' rows, cost no write).  NaN compares unequal to zero
+        // and is stored.
+        const bool skip0 = (opts & kOptSkipZeroStores) != 0;
         auto flush = [&](int first, int last, unsigned rw) {   // rw = rows[last]
             if constexpr (SPL) {
                 // rows 8-15 of each MFMA block hold the low-half products of
@@ -572,14 +579,20 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                             // MFMA column n of block c is output column 16c + n:
                             // the 16 lanes of a group store 64 contiguous bytes
 #pragma unroll
-                            for (int c = 0; c < CB; ++c) __builtin_nontemporal_store(acc[g][c][j], crow + 16 * c + ln);
+                            for (int c = 0; c < CB; ++c)
+                                if (!skip0 || acc[g][c][j] != 0.f)
+                                    __builtin_nontemporal_store(acc[g][c][j], crow + 16 * c + ln);
                         } else {
                             // MFMA column n of block c is output column n*CB + c:
                             // the lane owns CB adjacent columns (one vector store)
                             FV v;
+                            bool nz = !skip0;
 #pragma unroll
-                            for (int c = 0; c < CB; ++c) v[c] = acc[g][c][j];
-                            __builtin_nontemporal_store(v, (FV *)(crow + ln * CB));
+                            for (int c = 0; c < CB; ++c) {
+                                v[c] = acc[g][c][j];
+                                nz |= v[c] != 0.f;
+                            }
+                            if (nz) __builtin_nontemporal_store(v, (FV *)(crow + ln * CB));
                         }
                     }
                 }
@@ -613,7 +626,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                         const int rr = idx / W, col = idx % W;
                         const int r = row0 + 8 * h + rr;
                         const float x = tr[rr * W + col];
-                        if (r < c_rows) unsafeAtomicAdd(C + (size_t)r * ld + col0 + col, x);
+                        if (r < c_rows && (!skip0 || x != 0.f)) unsafeAtomicAdd(C + (size_t)r * ld + col0 + col, x);
                     }
                     __builtin_amdgcn_wave_barrier();
                 }

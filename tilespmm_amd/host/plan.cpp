@@ -77,6 +77,12 @@ double now_ms()
 struct tsp_plan {
     int dev = 0, prec = 0, rowA = 0, colA = 0, colB_p = 0;
     void *d_B = nullptr;          // colA rows of B, then hot_cap spare rows for hot-row copies
+    // C is zeroed when the plan is made and written only by its launches, so
+    // they skip storing exact zeros (TSP_LAUNCH_SKIP_ZERO_STORES: a
+    // row-block's empty rows cost no write) -- until the caller takes C's
+    // device pointer and may write into it, from then on every result is
+    // stored
+    bool c_shared = false;
     void *d_Bs = nullptr;         // tf32 plans: the same rows as split-bf16 words, made when a class first
                                   // uses tile pairs (their kernels read B in that form)
     int hot_cap = 0;              // spare rows after row colA
@@ -239,7 +245,8 @@ static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
     if (!c.active() || c.ntasks == 0) return TSP_OK;
     const bool pk = c.fmt == 2;
     const int flags = (p->prec == TSP_PREC_TF32 ? TSP_LAUNCH_OPERANDS_TF32 : 0) |
-                      (lane_indices_on(c) ? TSP_LAUNCH_LANE_INDICES : 0) | (c.var_pr ? TSP_LAUNCH_TILE_PAIRS : 0);
+                      (lane_indices_on(c) ? TSP_LAUNCH_LANE_INDICES : 0) | (c.var_pr ? TSP_LAUNCH_TILE_PAIRS : 0) |
+                      (p->c_shared ? 0 : TSP_LAUNCH_SKIP_ZERO_STORES);
     if (c.panel > 0) {
         // the counters are zeroed whenever the launch arguments change
         const std::vector<long long> sig{c.ntasks, c.var_w, c.var_s, c.var_tpw, c.var_order, c.place,
@@ -1552,6 +1559,10 @@ extern "C" int tsp_plan_device_c(tsp_plan *p, float **d_C)
 {
     if (!p || !d_C) return TSP_EINVAL;
     *d_C = p->d_C;
+    if (!p->c_shared) {
+        p->c_shared = true;
+        ++p->version;             // a graph captured with zero stores skipped is stale
+    }
     return TSP_OK;
 }
 
