@@ -108,20 +108,21 @@ def test_table_is_a_model_so_drop_in(tsp):
 
 EXTRA = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra.jsonl")
 EXTRA2 = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra2.jsonl")
+EXTRA3 = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra3.jsonl")
 
 
 def all_records():
-    return records() + [json.loads(l) for f in (EXTRA, EXTRA2) for l in open(f) if l.strip()]
+    return records() + [json.loads(l) for f in (EXTRA, EXTRA2, EXTRA3) for l in open(f) if l.strip()]
 
 
 def test_policy_against_exhaustive_tuning(tsp):
-    """On its training sweeps (408 cases, 51 matrices) the shipped tree is
-    x1.007 of the exhaustive optimum on average and x1.22 at worst; the
-    provisional single-leaf table (candidate 24) is x1.13 (worst x2.79)."""
+    """On its training sweeps (472 cases, 59 matrices) the shipped tree is
+    x1.008 of the exhaustive optimum on average and x1.22 at worst; the
+    provisional single-leaf table (candidate 24) is x1.17 (worst x3.32)."""
     g, d = tsp.policy_candidates()
     slow = []
     recs = all_records()
-    assert len(recs) == 408 and len({r["matrix"] for r in recs}) == 51
+    assert len(recs) == 472 and len({r["matrix"] for r in recs}) == 59
     for r in recs:
         pg, pd = tsp.predict(np.array(r["features"]), r["prec"])
         a = [i for i in range(len(g)) if g[i] == np.float32(pg) and d[i] == np.float32(pd)]
@@ -134,12 +135,13 @@ def test_policy_against_exhaustive_tuning(tsp):
 
 def test_policy_leave_one_matrix_out():
     """The fit generalises to matrices it has not seen: refitting without
-    each matrix in turn (policy_tune's fit as shipped: depth 4, at least 8
-    cases per leaf) and scoring the held-out matrix's cases gives x1.019 on
-    average, with 90% of the cases within x1.05.  The worst held-out cases
-    (x1.76, x1.56 at colB 32) are a small 64-row-block matrix, whose best
-    split (all 64-row tiles) the 11 policy features cannot tell from the
-    16- and 32-row-block matrices, which want 16-row tiles."""
+    each matrix in turn (policy_tune's fit as shipped: depth 5, at least 8
+    cases per leaf, worst-case weight 0.5) and scoring the held-out
+    matrix's cases gives x1.031 on average, with 85% of the cases within
+    x1.05.  The worst held-out cases (x1.95 for a banded matrix at colB 32,
+    x1.69 for a small 64-row-block matrix with scattered entries) are
+    matrices of a few microseconds per step whose best split the 11 policy
+    features cannot tell from their neighbours'."""
     import importlib.util
     spec = importlib.util.spec_from_file_location("policy_tune", os.path.join(ROOT, "tilespmm_amd", "policy_tune.py"))
     pt = importlib.util.module_from_spec(spec)
@@ -156,11 +158,11 @@ def test_policy_leave_one_matrix_out():
     for prec in (0, 1):
         rs = [r for r in recs if r["prec"] == prec]
         for m in sorted({r["matrix"] for r in rs}):
-            root, nodes = pt.fit_tree([r for r in rs if r["matrix"] != m], 4, 8, 0.0)
+            root, nodes = pt.fit_tree([r for r in rs if r["matrix"] != m], 5, 8, 0.5)
             held += [r["times_ms"][walk(root, nodes, r["features"])] / r["best_ms"] for r in rs if r["matrix"] == m]
     held = np.array(held)
-    assert held.size == 408
-    assert held.mean() <= 1.02 and (held <= 1.05).mean() >= 0.89 and held.max() <= 1.77, \
+    assert held.size == 472
+    assert held.mean() <= 1.032 and (held <= 1.05).mean() >= 0.84 and held.max() <= 1.95, \
         (held.mean(), (held <= 1.05).mean(), held.max())
 
 

@@ -230,6 +230,22 @@ def corpus(which):
             ("blocks8_2^15_d2", lambda rng: gen_blocks(rng, 1 << 15, 8, 0.02)),
         ]
         items += [seeded(n, mk) for n, mk in extra2]
+    if which == "extra3":
+        # neighbours of the one matrix a depth-4 leave-one-matrix-out refit
+        # served worst (64-row dense blocks with scattered single entries,
+        # unlike any other matrix of the corpora above), and the small
+        # 4-per-row uniform matrices next in that ranking
+        extra3 = [
+            ("blocks64_2^12_d8_s", lambda rng: gen_blocks(rng, 1 << 12, 64, 0.08, 1e-4)),
+            ("blocks64_2^13_d2_s", lambda rng: gen_blocks(rng, 1 << 13, 64, 0.02, 1e-4)),
+            ("blocks64_2^14_d2_s", lambda rng: gen_blocks(rng, 1 << 14, 64, 0.02, 1e-4)),
+            ("blocks64_2^14_d4_s", lambda rng: gen_blocks(rng, 1 << 14, 64, 0.04, 1e-4)),
+            ("blocks32_2^13_d4_s", lambda rng: gen_blocks(rng, 1 << 13, 32, 0.04, 1e-4)),
+            ("blocks48_2^13_d4_s", lambda rng: gen_blocks(rng, 3 << 12, 48, 0.04, 1e-4)),
+            ("uniform_2^15_k4", lambda rng: gen_uniform(rng, 1 << 15, 4)),
+            ("uniform_2^17_k4", lambda rng: gen_uniform(rng, 1 << 17, 4)),
+        ]
+        items += [seeded(n, mk) for n, mk in extra3]
     return items
 
 
@@ -707,7 +723,7 @@ def main():
     tf.add_argument("--per-group", action="store_true", help="one weight pair per (class, prec, width)")
     s = sub.add_parser("sweep")
     s.add_argument("--configs", type=int, nargs="*", default=[])
-    s.add_argument("--corpus", choices=["small", "full", "extra", "extra2"], default=None)
+    s.add_argument("--corpus", choices=["small", "full", "extra", "extra2", "extra3"], default=None)
     s.add_argument("--precs", type=int, nargs="*", default=[0, 1])
     s.add_argument("--colBs", type=int, nargs="*", default=[32, 128])
     s.add_argument("--reps", type=int, default=30)
