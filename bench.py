@@ -266,6 +266,9 @@ def apply_pins(plan, args):
     for bm, pr in zip((64, 16, 8), args.pairs or ()):
         if pr:
             plan.set_pairs(bm, pr - 1)
+    for bm, b3 in zip((64, 16, 8), args.b3 or ()):
+        if b3:
+            plan.set_b_3byte(bm, b3 - 1)
     lags = args.panel_lag or (2, 2, 2)
     for bm, pr, lg in zip((64, 16, 8), args.panels or (), lags):
         if pr:
@@ -284,7 +287,7 @@ def variant_of(c):
 
 def pins_of(plan, th, cls):
     """The bench flags that replay this plan's tuned configuration."""
-    f, o, t, w, s, p, li, pr, lg, tp = [], [], [], [], [], [], [], [], [], []
+    f, o, t, w, s, p, li, pr, lg, tp, b3 = [], [], [], [], [], [], [], [], [], [], []
     for bm in (64, 16, 8):
         c = cls.get(bm)
         f.append({"dense": 1, "packed": 2}[c["format"]] if c else 0)
@@ -297,9 +300,10 @@ def pins_of(plan, th, cls):
         pr.append(c["panel_rows"] if c else 0)
         lg.append(c["panel_lag"] if c else 0)
         tp.append(c["tile_pairs"] + 1 if c else 0)
+        b3.append(c["b_3byte"] + 1 if c else 0)
     j = lambda v: ",".join(str(x) for x in v)
     return (f"--no-tune --th {j(th)} --format {j(f)} --order {j(o)} --tpw {j(t)} --width {j(w)} "
-            f"--stages {j(s)} --place {j(p)} --lane-idx {j(li)} --pairs {j(tp)} --panels {j(pr)} "
+            f"--stages {j(s)} --place {j(p)} --lane-idx {j(li)} --pairs {j(tp)} --b3 {j(b3)} --panels {j(pr)} "
             f"--panel-lag {j(lg)} --hot-bytes {plan.get_hot_rows()[1]}")
 
 
@@ -384,13 +388,14 @@ def measure(tsp, hip, config, prec, colB, args, headline):
         v = plan.get_variant(bm)
         w = v[0] or default_width(hip, bm, prec, cbp)
         bn = tsp.tile_bn(bm, prec)
-        lines = tn * bn * (cbp // w) * max(1, -(-w * s // 128))
+        b3 = max(0, plan.get_b_3byte(bm))
+        lines = tn * bn * (cbp // w) * max(1, -(-w * (3 if b3 else s) // 128))
         cls[bm] = {"ms": cms, "reps": reps, "rows": sb.rows, "nnz": int(sb.nnz), "tiles": tn,
                    "format": {1: "dense", 2: "packed"}.get(plan.get_format(bm), "?"),
                    "order": {0: "side-by-side", 1: "side-by-side", 2: "chunk-major"}[v[3]],
                    "tasks_per_wave": max(1, v[2]), "stages": max(1, v[1]), "chunk_width": w,
                    "lane_indices": max(0, plan.get_lane_indices(bm)),
-                   "tile_pairs": max(0, plan.get_pairs(bm)),
+                   "tile_pairs": max(0, plan.get_pairs(bm)), "b_3byte": b3,
                    "placement": {0: "contiguous", 1: "interleaved", 2: "chunk-xcd"}.get(plan.get_placement(bm), "?"),
                    "panel_rows": plan.get_panels(bm)[0], "panel_lag": plan.get_panels(bm)[1],
                    "alg_bytes": b, "gbs": b / (cms * 1e-3) / 1e9, "alg_bytes_touched": b_touched,
@@ -404,9 +409,10 @@ def measure(tsp, hip, config, prec, colB, args, headline):
     # the dominant kernel's instantiation spmm_kernel<BM, W, PREC, S, PK, LI, SY, PR>;
     # the profiled HBM traffic applies only to the same instantiation and hot
     # rows (plans launch tf32 on operands they rounded once: kernel precision
-    # code 2)
+    # code 2, or 3 with B in the 3-byte form)
     tf = lambda b: "true" if b else "false"
-    kname = (f"spmm_kernel<{dom}, {dk['chunk_width']}, {2 if prec == 1 else 0}, {dk['stages']}, "
+    kcode = (3 if dk["b_3byte"] else 2) if prec == 1 else 0
+    kname = (f"spmm_kernel<{dom}, {dk['chunk_width']}, {kcode}, {dk['stages']}, "
              f"{tf(dk['format'] == 'packed')}, {tf(dk['lane_indices'])}, {tf(dk['panel_rows'])}, "
              f"{tf(dk['tile_pairs'])}>")
     traffic, traffic_note = None, "no profile of this workload in profiles/"
@@ -592,16 +598,18 @@ def hub_split(tsp, hip, args):
     hip.tsp_free(mark_dst)
 
 
-def stream_floor(tsp, hip, A, subs, prec, cbp):
+def stream_floor(tsp, hip, A, subs, prec, cbp, b3=False):
     """Gathers the B rows of every tile column index of every class of the
     split `subs`, in tile order, with nothing else in the loop
     (tsp_gather_index_stream: one colB_p-wide row per index, 8 loads in
     flight per lane), once from B's rows in place and once with the hot rows
     a plan copies (the most gathered columns gathered at least 4 times, up to
-    16 MB, at rows colA + slot).  The faster of the two is the floor of the
-    step's own gathers.  Beside it, the time to write C once (rows x colB_p
-    fp32, a memset of that size): the other compulsory stream of a step,
-    which shares the memory system with the gathers."""
+    16 MB, at rows colA + slot); tf32 also with the hot rows in the 3-byte
+    form (rows of colB_p x 3 bytes).  The faster of the first two is the
+    floor of the step's own gathers, or the third when the step's dominant
+    class reads B in the 3-byte form (b3).  Beside it, the time to write C
+    once (rows x colB_p fp32, a memset of that size): the other compulsory
+    stream of a step, which shares the memory system with the gathers."""
     import ctypes as C
     stream = np.concatenate([tsp.tile_create(sb, A.cols, bm, prec).arrays()["tile_colidx"].astype(np.int32)
                              for sb, bm in zip(subs, (64, 16, 8)) if sb.rows > 0])
@@ -623,15 +631,18 @@ def stream_floor(tsp, hip, A, subs, prec, cbp):
            "hot_share_of_gathers": round(float(cnt[order].sum() / max(stream.size, 1)), 4)}
     try:
         hip.tsp_memset(tab, 1, nrows * row_bytes)
-        for name in ("canonical", "hot_rows"):
+        forms = [("canonical", row_bytes), ("hot_rows", row_bytes)]
+        if prec == 1 and 3 * cbp in (96, 192, 384):
+            forms.append(("hot_rows_3byte", 3 * cbp))
+        for name, rb in forms:
             idx = stream if name == "canonical" else np.where(slot[stream] >= 0, A.cols + slot[stream],
                                                               stream).astype(np.int32)
             assert hip.tsp_memcpy_h2d(didx, idx.ctypes.data_as(C.c_void_p), idx.nbytes) == 0
-            assert hip.tsp_gather_index_stream(tab, nrows, row_bytes, didx, idx.size, sink, None) == 0
+            assert hip.tsp_gather_index_stream(tab, nrows, rb, didx, idx.size, sink, None) == 0
             reps = 5
             hip.tsp_event_record(e0, None)
             for _ in range(reps):
-                hip.tsp_gather_index_stream(tab, nrows, row_bytes, didx, idx.size, sink, None)
+                hip.tsp_gather_index_stream(tab, nrows, rb, didx, idx.size, sink, None)
             hip.tsp_event_record(e1, None)
             hip.tsp_event_sync(e1)
             ms = C.c_float()
@@ -644,7 +655,9 @@ def stream_floor(tsp, hip, A, subs, prec, cbp):
         for p in (tab, sink, didx):
             hip.tsp_free(p)
     out["hot_rows"]["rows"] = H
-    out["floor_ms"] = min(out["canonical"]["ms"], out["hot_rows"]["ms"])
+    out["floor_ms"] = (out["hot_rows_3byte"]["ms"] if b3 and "hot_rows_3byte" in out
+                       else min(out["canonical"]["ms"], out["hot_rows"]["ms"]))
+    out["floor_form"] = "hot rows, 3-byte B" if b3 and "hot_rows_3byte" in out else "4-byte B"
     cbytes = A.rows * cbp * 4
     cbuf = C.c_void_p()
     if hip.tsp_malloc(C.byref(cbuf), cbytes) == 0:
@@ -685,9 +698,10 @@ def gather_stream(tsp, hip, args):
     plan.run(zero_c=True)
     step_ms = plan.time(args.steps)
     hot_tuned = plan.get_hot_rows()[0]
+    b3 = any(plan.get_b_3byte(bm) == 1 for bm in (64, 16, 8))
     plan.close()
     del B
-    out = stream_floor(tsp, hip, A, subs, prec, cbp)
+    out = stream_floor(tsp, hip, A, subs, prec, cbp, b3=b3)
     print(json.dumps({"gather_stream": NAMES[args.config], "prec": prec, "colB": colB,
                       "tuned_step_ms": round(step_ms, 5), "tuned_hot_rows": hot_tuned, **out,
                       "gather_floor_over_step": round(out["floor_ms"] / step_ms, 4),
@@ -731,6 +745,8 @@ def main():
                     help="pin lane-loaded column indices per class 64,16,8 (1 off, 2 on, 0 keep)")
     ap.add_argument("--pairs", type=ints3, default=None,
                     help="pin tile pairs per class 64,16,8 (1 off, 2 on, 0 keep; fp16 8-/16-row classes, tf32 8-row class)")
+    ap.add_argument("--b3", type=ints3, default=None,
+                    help="pin B in the 3-byte form per class 64,16,8 (1 off, 2 on, 0 keep; tf32, 64-column chunks)")
     ap.add_argument("--panels", type=ints3, default=None,
                     help="pin the panel-synchronised sweep per class: B rows per panel (0 = off)")
     ap.add_argument("--panel-lag", type=ints3, default=None,
@@ -791,7 +807,8 @@ def main():
         return
     plan.close()
     # the floor of the headline step's own B-row gathers (stream_floor)
-    floor = stream_floor(tsp, hip, A, subs, A.prec, rec["colB_padded"])
+    dk = rec["classes"][max(rec["classes"], key=lambda k: rec["classes"][k]["ms"])]
+    floor = stream_floor(tsp, hip, A, subs, A.prec, rec["colB_padded"], b3=bool(dk.get("b_3byte")))
     floor["floor_over_step"] = round(floor["floor_ms"] / rec["ms_per_step"], 4)
     if "floor_plus_c_write_ms" in floor:
         floor["floor_plus_c_write_over_step"] = round(floor["floor_plus_c_write_ms"] / rec["ms_per_step"], 4)
@@ -817,7 +834,8 @@ def main():
     targets = {}
     for cfg in [int(x) for x in args.targets.split(",") if x.strip()]:
         targ = argparse.Namespace(**vars(args))
-        for k in ("th", "format", "order", "tpw", "width", "stages", "place", "lane_idx", "pairs", "panels", "panel_lag",
+        for k in ("th", "format", "order", "tpw", "width", "stages", "place", "lane_idx", "pairs", "b3", "panels",
+                  "panel_lag",
                   "hot_bytes",
                   "gamma",
                   "delta"):

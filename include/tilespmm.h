@@ -194,7 +194,7 @@ int tsp_plan_set_th(tsp_plan *plan, int th64, int th16, int th8);
  * (5 untimed + 10 timed runs each, src/csr2tile.h:962-1014).  With tune != 0
  * it then tunes each class's kernel variant (A format, chunk order and
  * width, tasks per wave, XCD placement, pipeline depth, index loads, tile
- * pairs, panel sweep), the hot B rows, and each class's threshold once more
+ * pairs, 3-byte B, panel sweep), the hot B rows, and each class's threshold once more
  * with its tuned variant.  Leaves the best schedule installed; outputs the
  * thresholds and the two timing parts. */
 int tsp_plan_tune(tsp_plan *plan, int tune, int th_out[3], double *model_ms, double *tune_ms);
@@ -223,10 +223,23 @@ int tsp_plan_get_variant(tsp_plan *plan, int bm, int *w, int *stages, int *tasks
 int tsp_plan_set_lane_indices(tsp_plan *plan, int bm, int on);
 int tsp_plan_get_lane_indices(tsp_plan *plan, int bm);
 /* Tile pairs (TSP_LAUNCH_TILE_PAIRS) for one class: 1 on, 0 off; fp16 8- and
- * 16-row classes only, with 64- or 128-column chunks (a launch with another
- * width fails).  tsp_plan_tune picks.  No counterpart in the reference. */
+ * 16-row classes with 64- or 128-column chunks, tf32 8-row classes with
+ * 64-column chunks (a launch with another width fails; tf32 pairs read a
+ * split-bf16 copy of B that the plan makes when they are first switched
+ * on).  tsp_plan_tune picks.  No counterpart in the reference. */
 int tsp_plan_set_pairs(tsp_plan *plan, int bm, int on);
 int tsp_plan_get_pairs(tsp_plan *plan, int bm);
+/* B in the 3-byte form (TSP_LAUNCH_B_3BYTE) for one class of a tf32 plan: 1
+ * on, 0 off (fp16 plans: TSP_EINVAL for on).  Switching it on makes the
+ * plan's 3-byte copy of B (colB_p * 3 bytes per row plus the hot-row
+ * slots) if it has none.  The setting applies to the class's launches at
+ * 64-column chunks without tile pairs or the panel sweep; the results are
+ * bit for bit those of the 4-byte form.  get returns whether the class's
+ * launches read the 3-byte form (1 / 0), or -1 on a bad argument.
+ * tsp_plan_tune picks, and frees the copy when no class keeps it.  No
+ * counterpart in the reference. */
+int tsp_plan_set_b_3byte(tsp_plan *plan, int bm, int on);
+int tsp_plan_get_b_3byte(tsp_plan *plan, int bm);
 int tsp_plan_set_placement(tsp_plan *plan, int bm, int placement);
 int tsp_plan_get_placement(tsp_plan *plan, int bm);
 /* Panel-synchronised sweep (tsp_spmm_launch_panels) for one class on the

@@ -228,6 +228,17 @@ int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const 
  * empty rows, for instance, cost no write.  NaN is stored.  No counterpart
  * in the reference, whose kernels store every row of every tile. */
 #define TSP_LAUNCH_SKIP_ZERO_STORES 16
+/* TSP_LAUNCH_B_3BYTE (tf32 with TSP_LAUNCH_OPERANDS_TF32, chunk width 64, no
+ * tile pairs; not for the panel sweep): d_B holds B's rows in the 3-byte
+ * form of tsp_pack_3byte_device -- each tf32 value as the top 3 bytes of its
+ * fp32 word, row r at byte offset r * colB_p * 3 -- which the kernels gather
+ * with 12-byte loads and widen in registers.  Every tf32 value is kept
+ * exactly, so the result is bit for bit that of the 4-byte launch, while each
+ * gathered row is a quarter smaller (and rows no longer start at multiples
+ * of a power of two, which spread the most gathered rows unevenly over the
+ * memory channels).  Other launches with the flag fail with TSP_EINVAL.  No
+ * counterpart in the reference. */
+#define TSP_LAUNCH_B_3BYTE 32
 int tsp_pairs_supported(int bm, int prec, int w);
 int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void *d_val,
                        const uint64_t *d_bitmap, const int *d_vptr, const unsigned *d_rows,
@@ -307,6 +318,17 @@ int tsp_round_tf32_device(void *d_x, size_t n, void *stream);
 int tsp_split_bf16_bits(const uint32_t *in, uint32_t *out, size_t n);
 int tsp_split_bf16_device(const void *d_src, void *d_dst, size_t n, void *stream);
 
+/* tf32 values in 3 bytes each (the B form of TSP_LAUNCH_B_3BYTE): the top 24
+ * bits of each fp32 word, little-endian, 4 values in 12 bytes; a NaN whose
+ * payload lies only in the dropped low byte gets the quiet bit.  Lossless
+ * for tf32 values (low 13 mantissa bits zero, e.g. after
+ * tsp_round_tf32_device).  n (a multiple of 4) values of `in` / d_src to
+ * 3 n bytes of `out` / d_dst; the device form runs asynchronously on
+ * `stream` (d_dst must not overlap d_src).  No counterpart in the
+ * reference. */
+int tsp_pack_3byte_bits(const uint32_t *in, void *out, size_t n);
+int tsp_pack_3byte_device(const void *d_src, void *d_dst, size_t n, void *stream);
+
 /* A plain streaming copy kernel (dst = src, 16-byte vectors), used to
  * calibrate HBM byte counters and the achievable copy bandwidth. */
 int tsp_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
@@ -319,7 +341,8 @@ int tsp_copy_kernel(void *dst, const void *src, size_t bytes, void *stream);
 int tsp_gather_kernel(const void *table, size_t table_bytes, int row_bytes, int iters, unsigned seed,
                       void *sink, void *stream);
 /* Row gathers in the order of an index stream: reads row d_idx[i] (row_bytes
- * 64, 128, 256 or 512, 16 bytes per lane) of a table of table_rows rows for
+ * 64, 128, 256 or 512, 16 bytes per lane; or 96, 192 or 384, 12 bytes per
+ * lane, the rows of TSP_LAUNCH_B_3BYTE) of a table of table_rows rows for
  * i = 0..n-1, the stream cut into contiguous pieces, one per wave, with 8
  * loads in flight per lane; indices outside the table are clamped to it.
  * Nothing is written unless an improbable bit pattern is read (d_sink, 256

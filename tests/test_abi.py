@@ -103,6 +103,15 @@ def test_error_strings_and_arg_checks(tsp):
              (16, 0, 256))] == [1, 1, 1, 0, 0, 0, 0, 0]
     assert hip.tsp_split_bf16_bits(None, None, 1) == hip.tsp_split_bf16_device(None, None, 1, None) == 1001
     assert host.tsp_plan_set_pairs(None, 16, 1) == 1001 and host.tsp_plan_get_pairs(None, 16) == -1
+    # 3-byte B: tf32 operands only (OPERANDS_TF32 set), no tile pairs; refused
+    # before any device call
+    b3 = lambda prec, flags: hip.tsp_spmm_launch_ex(8, prec, 1, 64, dummy, None, None, dummy, dummy, dummy, dummy,
+                                                    dummy, 0, None, 64, 1, 0, 0, 0, flags)
+    assert b3(0, 1 | 32) == 1001 and b3(1, 32) == 1001 and b3(1, 1 | 8 | 32) == 1001
+    assert hip.tsp_pack_3byte_bits(None, None, 4) == hip.tsp_pack_3byte_device(None, None, 4, None) == 1001
+    assert hip.tsp_pack_3byte_device(dummy, C.c_void_p(1 << 20), 6, None) == 1001   # n a multiple of 4
+    assert hip.tsp_pack_3byte_device(C.c_void_p(1 << 20), C.c_void_p((1 << 20) + 8), 16, None) == 1001  # overlap
+    assert host.tsp_plan_set_b_3byte(None, 8, 1) == 1001 and host.tsp_plan_get_b_3byte(None, 8) == -1
     assert host.tsp_plan_graph_capture(None, 1) == 1001
     assert host.tsp_plan_graph_run(None, 1) == 1001
     assert host.tsp_plan_graph_time(None, 1, None) == 1001

@@ -1079,6 +1079,186 @@ def test_tf32_prerounded_launch_matches_rounding_launch(gpu, orc, bm):
             hip.tsp_free(p)
 
 
+def same_bits_or_nan(a, b):
+    """Equal bit for bit, except that NaN equals NaN whatever its payload."""
+    na, nb = np.isnan(a), np.isnan(b)
+    return np.array_equal(na, nb) and np.array_equal(a.view(np.uint32)[~na], b.view(np.uint32)[~nb])
+
+
+@pytest.mark.parametrize("colB", [64, 128])
+@pytest.mark.parametrize("bm", [64, 16, 8])
+def test_b_3byte_launch_matches_4byte_launch(gpu, orc, bm, colB):
+    """TSP_LAUNCH_B_3BYTE: B's tf32 values as the top 3 bytes of their fp32
+    words (tsp_pack_3byte_device, equal byte for byte to the host packing)
+    give the C of the 4-byte launch of the same operands bit for bit, for
+    every 64-column variant (dense and packed A, depth 1-3, scalar and
+    lane-loaded indices), with the second column chunk at a 3-byte offset
+    (colB 128).  An Inf and a NaN whose payload lies only in the dropped low
+    byte (it becomes a quiet NaN) reach the same rows of C as NaN / Inf.
+    Launches the form has no kernel for are refused."""
+    tsp = gpu
+    hip, _ = tsp.load()
+    rng = np.random.default_rng(90 + bm + colB)
+    A = random_matrix(tsp, rng, 3 * bm + 5, 400, 40, 1)
+    B, cbp = random_b(tsp, rng, A.cols, colB, 1)
+    nan_row, inf_row = int(A.colidx[0]), int(A.colidx[A.nnz // 2])
+    if inf_row == nan_row:
+        inf_row = int(A.colidx[-1])
+    Bu = B.view(np.uint32)
+    Bu[nan_row, 3] = 0x7f800001
+    Bu[inf_row, 5] = 0x7f800000
+    sub = tsp.Csr(A.rows, A.cols, A.rowptr, A.colidx, A.val, 1)
+    sub.orig_row = np.arange(A.rows, dtype=np.int32)
+    t = tsp.tile_create(sub, A.cols, bm, 1)
+    arr = t.arrays()
+    rows, cs = tsp.pretreatment(t, 1 << 20)
+    assert not (rows & 0x80000000).any()
+    bufs = {}
+
+    def alloc(name, nbytes):
+        p = C.c_void_p()
+        assert hip.tsp_malloc(C.byref(p), max(nbytes, 4)) == 0
+        bufs[name] = p
+        return p
+
+    def up(name, a):
+        p = alloc(name, a.nbytes)
+        assert hip.tsp_memcpy_h2d(p, a.ctypes.data_as(C.c_void_p), a.nbytes) == 0
+        return p
+
+    def down(name, like):
+        out = np.zeros_like(like)
+        assert hip.tsp_memcpy_d2h(out.ctypes.data_as(C.c_void_p), bufs[name], out.nbytes) == 0
+        return out
+
+    try:
+        dense = np.ascontiguousarray(arr["dense"]).view(np.float32)
+        up("val", dense); up("col", arr["tile_colidx"]); up("rows", rows); up("cs", cs); up("B", B)
+        assert hip.tsp_round_tf32_device(bufs["val"], dense.size, None) == 0
+        assert hip.tsp_round_tf32_device(bufs["B"], B.size, None) == 0
+        alloc("B3", B.size * 3)
+        assert hip.tsp_pack_3byte_device(bufs["B"], bufs["B3"], B.size, None) == 0
+        assert hip.tsp_device_sync() == 0
+        Br = down("B", B)
+        host3 = np.zeros(B.size * 3, np.uint8)
+        assert hip.tsp_pack_3byte_bits(Br.ctypes.data_as(C.c_void_p), host3.ctypes.data_as(C.c_void_p), B.size) == 0
+        assert np.array_equal(down("B3", host3), host3)
+        Cz = np.zeros((A.rows, cbp), dtype=np.float32)
+        alloc("C4", Cz.nbytes)
+        alloc("C3", Cz.nbytes)
+        variants = [(False, None, None)]
+        if bm != 64:
+            bn = tsp.tile_bn(bm, 1)
+            up("bmp", np.ascontiguousarray(arr["bitmap"]))
+            nv, pv, vp = C.c_longlong(), C.c_void_p(), C.c_void_p()
+            assert hip.tsp_tiles_pack_device(t.tilenum, bm, bn, 1, bufs["val"], bufs["bmp"], C.byref(nv),
+                                             C.byref(pv), C.byref(vp), None) == 0
+            bufs["pv"], bufs["vp"] = pv, vp
+            variants.append((True, pv, vp))
+
+        def launch(cname, packed, pv, vp, b, s, flags, w=64):
+            assert hip.tsp_memset(bufs[cname], 0, Cz.nbytes) == 0
+            return hip.tsp_spmm_launch_ex(bm, 1, len(rows), cbp, pv if packed else bufs["val"],
+                                          bufs["bmp"] if packed else None, vp if packed else None, bufs["rows"],
+                                          bufs["cs"], b, bufs[cname], bufs["col"], A.rows, None, w, s, 0, 0, 0,
+                                          flags)
+        first = None
+        for packed, pv, vp in variants:
+            for li in ((0, 2) if bm != 64 else (0,)):
+                for s in (1, 2, 3):
+                    say(f"3-byte B bm={bm} colB={colB} packed={packed} lane indices={li} stages={s}")
+                    assert launch("C4", packed, pv, vp, bufs["B"], s, 1 | li) == 0
+                    assert launch("C3", packed, pv, vp, bufs["B3"], s, 1 | li | 32) == 0
+                    assert hip.tsp_device_sync() == 0
+                    c4, c3 = down("C4", Cz), down("C3", Cz)
+                    assert same_bits_or_nan(c3, c4), (packed, li, s)
+                    first = c4 if first is None else first
+        # the NaN and the Inf reached C, and every other entry is within
+        # the tf32 tolerance of the fp64 reference (a tile multiplies its
+        # zeros too, and 0 x NaN = 0 x Inf = NaN: every row of a row-block
+        # with a tile on those columns is hit, as in the reference's tiles)
+        assert np.isnan(first[:, 3]).any() and np.isinf(first).any()
+        uses = np.array([np.isin(A.colidx[A.rowptr[r]:A.rowptr[r + 1]], (nan_row, inf_row)).any()
+                         for r in range(A.rows)])
+        hit = np.repeat(np.add.reduceat(uses, np.arange(0, A.rows, bm)) > 0, bm)[:A.rows]
+        Bf = B.copy()
+        Bf.view(np.uint32)[nan_row, 3] = 0
+        Bf.view(np.uint32)[inf_row, 5] = 0
+        Cref, Cabs = reference(orc, A, Bf, colB)
+        assert_close(first[~hit, :colB], Cref[~hit], Cabs[~hit], 1, f"bm {bm}")
+        # refused: a chunk width without a 3-byte kernel, fp16, tile pairs,
+        # and operands not declared tf32 -- all before any launch
+        if cbp % 128 == 0 and bm != 64:
+            assert launch("C3", False, None, None, bufs["B3"], 1, 1 | 32, w=128) != 0
+        assert launch("C3", False, None, None, bufs["B3"], 1, 32) != 0
+        assert launch("C3", False, None, None, bufs["B3"], 1, 1 | 8 | 32) != 0
+        assert hip.tsp_spmm_launch_ex(bm, 0, len(rows), cbp, bufs["val"], None, None, bufs["rows"], bufs["cs"],
+                                      bufs["B3"], bufs["C3"], bufs["col"], A.rows, None, 64, 1, 0, 0, 0, 1 | 32) != 0
+    finally:
+        for p in bufs.values():
+            hip.tsp_free(p)
+
+
+def test_plan_b_3byte(gpu, orc):
+    """A tf32 plan whose classes read B in the 3-byte form computes C bit for
+    bit as with the 4-byte form -- with hot rows too, whose slots in the
+    3-byte copy are refilled every step -- at 64-column chunks; at another
+    width the class reads the 4-byte form again.  Split tasks (atomic
+    flushes) stay within tolerance.  fp16 plans refuse the form."""
+    tsp = gpu
+    rng = np.random.default_rng(123)
+    A = skewed_matrix(tsp, rng, 3000, 4096, 60, 1)
+    unsplit = (1 << 20,) * 3
+    for colB in (64, 128):
+        B, cbp = random_b(tsp, rng, A.cols, colB, 1)
+        Cref, Cabs = reference(orc, A, B, colB)
+        subs = tsp.matrix_split(A, 2.0, 1.5)
+        tiles = [tsp.tile_create(s, A.cols, bm, 1) for s, bm in zip(subs, (64, 16, 8))]
+        active = [bm for t, bm in zip(tiles, (64, 16, 8)) if t.tilenum]
+        assert len(active) == 3
+        plan = tsp.Plan(tiles[0], tiles[1], tiles[2], A.rows, A.cols, cbp, 1, B)
+        try:
+            plan.set_th(*unsplit)
+            for bm in active:
+                plan.set_variant(bm, 64)
+            plan.run(zero_c=True)
+            base = plan.download_c()
+            assert_close(base[:, :colB], Cref, Cabs, 1, f"4-byte B colB={colB}")
+            for bm in active:
+                assert plan.get_b_3byte(bm) == 0
+                plan.set_b_3byte(bm, True)
+                assert plan.get_b_3byte(bm) == 1
+            for budget in (0, 1 << 20):
+                say(f"plan 3-byte B colB={colB} hot budget={budget}")
+                plan.set_hot_rows(budget)
+                plan.run(zero_c=True)
+                assert np.array_equal(plan.download_c().view(np.uint32), base.view(np.uint32)), budget
+                plan.time(3)
+                plan.run(zero_c=True)
+                assert np.array_equal(plan.download_c().view(np.uint32), base.view(np.uint32)), budget
+            if cbp % 128 == 0:
+                plan.set_variant(8, 128)
+                assert plan.get_b_3byte(8) == 0
+                plan.run(zero_c=True)
+                assert np.array_equal(plan.download_c().view(np.uint32), base.view(np.uint32))
+            plan.set_th(8, 8, 8)
+            plan.run(zero_c=True)
+            assert_close(plan.download_c()[:, :colB], Cref, Cabs, 1, f"3-byte B, split tasks, colB={colB}")
+        finally:
+            plan.close()
+    Af = skewed_matrix(tsp, rng, 500, 1024, 20, 0)
+    Bf, cbp = random_b(tsp, rng, Af.cols, 64, 0)
+    subs = tsp.matrix_split(Af, 2.0, 1.5)
+    tiles = [tsp.tile_create(s, Af.cols, bm, 0) for s, bm in zip(subs, (64, 16, 8))]
+    plan = tsp.Plan(tiles[0], tiles[1], tiles[2], Af.rows, Af.cols, cbp, 0, Bf)
+    try:
+        with pytest.raises(Exception):
+            plan.set_b_3byte(8, True)
+        assert plan.get_b_3byte(8) == 0
+    finally:
+        plan.close()
+
+
 @pytest.mark.parametrize("prec", [0, 1])
 def test_chunk_xcd_placement_chunk_counts(gpu, orc, prec):
     """One column chunk per XCD group with 2, 4 and 8 chunks (colB 64, 128,

@@ -371,6 +371,42 @@ def test_split_bf16_bits(tsp):
     assert nan.sum() == 3 and (out[nan] == np.uint32(0x7FC07FC0)).all()
 
 
+def test_pack_3byte_bits(tsp):
+    """The 3-byte form of B (tsp_pack_3byte_bits, the function the device
+    packing calls): value i occupies bytes 3i .. 3i+2, little-endian, and
+    holds bits 8-31 of its fp32 word, so widening (bytes as bits 8-31, zero
+    low byte) gives back every tf32 value exactly -- every sign, exponent
+    and mantissa, zeros, subnormals and Inf; a NaN stays a NaN (one whose
+    payload lies only in the dropped byte gets the quiet bit); n must be a
+    multiple of 4."""
+    hip = tsp.load()[0]
+    rng = np.random.default_rng(6)
+    raw = rng.integers(0, 1 << 32, 100000, dtype=np.uint64).astype(np.uint32)
+    x = np.concatenate([raw, np.array([0x3F800000, 0x7F7FFFFF, 0x00000001, 0x00800000, 0x80000000, 0,
+                                       0x7F800000, 0xFF800000, 0x7F800001, 0xFF8000FF, 0x7FC00000, 0x7F800100],
+                                      np.uint32)])
+    x = x[: x.size // 4 * 4]
+    tf = np.zeros_like(x)
+    assert hip.tsp_round_tf32_bits(x.ctypes.data_as(C.c_void_p), tf.ctypes.data_as(C.c_void_p), x.size) == 0
+    out = np.zeros(3 * tf.size, np.uint8)
+    assert hip.tsp_pack_3byte_bits(tf.ctypes.data_as(C.c_void_p), out.ctypes.data_as(C.c_void_p), tf.size) == 0
+    b = out.reshape(-1, 3).astype(np.uint32)
+    wide = (b[:, 0] << np.uint32(8)) | (b[:, 1] << np.uint32(16)) | (b[:, 2] << np.uint32(24))
+    f, g = tf.view(np.float32), wide.view(np.float32)
+    nan = np.isnan(f)
+    assert nan.sum() >= 3
+    # tf32 values have a zero low byte: the form is the identity on them
+    assert ((tf[~nan] & np.uint32(0xFF)) == 0).all()
+    assert np.array_equal(wide[~nan], tf[~nan])
+    assert np.isnan(g[nan]).all() and np.array_equal(np.signbit(g[nan]), np.signbit(f[nan]))
+    assert np.array_equal(wide[nan] & np.uint32(0xFF800000), tf[nan] & np.uint32(0xFF800000))
+    # a NaN whose payload is all in the low byte keeps being a NaN, quiet
+    lowpay = nan & ((tf & np.uint32(0x007FFF00)) == 0)
+    assert lowpay.sum() >= 2 and ((wide[lowpay] & np.uint32(0x00400000)) != 0).all()
+    # four values per 12 bytes, n a multiple of 4
+    assert hip.tsp_pack_3byte_bits(tf.ctypes.data_as(C.c_void_p), out.ctypes.data_as(C.c_void_p), 6) == 1001
+
+
 def test_round_tf32_bits_special_values(tsp, orc):
     """The kernels' tf32 operand rounding (tsp_round_tf32_bits, the same
     function the device code calls) equals the oracle's nearest-even rounding

@@ -175,6 +175,8 @@ HIP_SYMBOLS = {
     "tsp_pairs_supported": (C.c_int, [C.c_int, C.c_int, C.c_int]),
     "tsp_split_bf16_bits": (C.c_int, [_P, _P, C.c_size_t]),
     "tsp_split_bf16_device": (C.c_int, [_P, _P, C.c_size_t, _P]),
+    "tsp_pack_3byte_bits": (C.c_int, [_P, _P, C.c_size_t]),
+    "tsp_pack_3byte_device": (C.c_int, [_P, _P, C.c_size_t, _P]),
     "tsp_switch_v64": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v16": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
     "tsp_switch_v8": (C.c_int, [C.c_int, C.c_int, C.c_int, _P, _P, _P, _P, _P, _P, C.c_int, _P]),
@@ -245,6 +247,8 @@ HOST_SYMBOLS = {
     "tsp_plan_get_lane_indices": (C.c_int, [_P, C.c_int]),
     "tsp_plan_set_pairs": (C.c_int, [_P, C.c_int, C.c_int]),
     "tsp_plan_get_pairs": (C.c_int, [_P, C.c_int]),
+    "tsp_plan_set_b_3byte": (C.c_int, [_P, C.c_int, C.c_int]),
+    "tsp_plan_get_b_3byte": (C.c_int, [_P, C.c_int]),
     "tsp_plan_get_placement": (C.c_int, [_P, C.c_int]),
     "tsp_plan_set_panels": (C.c_int, [_P, C.c_int, C.c_int, C.c_int]),
     "tsp_plan_get_panels": (C.c_int, [_P, C.c_int, _IP, _IP]),
@@ -688,11 +692,22 @@ class Plan:
         return load()[1].tsp_plan_get_lane_indices(self.p, bm)
 
     def set_pairs(self, bm: int, on: bool):
-        """Tile pairs (two tiles per K = 32 MFMA; fp16 8-/16-row classes)."""
+        """Tile pairs (two tiles per K = 32 MFMA; fp16 8-/16-row classes,
+        tf32 8-row classes)."""
         _check("tsp_plan_set_pairs", load()[1].tsp_plan_set_pairs(self.p, bm, int(on)))
 
     def get_pairs(self, bm: int) -> int:
         return load()[1].tsp_plan_get_pairs(self.p, bm)
+
+    def set_b_3byte(self, bm: int, on: bool):
+        """B in the 3-byte form for a class of a tf32 plan (64-column chunks,
+        single tiles, no panel sweep): same result, a quarter fewer bytes
+        per gathered B row."""
+        _check("tsp_plan_set_b_3byte", load()[1].tsp_plan_set_b_3byte(self.p, bm, int(on)))
+
+    def get_b_3byte(self, bm: int) -> int:
+        """Whether the class's launches read B in the 3-byte form."""
+        return load()[1].tsp_plan_get_b_3byte(self.p, bm)
 
     def set_placement(self, bm: int, placement: int):
         """XCD placement: 0 = contiguous eighths, 1 = runs dealt round-robin."""

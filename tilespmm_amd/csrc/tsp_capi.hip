@@ -310,11 +310,16 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
                        int placement, int flags)
 {
     if (flags & ~(TSP_LAUNCH_OPERANDS_TF32 | TSP_LAUNCH_LANE_INDICES | TSP_LAUNCH_TILE_PAIRS |
-                  TSP_LAUNCH_SKIP_ZERO_STORES))
+                  TSP_LAUNCH_SKIP_ZERO_STORES | TSP_LAUNCH_B_3BYTE))
         return TSP_EINVAL;
     if ((flags & TSP_LAUNCH_TILE_PAIRS) &&
         (!tsp_pairs_supported(bm, prec, w > 0 ? w : tsp::default_chunk_width(bm, colB_p)) ||
          (prec == TSP_PREC_TF32 && !(flags & TSP_LAUNCH_OPERANDS_TF32))))
+        return TSP_EINVAL;
+    // 3-byte B: tf32 values only, single tiles (the chunk width is checked by
+    // the kernel selection: only 64-column instantiations exist)
+    if ((flags & TSP_LAUNCH_B_3BYTE) && (prec != TSP_PREC_TF32 || !(flags & TSP_LAUNCH_OPERANDS_TF32) ||
+                                         (flags & TSP_LAUNCH_TILE_PAIRS)))
         return TSP_EINVAL;
     if (bm != 64 && bm != 16 && bm != 8) return TSP_EINVAL;
     if (prec != TSP_PREC_FP16 && prec != TSP_PREC_TF32) return TSP_EINVAL;
@@ -326,7 +331,9 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
     if (w > 0 && (colB_p % w != 0 || !tsp::valid_variant(bm, w, stages > 0 ? stages : 1))) return TSP_EINVAL;
     if (rowblkblock == 0) return TSP_OK;
     if (!d_val || !d_rows || !d_colstart || !d_B || !d_C || !d_colidx) return TSP_EINVAL;
-    const int kprec = prec == TSP_PREC_TF32 && (flags & TSP_LAUNCH_OPERANDS_TF32) ? tsp::kPrecTf32Exact : prec;
+    const int kprec = (flags & TSP_LAUNCH_B_3BYTE)                                   ? tsp::kPrecTf32B3
+                      : prec == TSP_PREC_TF32 && (flags & TSP_LAUNCH_OPERANDS_TF32) ? tsp::kPrecTf32Exact
+                                                                                    : prec;
     return tsp::launch(bm, kprec, rowblkblock, colB_p, d_val, d_bitmap, d_vptr, d_rows, d_colstart, d_B,
                        d_C, d_colidx, c_rows, (hipStream_t)stream, w, stages, tasks_per_wave, order,
                        placement, (flags & TSP_LAUNCH_LANE_INDICES) != 0, 0, 0, 1, nullptr, 0, false,
@@ -411,6 +418,19 @@ __global__ __launch_bounds__(256) void round_tf32_kernel(uint32_t *__restrict__ 
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) x[i] = round_tf32_bits(x[i]);
 }
+// 4 values (16 bytes in) -> 12 bytes out per thread
+__global__ __launch_bounds__(256) void pack_3byte_kernel(const uint32_t *__restrict__ x, uint32_t *__restrict__ y,
+                                                         size_t groups)
+{
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < groups; i += stride) {
+        const uint32_t a = pack_3byte_bits(x[4 * i]), b = pack_3byte_bits(x[4 * i + 1]),
+                       c = pack_3byte_bits(x[4 * i + 2]), d = pack_3byte_bits(x[4 * i + 3]);
+        y[3 * i] = a | b << 24;
+        y[3 * i + 1] = b >> 8 | c << 16;
+        y[3 * i + 2] = c >> 16 | d << 8;
+    }
+}
 __global__ __launch_bounds__(256) void split_bf16_kernel(const uint32_t *__restrict__ x, uint32_t *__restrict__ y,
                                                         size_t n)
 {
@@ -433,6 +453,32 @@ int tsp_split_bf16_bits(const uint32_t *in, uint32_t *out, size_t n)
 {
     if (n && (!in || !out)) return TSP_EINVAL;
     for (size_t i = 0; i < n; ++i) out[i] = tsp::split_bf16_bits(in[i]);
+    return TSP_OK;
+}
+
+int tsp_pack_3byte_device(const void *d_src, void *d_dst, size_t n, void *stream)
+{
+    if (n % 4 || (n && (!d_src || !d_dst))) return TSP_EINVAL;
+    if (n == 0) return TSP_OK;
+    if (((uintptr_t)d_src | (uintptr_t)d_dst) & 3) return TSP_EINVAL;
+    const char *s0 = (const char *)d_src, *d0 = (const char *)d_dst;
+    if (d0 < s0 + 4 * n && s0 < d0 + 3 * n) return TSP_EINVAL;   // overlapping
+    const size_t g = n / 4, b = (g + 255) / 256;
+    tsp::pack_3byte_kernel<<<(unsigned)(b < 16384 ? b : 16384), 256, 0, (hipStream_t)stream>>>(
+        (const uint32_t *)d_src, (uint32_t *)d_dst, g);
+    return (int)hipGetLastError();
+}
+
+int tsp_pack_3byte_bits(const uint32_t *in, void *out, size_t n)
+{
+    if (n % 4 || (n && (!in || !out))) return TSP_EINVAL;
+    unsigned char *o = (unsigned char *)out;
+    for (size_t i = 0; i < n; ++i) {
+        const uint32_t v = tsp::pack_3byte_bits(in[i]);
+        o[3 * i] = (unsigned char)v;
+        o[3 * i + 1] = (unsigned char)(v >> 8);
+        o[3 * i + 2] = (unsigned char)(v >> 16);
+    }
     return TSP_OK;
 }
 
@@ -472,7 +518,8 @@ int tsp_gather_kernel(const void *table, size_t table_bytes, int row_bytes, int 
 int tsp_gather_index_stream(const void *d_table, long long table_rows, int row_bytes, const int *d_idx, long long n,
                             void *d_sink, void *stream)
 {
-    const bool rb_ok = row_bytes == 64 || row_bytes == 128 || row_bytes == 256 || row_bytes == 512;
+    const bool rb_ok = row_bytes == 64 || row_bytes == 128 || row_bytes == 256 || row_bytes == 512 ||
+                       row_bytes == 96 || row_bytes == 192 || row_bytes == 384;
     if (!rb_ok || n < 0 || (n > 0 && (!d_table || !d_idx || !d_sink || table_rows <= 0))) return TSP_EINVAL;
     if ((uintptr_t)d_table & 15) return TSP_EINVAL;
     return tsp::launch_stream_gather(d_table, table_rows, row_bytes, d_idx, n, d_sink, (hipStream_t)stream);

@@ -10,13 +10,18 @@ namespace tsp {
 constexpr int kWavesPerBlock = 4;
 constexpr int kBlockThreads = 64 * kWavesPerBlock;
 
-// Tile width BN for a row-block height BM and precision (fp16: 64->32,
-// 16->16, 8->16; tf32: 64->16, 16->8, 8->8), as src/main.cu:267-275 fixes it.
 // Internal precision code of tf32 launches whose operands are tf32 values
 // already (the kernels then skip the per-operand rounding); tile shapes are
 // those of TSP_PREC_TF32.
 constexpr int kPrecTf32Exact = 2;
+// The same, with B's rows in the 3-byte form of pack_3byte_bits (row stride
+// colB_p * 3 bytes): 25% fewer bytes per gathered row, lossless for tf32
+// values.  Built for 64-column chunks (the kernels whose gathered registers
+// are the MFMA operands), without tile pairs or the panel sweep.
+constexpr int kPrecTf32B3 = 3;
 
+// Tile width BN for a row-block height BM and precision (fp16: 64->32,
+// 16->16, 8->16; tf32: 64->16, 16->8, 8->8), as src/main.cu:267-275 fixes it.
 constexpr __host__ __device__ int tile_bn(int bm, int prec)
 {
     return prec == 0 ? (bm == 64 ? 32 : 16) : (bm == 64 ? 16 : 8);
@@ -52,6 +57,18 @@ __host__ __device__ inline uint32_t split_bf16_bits(uint32_t x)
     uint32_t lb;
     __builtin_memcpy(&lb, &lo, 4);
     return hi | (lb >> 16);
+}
+
+// A tf32 value in 3 bytes: the top 24 bits of its fp32 word (sign, exponent,
+// the 10 tf32 mantissa bits and 5 zero bits), which keep every tf32 value
+// exactly; 4 values pack into 12 bytes, little-endian.  A NaN whose payload
+// lies only in the dropped low byte gets the quiet bit, so that it stays a
+// NaN.  The kernels widen a lane's 12 bytes back into 4 fp32 words
+// (widen_3byte).
+__host__ __device__ inline uint32_t pack_3byte_bits(uint32_t x)
+{
+    const bool nan_low_payload = (x & 0x7f800000u) == 0x7f800000u && (x & 0x007fffffu) && !(x & 0x007fff00u);
+    return (nan_low_payload ? x | 0x00400000u : x) >> 8;
 }
 
 // Placement of a launch's workgroups on the XCDs.  The hardware deals
@@ -110,9 +127,9 @@ const void *select_kernel(int bm, int prec, int w, int s, bool packed, bool lane
                           bool pair = false);
 // The instantiations of one row-block class (tsp_spmm_bm{64,16,8}.hip);
 // nullptr for a variant that is not built.  prec: TSP_PREC_FP16,
-// TSP_PREC_TF32 or kPrecTf32Exact.  pair: the tile-pair form (fp16 8- and
-// 16-row tiles at 64- and 128-column chunks; kPrecTf32Exact 8-row tiles at
-// 64-column chunks).
+// TSP_PREC_TF32, kPrecTf32Exact or kPrecTf32B3.  pair: the tile-pair form
+// (fp16 8- and 16-row tiles at 64- and 128-column chunks; kPrecTf32Exact
+// 8-row tiles at 64-column chunks).
 const void *select_kernel_bm64(int prec, int w, int s, bool packed, bool lane_idx, bool sync, bool pair);
 const void *select_kernel_bm16(int prec, int w, int s, bool packed, bool lane_idx, bool sync, bool pair);
 const void *select_kernel_bm8(int prec, int w, int s, bool packed, bool lane_idx, bool sync, bool pair);

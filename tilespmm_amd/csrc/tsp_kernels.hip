@@ -263,20 +263,57 @@ __global__ __launch_bounds__(256) void stream_gather_kernel(const u4 *__restrict
     if ((acc.x & 0xfffffu) == 0x12345u) sink[threadIdx.x] = acc.x ^ acc.y ^ acc.z ^ acc.w;
 }
 
+// The same for rows of 3-byte tf32 values (kPrecTf32B3's B): 12 bytes per
+// lane, as the kernels load them.
+template <int ROWB>
+__global__ __launch_bounds__(256) void stream_gather3_kernel(const uint32_t *__restrict__ tab, long long nrows,
+                                                             const int *__restrict__ idx, long long n,
+                                                             long long per_wave, uint32_t *__restrict__ sink)
+{
+    constexpr int RL = ROWB / 12, RPW = 64 / RL;   // lanes per row, rows per wave instruction
+    const long long wave = ((long long)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int lane = threadIdx.x & 63, q = lane / RL, sub = lane % RL;
+    const long long b = wave * per_wave, e = min(b + per_wave, n);
+    uint32_t acc = 0u;
+    for (long long i = b; i < e; i += 8 * RPW) {
+        uint32_t v[8][3];
+        bool in[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const long long j = i + (long long)u * RPW + q;
+            in[u] = j < e;
+            long long r = in[u] ? (long long)idx[j] : 0;
+            r = r < 0 ? 0 : (r >= nrows ? nrows - 1 : r);
+            // always a valid row: the three words load as one 3-dword load
+            const uint32_t *p = tab + (size_t)r * (ROWB / 4) + 3 * sub;
+            v[u][0] = p[0];
+            v[u][1] = p[1];
+            v[u][2] = p[2];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc ^= in[u] ? v[u][0] ^ v[u][1] ^ v[u][2] : 0u;
+    }
+    if ((acc & 0xfffffu) == 0x12345u) sink[threadIdx.x] = acc;
+}
+
 int launch_stream_gather(const void *table, long long nrows, int row_bytes, const int *idx, long long n, void *sink,
                          hipStream_t s)
 {
     if (n <= 0) return 0;
     const u4 *t = (const u4 *)table;
+    const uint32_t *t3 = (const uint32_t *)table;
     uint32_t *k = (uint32_t *)sink;
     const long long waves = (long long)kGatherBlocks * 4;
-    const int rpw = 64 / (row_bytes / 16);
+    const int rpw = 64 / (row_bytes % 16 ? row_bytes / 12 : row_bytes / 16);
     const long long per = ((n + waves - 1) / waves + 8 * rpw - 1) / (8 * rpw) * (8 * rpw);
     switch (row_bytes) {
     case 64: stream_gather_kernel<64><<<kGatherBlocks, 256, 0, s>>>(t, nrows, idx, n, per, k); break;
     case 128: stream_gather_kernel<128><<<kGatherBlocks, 256, 0, s>>>(t, nrows, idx, n, per, k); break;
     case 256: stream_gather_kernel<256><<<kGatherBlocks, 256, 0, s>>>(t, nrows, idx, n, per, k); break;
     case 512: stream_gather_kernel<512><<<kGatherBlocks, 256, 0, s>>>(t, nrows, idx, n, per, k); break;
+    case 96: stream_gather3_kernel<96><<<kGatherBlocks, 256, 0, s>>>(t3, nrows, idx, n, per, k); break;
+    case 192: stream_gather3_kernel<192><<<kGatherBlocks, 256, 0, s>>>(t3, nrows, idx, n, per, k); break;
+    case 384: stream_gather3_kernel<384><<<kGatherBlocks, 256, 0, s>>>(t3, nrows, idx, n, per, k); break;
     default: return TSP_EINVAL;
     }
     return (int)hipGetLastError();

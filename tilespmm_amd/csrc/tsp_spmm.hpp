@@ -37,7 +37,8 @@
 //   * tf32: operands are rounded to tf32 (nearest-even, 10 mantissa bits) in
 //     registers and multiplied with v_mfma_f32_16x16x4_f32 -- a tf32 product
 //     is exact in fp32, so this is tf32 arithmetic with fp32 accumulate
-//     (CDNA4 has no xf32 MFMA);
+//     (CDNA4 has no xf32 MFMA); with 64-column chunks B may also come in a
+//     3-byte form (kPrecTf32B3: 12-byte loads, widened in registers);
 //   * workgroups are placed on the 8 XCDs (each with its own L2) either as
 //     8 contiguous ranges of task ranges (neighbouring row-blocks share B
 //     rows) or as runs of 4 workgroups dealt to the XCDs in turn (skewed
@@ -93,6 +94,16 @@ __device__ __forceinline__ int place_block(int b, int nb, int placement)
     return x < r ? x * (q + 1) + k : r * (q + 1) + (x - r) * q + k;
 }
 
+// 4 tf32 values in the 3-byte form of pack_3byte_bits (bytes 0-11 of p,
+// 3 per value, little-endian) -> their fp32 words.  v_perm_b32 takes bytes
+// 0-3 from its second operand and 4-7 from its first; selector 0x0c gives a
+// zero byte.
+__device__ __forceinline__ u4 widen_3byte(u4 p)
+{
+    return u4{p.x << 8, __builtin_amdgcn_perm(p.y, p.x, 0x0504030cu), __builtin_amdgcn_perm(p.z, p.y, 0x0403020cu),
+              p.z & 0xffffff00u};
+}
+
 // PK selects the bitmap-packed A format (8- and 16-row classes): per tile a
 // row-major occupancy bitmap (BM*BN bits, bit r*BN+c) in `bmp`, and the values
 // of its set bits, in bit order, at `val_` + vptr[tile].  Each lane expands its
@@ -107,8 +118,12 @@ __device__ __forceinline__ int place_block(int b, int nb, int placement)
 // With tile pairs, the synchronised 64-column kernels are held to 5 waves in
 // 96 registers (the compiler's own choice lands one register past it); the
 // 128-column pair kernels are limited to 4 waves by their LDS panels anyway.
+// The 3-byte B kernels are held to the waves of their 4-byte counterparts
+// at depth 3 (8- and 16-row: 5 in 96 registers) and 2 (8-row: 7 in 72): the
+// widening's temporaries cost up to 6 registers more.
 template <int BM, int W, int PREC, int S, bool PK, bool SY, bool PR>
 constexpr int kMinWaves = PR ? (SY && W == 64 && S == 1 ? 5 : 1)
+                          : PREC == kPrecTf32B3 && BM <= 16 ? (S == 3 ? 5 : S == 2 && BM == 8 ? 7 : 1)
                           : BM == 64 && W == 64 && S == 1 && !SY                                      ? 3
                           : SY && PREC == TSP_PREC_FP16 && BM == 16 && W == 128 && S == 1 ? 5
                           : SY && PREC == TSP_PREC_FP16 && BM == 8 && W == 128 && S == 1  ? 5
@@ -169,6 +184,10 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     // registers feed the MFMAs directly and the panel never passes through
     // LDS.  Each load instruction still covers 4 whole 256-byte rows.
     constexpr bool DB = !F16 && VPR == 16 && CB == VV && (SPL ? NV == 4 : NV == KS);
+    // B rows in the 3-byte form: a lane's 4 values are 12 bytes at 3 bytes
+    // per value, widened just before the MFMAs that use them
+    constexpr bool B3 = PREC == kPrecTf32B3;
+    static_assert(!B3 || (DB && !PR && !SY), "3-byte B: 64-column tf32 chunks, single tiles, no panel sweep");
     constexpr int AW = F16 ? (BNU == 32 ? 4 : 2) : SPL ? 4 : KS;   // A words per row group
     using VT = typename std::conditional<F16, _Float16, float>::type;
     using RV = VT __attribute__((ext_vector_type(CB)));     // CB values of one B row
@@ -526,8 +545,16 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
         };
         auto load_b = [&](const int (&cid)[NV], u4 (&dst)[NV]) {
 #pragma unroll
-            for (int i = 0; i < NV; ++i)
-                dst[i] = *(const u4 *)(Bb + ((size_t)cid[i] * ld + col0 + pcol[i]) * sizeof(VT));
+            for (int i = 0; i < NV; ++i) {
+                if constexpr (B3) {
+                    // 12 bytes, 4-byte aligned (rows and chunk columns are
+                    // multiples of 4 values): one 3-dword load
+                    const uint32_t *q = (const uint32_t *)(Bb + ((size_t)cid[i] * ld + col0 + pcol[i]) * 3);
+                    dst[i] = u4{q[0], q[1], q[2], 0u};
+                } else {
+                    dst[i] = *(const u4 *)(Bb + ((size_t)cid[i] * ld + col0 + pcol[i]) * sizeof(VT));
+                }
+            }
         };
         // Flush the accumulators of tasks first..last, which this wave ran back
         // to back and which share one row-block.  A split task (bit 31) is added
@@ -719,6 +746,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
                     RV rv;
                     if constexpr (DB) {
                         u4 x = bd[s];
+                        if constexpr (B3) x = widen_3byte(x);
                         if constexpr (RND) {
                             x.x = rnd(x.x); x.y = rnd(x.y);
                             x.z = rnd(x.z); x.w = rnd(x.w);
@@ -995,13 +1023,18 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
 }
 
 // Host-side address of one instantiation for a launch precision
-// (TSP_PREC_FP16, TSP_PREC_TF32 or kPrecTf32Exact); taking it instantiates
-// the kernel.
+// (TSP_PREC_FP16, TSP_PREC_TF32, kPrecTf32Exact, or kPrecTf32B3 at 64-column
+// chunks without the panel sweep -- nullptr for other chunk widths); taking
+// it instantiates the kernel.
 template <int BM, int W, int S, bool PK, bool LI, bool SY>
 const void *pick_kernel(int prec)
 {
     if (prec == TSP_PREC_FP16) return (const void *)&spmm_kernel<BM, W, TSP_PREC_FP16, S, PK, LI, SY>;
     if (prec == kPrecTf32Exact) return (const void *)&spmm_kernel<BM, W, kPrecTf32Exact, S, PK, LI, SY>;
+    if (prec == kPrecTf32B3) {
+        if constexpr (W == 64 && !SY) return (const void *)&spmm_kernel<BM, W, kPrecTf32B3, S, PK, LI, SY>;
+        return nullptr;
+    }
     return (const void *)&spmm_kernel<BM, W, TSP_PREC_TF32, S, PK, LI, SY>;
 }
 

@@ -38,6 +38,7 @@ struct ClassDev {
     int var_li = 0;               // lane-loaded column indices (TSP_LAUNCH_LANE_INDICES), where a kernel has them
     int wdef = 0;                 // the library's default chunk width for this class
     int var_pr = 0;               // tile pairs (TSP_LAUNCH_TILE_PAIRS; fp16 8-/16-row, 64-/128-column chunks)
+    int var_b3 = 0;               // tf32: B in the 3-byte form (TSP_LAUNCH_B_3BYTE), where a kernel has it
     int fmt = 1;                  // A format on the device: 1 dense tiles, 2 bitmap-packed
     bool pack_ok = false;         // packed format is worth trying (fewer bytes)
     void *d_pval = nullptr;       // packed values (+4 elements of padding)
@@ -85,6 +86,8 @@ struct tsp_plan {
     bool c_shared = false;
     void *d_Bs = nullptr;         // tf32 plans: the same rows as split-bf16 words, made when a class first
                                   // uses tile pairs (their kernels read B in that form)
+    void *d_B3 = nullptr;         // tf32 plans: the same rows in the 3-byte form (colB_p * 3 bytes per row),
+                                  // made when a class first reads B that way
     int hot_cap = 0;              // spare rows after row colA
     int nhot = 0;                 // hot slots in use: row colA + s copies B row d_hot[s]
     int *d_hot = nullptr;
@@ -230,6 +233,14 @@ static bool reads_split_b(const tsp_plan *p, const ClassDev &c)
     return p->prec == TSP_PREC_TF32 && c.var_pr;
 }
 
+// The class's launches read B in the 3-byte form: asked for, and a kernel
+// exists for the variant (tf32, 64-column chunks, single tiles, no panel
+// sweep).
+static bool b3_on(const tsp_plan *p, const ClassDev &c)
+{
+    return p->prec == TSP_PREC_TF32 && c.var_b3 && (c.var_w ? c.var_w : c.wdef) == 64 && !c.var_pr && c.panel == 0;
+}
+
 // The class's launches load column indices per lane: asked for, and a
 // lane-loaded kernel exists for the variant (every packed one; dense ones at
 // chunks of up to 128 columns, without tile pairs or the panel sweep).
@@ -244,9 +255,10 @@ static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
 {
     if (!c.active() || c.ntasks == 0) return TSP_OK;
     const bool pk = c.fmt == 2;
+    const bool b3 = b3_on(p, c);
     const int flags = (p->prec == TSP_PREC_TF32 ? TSP_LAUNCH_OPERANDS_TF32 : 0) |
                       (lane_indices_on(c) ? TSP_LAUNCH_LANE_INDICES : 0) | (c.var_pr ? TSP_LAUNCH_TILE_PAIRS : 0) |
-                      (p->c_shared ? 0 : TSP_LAUNCH_SKIP_ZERO_STORES);
+                      (p->c_shared ? 0 : TSP_LAUNCH_SKIP_ZERO_STORES) | (b3 ? TSP_LAUNCH_B_3BYTE : 0);
     if (c.panel > 0) {
         // the counters are zeroed whenever the launch arguments change
         const std::vector<long long> sig{c.ntasks, c.var_w, c.var_s, c.var_tpw, c.var_order, c.place,
@@ -262,7 +274,8 @@ static int launch_class(tsp_plan *p, ClassDev &c, void *stream = nullptr)
         return st;
     }
     return tsp_spmm_launch_ex(c.bm, p->prec, c.ntasks, p->colB_p, pk ? c.d_pval : c.d_val, pk ? c.d_bmp : nullptr,
-                              pk ? c.d_vptr : nullptr, c.d_rows, c.d_colstart, reads_split_b(p, c) ? p->d_Bs : p->d_B,
+                              pk ? c.d_vptr : nullptr, c.d_rows, c.d_colstart,
+                              reads_split_b(p, c) ? p->d_Bs : b3 ? p->d_B3 : p->d_B,
                               p->d_C, c.d_colidx, p->rowA,
                               stream ? stream : c.stream, c.var_w, c.var_s, c.var_tpw, c.var_order, c.place, flags);
 }
@@ -384,6 +397,50 @@ static int ensure_split_b(tsp_plan *p)
     return TSP_OK;
 }
 
+// The 3-byte form of a tf32 plan's B (TSP_LAUNCH_B_3BYTE): its canonical
+// rows, converted once, and the spare hot-row slots, which every step
+// refills from those rows.
+static long long b3_row_bytes(const tsp_plan *p) { return 3LL * p->colB_p; }
+static int ensure_b3(tsp_plan *p)
+{
+    if (p->d_B3) return TSP_OK;
+    const size_t n = ((size_t)p->colA + (size_t)p->hot_cap) * (size_t)p->colB_p;
+    TSP_TRY(tsp_device_sync());
+    void *b3 = nullptr;
+    TSP_TRY(tsp_malloc(&b3, n * 3));
+    int st = tsp_pack_3byte_device(p->d_B, b3, (size_t)p->colA * (size_t)p->colB_p, nullptr);
+    if (st == TSP_OK && p->nhot) st = tsp_hot_rows_gather(b3, p->colA, b3_row_bytes(p), p->d_hot, p->nhot, nullptr);
+    if (st == TSP_OK) st = tsp_device_sync();
+    if (st != TSP_OK) {               // never keep a half-made copy
+        tsp_free(b3);
+        return st;
+    }
+    p->d_B3 = b3;
+    return TSP_OK;
+}
+
+extern "C" int tsp_plan_set_b_3byte(tsp_plan *p, int bm, int on)
+{
+    if (p) ++p->version;          // any captured graph is stale now
+    if (!p || (on != 0 && on != 1)) return TSP_EINVAL;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) {
+            if (on && p->prec != TSP_PREC_TF32) return TSP_EINVAL;
+            if (on) TSP_TRY(ensure_b3(p));
+            c.var_b3 = on;
+            return TSP_OK;
+        }
+    return TSP_EINVAL;
+}
+
+extern "C" int tsp_plan_get_b_3byte(tsp_plan *p, int bm)
+{
+    if (!p) return -1;
+    for (ClassDev &c : p->cls)
+        if (c.bm == bm) return b3_on(p, c) ? 1 : 0;
+    return -1;
+}
+
 extern "C" int tsp_plan_set_pairs(tsp_plan *p, int bm, int on)
 {
     if (p) ++p->version;          // any captured graph is stale now
@@ -461,6 +518,7 @@ extern "C" int tsp_plan_destroy(tsp_plan *p)
     }
     tsp_free(p->d_B);
     tsp_free(p->d_Bs);
+    tsp_free(p->d_B3);
     tsp_free(p->d_hot);
     tsp_free(p->d_flush);
     tsp_free(p->d_C);
@@ -691,13 +749,15 @@ static long long b_row_bytes(const tsp_plan *p) { return (long long)tsph::val_si
 static int hot_gather(tsp_plan *p)
 {
     if (!p->nhot) return TSP_OK;
-    bool plain = false, split = false;
+    bool plain = false, split = false, b3 = false;
     for (const ClassDev &c : p->cls)
-        if (c.active() && c.ntasks > 0) (reads_split_b(p, c) ? split : plain) = true;
-    if (plain || !split)
+        if (c.active() && c.ntasks > 0) (reads_split_b(p, c) ? split : b3_on(p, c) ? b3 : plain) = true;
+    if (plain || (!split && !b3))
         TSP_TRY(tsp_hot_rows_gather(p->d_B, p->colA, b_row_bytes(p), p->d_hot, p->nhot, p->main));
     if (split && p->d_Bs)
         TSP_TRY(tsp_hot_rows_gather(p->d_Bs, p->colA, b_row_bytes(p), p->d_hot, p->nhot, p->main));
+    if (b3 && p->d_B3)
+        TSP_TRY(tsp_hot_rows_gather(p->d_B3, p->colA, b3_row_bytes(p), p->d_hot, p->nhot, p->main));
     return TSP_OK;
 }
 
@@ -1059,7 +1119,8 @@ static int tune_time_step(tsp_plan *p, double min_ms, double *ms);
 static int tune_class(tsp_plan *p, ClassDev &c)
 {
     if (!c.active() || c.ntasks == 0 || c.var_w || c.var_order || c.var_tpw) return TSP_OK;
-    c.var_pr = 0;                 // steps 1-3 without tile pairs (step 4 tries them)
+    c.var_pr = 0;                 // steps 1-3 without tile pairs or 3-byte B (step 4 tries them)
+    c.var_b3 = 0;
     tsp_kernel_info k;
     TSP_TRY(tsp_kernel_probe(c.bm, p->prec, p->colB_p, &k));
     const bool chunks = p->colB_p / k.cols_per_task >= 2;
@@ -1199,22 +1260,27 @@ static int tune_class(tsp_plan *p, ClassDev &c)
     //    load.  fp16 8- and 16-row classes also try tile pairs (two tiles per
     //    K = 32 MFMA) at 64- and 128-column chunks, tf32 8-row classes at 64
     //    (split-bf16 products), with the same depths and index modes (depth
-    //    1-2 on dense tiles).  The fastest option wins
+    //    1-2 on dense tiles).  tf32 classes at 64-column chunks also try B
+    //    in the 3-byte form (every depth and index mode).  The fastest option wins
     //    unless it is within 1% of step 3's choice at depth 1 with scalar
     //    indices (comparing each option with the best so far instead would
     //    make the pick depend on the order).
     struct DOpt {
-        int w, order, place, st, li, pr;
+        int w, order, place, st, li, pr, b3;
         double ms;
     };
     std::vector<WOpt> dw{{c.var_w, c.var_order, c.place}};
     if (runner.w >= 0) dw.push_back(runner);
     const int nli = c.fmt == 2 ? 2 : 1;
+    // the 3-byte copy of B; without room for it that form is not tried
+    const bool b3_ok = p->prec == TSP_PREC_TF32 && ensure_b3(p) == TSP_OK;
     std::vector<DOpt> dopt;
     for (const WOpt &d : dw) {
         const int wd = d.w ? d.w : k.cols_per_task;
-        for (int li = 0; li < (c.fmt == 2 || (wd <= 128 && c.bm != 64) ? 2 : 1); ++li)
-            for (int st = 1; st <= (wd == 256 ? 2 : 3); ++st) dopt.push_back({d.w, d.order, d.place, st, li, 0, 1e30});
+        for (int b3 = 0; b3 <= (b3_ok && wd == 64 ? 1 : 0); ++b3)
+            for (int li = 0; li < (c.fmt == 2 || (wd <= 128 && c.bm != 64) ? 2 : 1); ++li)
+                for (int st = 1; st <= (wd == 256 ? 2 : 3); ++st)
+                    dopt.push_back({d.w, d.order, d.place, st, li, 0, b3, 1e30});
     }
     bool pair_ok = p->prec == TSP_PREC_FP16 ? c.bm != 64 : c.bm == 8;
     // tf32 pairs read a split copy of B; without room for it they are not tried
@@ -1227,7 +1293,7 @@ static int tune_class(tsp_plan *p, ClassDev &c)
             int place = c.place, order = nch >= 2 ? (c.var_order ? c.var_order : 1) : 0;
             if (place == TSP_PLACE_CHUNK_XCD && !(nch == 2 || nch == 4 || nch == 8)) place = TSP_PLACE_INTERLEAVED;
             for (int li = 0; li < nli; ++li)
-                for (int st = 1; st <= (c.fmt == 2 ? 3 : 2); ++st) dopt.push_back({w, order, place, st, li, 1, 1e30});
+                for (int st = 1; st <= (c.fmt == 2 ? 3 : 2); ++st) dopt.push_back({w, order, place, st, li, 1, 0, 1e30});
         }
     for (int round = 0; round < 2; ++round)
         for (DOpt &o : dopt) {
@@ -1237,6 +1303,7 @@ static int tune_class(tsp_plan *p, ClassDev &c)
             c.var_s = o.st;
             c.var_li = o.li;
             c.var_pr = o.pr;
+            c.var_b3 = o.b3;
             double t = 0;
             TSP_TRY(tune_time_class(p, c.bm, &t));
             o.ms = std::min(o.ms, t);
@@ -1251,12 +1318,13 @@ static int tune_class(tsp_plan *p, ClassDev &c)
     c.var_s = dopt[db].st;
     c.var_li = dopt[db].li;
     c.var_pr = dopt[db].pr;
+    c.var_b3 = dopt[db].b3;
     if (log)
         for (size_t j = 0; j < dopt.size(); ++j)
-            fprintf(stderr, "tune bm=%d chunk width %d order=%d placement=%s stages %d %s indices%s: %.5f ms%s\n",
+            fprintf(stderr, "tune bm=%d chunk width %d order=%d placement=%s stages %d %s indices%s%s: %.5f ms%s\n",
                     c.bm, dopt[j].w ? dopt[j].w : k.cols_per_task, dopt[j].order, place_name[dopt[j].place],
-                    dopt[j].st, dopt[j].li ? "lane" : "scalar", dopt[j].pr ? " tile pairs" : "", dopt[j].ms,
-                    j == db ? "  <- kept" : "");
+                    dopt[j].st, dopt[j].li ? "lane" : "scalar", dopt[j].pr ? " tile pairs" : "",
+                    dopt[j].b3 ? " 3-byte B" : "", dopt[j].ms, j == db ? "  <- kept" : "");
     return tune_panels(p, c, dopt[db].ms);
 }
 
@@ -1379,13 +1447,17 @@ static int tune_time_step(tsp_plan *p, double min_ms, double *ms)
 // Hot B rows during tuning.  The thresholds and class variants are tuned
 // with kHotTuneBytes of hot rows whenever any column is gathered at least
 // TSP_HOT_MIN_GATHERS times; then whole steps are timed without hot rows and
-// with them (best of two interleaved rounds of at least 20 ms each) and the
-// hot rows stay when they are at least 2% faster.  On the skewed MI355X cases
+// with them (best of three interleaved rounds, each 3 untimed steps after
+// the switch and then at least 30 ms) and the hot rows stay when they are at
+// least 1% faster.  (With two rounds of 20 ms straight after the switch,
+// configuration 5 in tf32 with B in the 3-byte form measured 3.55 ms with
+// them and 3.53 without, where single runs of each give 3.44 and 3.61 ms.)
+// On the skewed MI355X cases
 // the step time is flat from 8 to 64 MB of hot rows (RMAT scale 22: within
 // 0.4% tf32 and 1% fp16) and 1-3% slower at 4 MB, so one budget in the middle
 // of that plateau is timed instead of a noisy search over several.  Deciding
 // before the variants are tuned is not enough: with the default variants the
-// hot rows may miss the 2% bar, and variants tuned without them then hide
+// hot rows may miss the bar, and variants tuned without them then hide
 // their gain (RMAT fp16 colB 128 ran 4.8 instead of 3.9 ms that way).
 // TSP_HOT_BYTES=<bytes> pins the budget instead.
 static constexpr long long kHotTuneBytes = 16LL << 20;
@@ -1399,18 +1471,45 @@ static int hot_candidates(tsp_plan *p, long long *ncand)
     return TSP_OK;
 }
 
+// A class's tuned variant, to compare two tunings and reinstall one.
+struct ClassVariant {
+    int fmt, w, s, tpw, order, li, pr, b3, place, panel, lag;
+};
+static ClassVariant save_variant(const ClassDev &c)
+{
+    return {c.fmt, c.var_w, c.var_s, c.var_tpw, c.var_order, c.var_li, c.var_pr, c.var_b3, c.place, c.panel,
+            c.panel_lag};
+}
+static int restore_variant(tsp_plan *p, ClassDev &c, const ClassVariant &v)
+{
+    if (!c.active()) return TSP_OK;
+    TSP_TRY(tsp_plan_set_format(p, c.bm, v.fmt));
+    TSP_TRY(tsp_plan_set_panels(p, c.bm, v.panel, v.panel > 0 ? v.lag : 1));
+    c.var_w = v.w;
+    c.var_s = v.s;
+    c.var_tpw = v.tpw;
+    c.var_order = v.order;
+    c.var_li = v.li;
+    c.var_pr = v.pr;
+    c.var_b3 = v.b3;
+    c.place = v.place;
+    ++p->version;
+    return TSP_OK;
+}
+
 static int decide_hot_rows(tsp_plan *p, bool *kept)
 {
     const long long budgets[2] = {0, kHotTuneBytes};
     double best[2] = {1e30, 1e30};
-    for (int round = 0; round < 2; ++round)
+    for (int round = 0; round < 3; ++round)
         for (int j = 0; j < 2; ++j) {
             TSP_TRY(tsp_plan_set_hot_rows(p, budgets[j]));
             double ms = 0;
-            TSP_TRY(tune_time_step(p, 20.0, &ms));
+            if (p->tune_mode != TSP_TUNE_COLD) TSP_TRY(tsp_plan_time(p, 3, &ms));
+            TSP_TRY(tune_time_step(p, 30.0, &ms));
             best[j] = std::min(best[j], ms);
         }
-    *kept = best[1] <= 0.98 * best[0];
+    *kept = best[1] <= 0.99 * best[0];
     if (getenv("TSP_TUNE_LOG"))
         for (int j = 0; j < 2; ++j)
             fprintf(stderr, "tune hot rows %lld MB: %.5f ms%s\n", budgets[j] >> 20, best[j],
@@ -1491,13 +1590,33 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
         bool kept = false;
         if (hot_tuning) TSP_TRY(decide_hot_rows(p, &kept));
         if (hot_tuning && !kept) {
-            // the variants were tuned for the hot rows: tune them again without
+            // the variants were tuned for the hot rows: tune them again
+            // without, and keep the new set only if it runs the step faster
+            // without hot rows than the first set does (a tuning from
+            // scratch can settle elsewhere: configuration 5 in tf32 went
+            // from 3.63 ms with the first set to 4.74 ms)
+            ClassVariant first[3], second[3];
+            for (int i = 0; i < 3; ++i) first[i] = save_variant(p->cls[i]);
             for (ClassDev &c : p->cls) {
-                c.var_w = c.var_s = c.var_tpw = c.var_order = c.var_li = c.var_pr = 0;
+                c.var_w = c.var_s = c.var_tpw = c.var_order = c.var_li = c.var_pr = c.var_b3 = 0;
                 c.place = TSP_PLACE_CONTIGUOUS;
                 TSP_TRY(tsp_plan_set_panels(p, c.bm, 0, 1));
                 TSP_TRY(tune_class(p, c));
             }
+            for (int i = 0; i < 3; ++i) second[i] = save_variant(p->cls[i]);
+            double t[2] = {1e30, 1e30};
+            for (int round = 0; round < 2; ++round)
+                for (int j = 0; j < 2; ++j) {
+                    for (int i = 0; i < 3; ++i) TSP_TRY(restore_variant(p, p->cls[i], j ? second[i] : first[i]));
+                    double ms = 0;
+                    TSP_TRY(tune_time_step(p, 20.0, &ms));
+                    t[j] = std::min(t[j], ms);
+                }
+            const bool retuned = t[1] <= t[0];
+            for (int i = 0; i < 3; ++i) TSP_TRY(restore_variant(p, p->cls[i], retuned ? second[i] : first[i]));
+            if (getenv("TSP_TUNE_LOG"))
+                fprintf(stderr, "tune without hot rows: variants tuned with them %.5f ms, re-tuned %.5f ms%s\n", t[0],
+                        t[1], retuned ? "  <- re-tuned kept" : "  <- first kept");
         }
         // The thresholds again, with the tuned variants: the cross product
         // above timed them with the library's default variants, and a
@@ -1533,13 +1652,22 @@ extern "C" int tsp_plan_tune(tsp_plan *p, int tune, int th_out[3], double *model
             best[i] = opts[i][bj];
         }
         TSP_TRY(tsp_plan_set_th(p, best[0], best[1], best[2]));
-        // the split form of B stays only if a tuned class reads it
-        bool split = false;
-        for (ClassDev &c : p->cls) split |= c.active() && reads_split_b(p, c);
+        // the split and 3-byte forms of B stay only if a tuned class reads them
+        bool split = false, b3 = false;
+        for (ClassDev &c : p->cls) {
+            split |= c.active() && reads_split_b(p, c);
+            b3 |= c.active() && b3_on(p, c);
+        }
         if (p->d_Bs && !split) {
             TSP_TRY(tsp_device_sync());
             TSP_TRY(tsp_free(p->d_Bs));
             p->d_Bs = nullptr;
+        }
+        if (p->d_B3 && !b3) {
+            TSP_TRY(tsp_device_sync());
+            TSP_TRY(tsp_free(p->d_B3));
+            p->d_B3 = nullptr;
+            for (ClassDev &c : p->cls) c.var_b3 = 0;
         }
         t3 = now_ms();
     }
