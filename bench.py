@@ -614,6 +614,9 @@ def stream_floor(tsp, hip, A, subs, prec, cbp, b3=False):
     stream = np.concatenate([tsp.tile_create(sb, A.cols, bm, prec).arrays()["tile_colidx"].astype(np.int32)
                              for sb, bm in zip(subs, (64, 16, 8)) if sb.rows > 0])
     row_bytes = cbp * (2 if prec == 0 else 4)
+    if row_bytes not in (64, 128, 256, 512):
+        return {"row_bytes": row_bytes, "indices": int(stream.size),
+                "skipped": "the index-stream probe reads rows of 64 to 512 bytes"}
     cnt = np.bincount(stream, minlength=A.cols)
     H = min(int((16 << 20) // row_bytes), int((cnt >= 4).sum()))
     order = np.argsort(-cnt, kind="stable")[:H]
@@ -704,7 +707,7 @@ def gather_stream(tsp, hip, args):
     out = stream_floor(tsp, hip, A, subs, prec, cbp, b3=b3)
     print(json.dumps({"gather_stream": NAMES[args.config], "prec": prec, "colB": colB,
                       "tuned_step_ms": round(step_ms, 5), "tuned_hot_rows": hot_tuned, **out,
-                      "gather_floor_over_step": round(out["floor_ms"] / step_ms, 4),
+                      "gather_floor_over_step": round(out["floor_ms"] / step_ms, 4) if "floor_ms" in out else None,
                       "floor_plus_c_write_over_step": round(out.get("floor_plus_c_write_ms", 0.0) / step_ms, 4)}),
           flush=True)
 
@@ -746,7 +749,7 @@ def main():
     ap.add_argument("--pairs", type=ints3, default=None,
                     help="pin tile pairs per class 64,16,8 (1 off, 2 on, 0 keep; fp16 8-/16-row classes, tf32 8-row class)")
     ap.add_argument("--b3", type=ints3, default=None,
-                    help="pin B in the 3-byte form per class 64,16,8 (1 off, 2 on, 0 keep; tf32, 64-column chunks)")
+                    help="pin B in the 3-byte form per class 64,16,8 (1 off, 2 on, 0 keep; tf32)")
     ap.add_argument("--panels", type=ints3, default=None,
                     help="pin the panel-synchronised sweep per class: B rows per panel (0 = off)")
     ap.add_argument("--panel-lag", type=ints3, default=None,
@@ -809,7 +812,8 @@ def main():
     # the floor of the headline step's own B-row gathers (stream_floor)
     dk = rec["classes"][max(rec["classes"], key=lambda k: rec["classes"][k]["ms"])]
     floor = stream_floor(tsp, hip, A, subs, A.prec, rec["colB_padded"], b3=bool(dk.get("b_3byte")))
-    floor["floor_over_step"] = round(floor["floor_ms"] / rec["ms_per_step"], 4)
+    if "floor_ms" in floor:
+        floor["floor_over_step"] = round(floor["floor_ms"] / rec["ms_per_step"], 4)
     if "floor_plus_c_write_ms" in floor:
         floor["floor_plus_c_write_over_step"] = round(floor["floor_plus_c_write_ms"] / rec["ms_per_step"], 4)
     rec["gather_floor"] = floor

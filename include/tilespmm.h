@@ -232,9 +232,9 @@ int tsp_plan_get_pairs(tsp_plan *plan, int bm);
 /* B in the 3-byte form (TSP_LAUNCH_B_3BYTE) for one class of a tf32 plan: 1
  * on, 0 off (fp16 plans: TSP_EINVAL for on).  Switching it on makes the
  * plan's 3-byte copy of B (colB_p * 3 bytes per row plus the hot-row
- * slots) if it has none.  The setting applies to the class's launches at
- * 64-column chunks without tile pairs or the panel sweep; the results are
- * bit for bit those of the 4-byte form.  get returns whether the class's
+ * slots) if it has none.  The setting applies to the class's launches
+ * without tile pairs or the panel sweep; the results are bit for bit those
+ * of the 4-byte form.  get returns whether the class's
  * launches read the 3-byte form (1 / 0), or -1 on a bad argument.
  * tsp_plan_tune picks, and frees the copy when no class keeps it.  No
  * counterpart in the reference. */

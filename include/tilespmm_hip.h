@@ -228,11 +228,12 @@ int tsp_spmm_launch_placed(int bm, int prec, int rowblkblock, int colB_p, const 
  * empty rows, for instance, cost no write.  NaN is stored.  No counterpart
  * in the reference, whose kernels store every row of every tile. */
 #define TSP_LAUNCH_SKIP_ZERO_STORES 16
-/* TSP_LAUNCH_B_3BYTE (tf32 with TSP_LAUNCH_OPERANDS_TF32, chunk width 64, no
- * tile pairs; not for the panel sweep): d_B holds B's rows in the 3-byte
- * form of tsp_pack_3byte_device -- each tf32 value as the top 3 bytes of its
- * fp32 word, row r at byte offset r * colB_p * 3 -- which the kernels gather
- * with 12-byte loads and widen in registers.  Every tf32 value is kept
+/* TSP_LAUNCH_B_3BYTE (tf32 with TSP_LAUNCH_OPERANDS_TF32, no tile pairs; not
+ * for the panel sweep): d_B holds B's rows in the 3-byte form of
+ * tsp_pack_3byte_device -- each tf32 value as the top 3 bytes of its fp32
+ * word, row r at byte offset r * colB_p * 3 -- which the kernels gather with
+ * 12-byte loads and widen in registers (64-column chunks) or before their
+ * LDS panel (other widths).  Every tf32 value is kept
  * exactly, so the result is bit for bit that of the 4-byte launch, while each
  * gathered row is a quarter smaller (and rows no longer start at multiples
  * of a power of two, which spread the most gathered rows unevenly over the

@@ -1085,17 +1085,19 @@ def same_bits_or_nan(a, b):
     return np.array_equal(na, nb) and np.array_equal(a.view(np.uint32)[~na], b.view(np.uint32)[~nb])
 
 
-@pytest.mark.parametrize("colB", [64, 128])
+@pytest.mark.parametrize("colB", [64, 128, 256])
 @pytest.mark.parametrize("bm", [64, 16, 8])
 def test_b_3byte_launch_matches_4byte_launch(gpu, orc, bm, colB):
     """TSP_LAUNCH_B_3BYTE: B's tf32 values as the top 3 bytes of their fp32
     words (tsp_pack_3byte_device, equal byte for byte to the host packing)
     give the C of the 4-byte launch of the same operands bit for bit, for
-    every 64-column variant (dense and packed A, depth 1-3, scalar and
-    lane-loaded indices), with the second column chunk at a 3-byte offset
-    (colB 128).  An Inf and a NaN whose payload lies only in the dropped low
-    byte (it becomes a quiet NaN) reach the same rows of C as NaN / Inf.
-    Launches the form has no kernel for are refused."""
+    every variant the 4-byte form has (chunk widths 32-256 -- 64 gathers
+    into the MFMA operands, the others widen into the LDS panel -- dense
+    and packed A, depth 1-3, scalar and lane-loaded indices), with later
+    column chunks at 3-byte offsets.  An Inf and a NaN whose payload lies
+    only in the dropped low byte (it becomes a quiet NaN) reach the same
+    rows of C as NaN / Inf.  Tile pairs, the panel sweep, fp16 and operands
+    not declared tf32 refuse the form."""
     tsp = gpu
     hip, _ = tsp.load()
     rng = np.random.default_rng(90 + bm + colB)
@@ -1163,16 +1165,25 @@ def test_b_3byte_launch_matches_4byte_launch(gpu, orc, bm, colB):
                                           bufs["cs"], b, bufs[cname], bufs["col"], A.rows, None, w, s, 0, 0, 0,
                                           flags)
         first = None
-        for packed, pv, vp in variants:
-            for li in ((0, 2) if bm != 64 else (0,)):
-                for s in (1, 2, 3):
-                    say(f"3-byte B bm={bm} colB={colB} packed={packed} lane indices={li} stages={s}")
-                    assert launch("C4", packed, pv, vp, bufs["B"], s, 1 | li) == 0
-                    assert launch("C3", packed, pv, vp, bufs["B3"], s, 1 | li | 32) == 0
-                    assert hip.tsp_device_sync() == 0
-                    c4, c3 = down("C4", Cz), down("C3", Cz)
-                    assert same_bits_or_nan(c3, c4), (packed, li, s)
-                    first = c4 if first is None else first
+        ran = 0
+        for w in (32, 64, 128, 256):
+            if cbp % w:
+                continue
+            for packed, pv, vp in variants:
+                for li in ((0, 2) if bm != 64 else (0,)):
+                    for s in (1, 2, 3):
+                        say(f"3-byte B bm={bm} colB={colB} w={w} packed={packed} lane indices={li} stages={s}")
+                        st4 = launch("C4", packed, pv, vp, bufs["B"], s, 1 | li, w)
+                        st3 = launch("C3", packed, pv, vp, bufs["B3"], s, 1 | li | 32, w)
+                        assert (st3 == 0) == (st4 == 0), (w, packed, li, s, st4, st3)
+                        if st4:
+                            continue      # a variant neither form has
+                        assert hip.tsp_device_sync() == 0
+                        c4, c3 = down("C4", Cz), down("C3", Cz)
+                        assert same_bits_or_nan(c3, c4), (w, packed, li, s)
+                        first = c4 if first is None else first
+                        ran += 1
+        assert ran >= (6 if bm == 64 else 12)
         # the NaN and the Inf reached C, and every other entry is within
         # the tf32 tolerance of the fp64 reference (a tile multiplies its
         # zeros too, and 0 x NaN = 0 x Inf = NaN: every row of a row-block
@@ -1186,10 +1197,11 @@ def test_b_3byte_launch_matches_4byte_launch(gpu, orc, bm, colB):
         Bf.view(np.uint32)[inf_row, 5] = 0
         Cref, Cabs = reference(orc, A, Bf, colB)
         assert_close(first[~hit, :colB], Cref[~hit], Cabs[~hit], 1, f"bm {bm}")
-        # refused: a chunk width without a 3-byte kernel, fp16, tile pairs,
-        # and operands not declared tf32 -- all before any launch
-        if cbp % 128 == 0 and bm != 64:
-            assert launch("C3", False, None, None, bufs["B3"], 1, 1 | 32, w=128) != 0
+        # refused: the panel sweep, fp16, tile pairs, and operands not
+        # declared tf32 -- all before any launch
+        assert hip.tsp_spmm_launch_panels(bm, 1, len(rows), cbp, bufs["val"], None, None, bufs["rows"], bufs["cs"],
+                                          bufs["B3"], bufs["C3"], bufs["col"], A.rows, None, 64, 1, 0, 0, 0, 1 | 32,
+                                          A.cols, 256, 2, bufs["C4"], 1024) != 0
         assert launch("C3", False, None, None, bufs["B3"], 1, 32) != 0
         assert launch("C3", False, None, None, bufs["B3"], 1, 1 | 8 | 32) != 0
         assert hip.tsp_spmm_launch_ex(bm, 0, len(rows), cbp, bufs["val"], None, None, bufs["rows"], bufs["cs"],
@@ -1202,8 +1214,8 @@ def test_b_3byte_launch_matches_4byte_launch(gpu, orc, bm, colB):
 def test_plan_b_3byte(gpu, orc):
     """A tf32 plan whose classes read B in the 3-byte form computes C bit for
     bit as with the 4-byte form -- with hot rows too, whose slots in the
-    3-byte copy are refilled every step -- at 64-column chunks; at another
-    width the class reads the 4-byte form again.  Split tasks (atomic
+    3-byte copy are refilled every step -- at any chunk width; with tile
+    pairs the class reads the split form instead.  Split tasks (atomic
     flushes) stay within tolerance.  fp16 plans refuse the form."""
     tsp = gpu
     rng = np.random.default_rng(123)
@@ -1236,11 +1248,19 @@ def test_plan_b_3byte(gpu, orc):
                 plan.time(3)
                 plan.run(zero_c=True)
                 assert np.array_equal(plan.download_c().view(np.uint32), base.view(np.uint32)), budget
-            if cbp % 128 == 0:
-                plan.set_variant(8, 128)
-                assert plan.get_b_3byte(8) == 0
-                plan.run(zero_c=True)
-                assert np.array_equal(plan.download_c().view(np.uint32), base.view(np.uint32))
+            for w in (32, 128):
+                if cbp % w == 0:
+                    plan.set_variant(8, w)
+                    assert plan.get_b_3byte(8) == 1
+                    plan.run(zero_c=True)
+                    assert np.array_equal(plan.download_c().view(np.uint32), base.view(np.uint32)), w
+            plan.set_variant(8, 64)
+            plan.set_pairs(8, True)
+            assert plan.get_b_3byte(8) == 0 and plan.get_pairs(8) == 1
+            plan.run(zero_c=True)
+            assert_close(plan.download_c()[:, :colB], Cref, Cabs, 1, f"tile pairs beside 3-byte B, colB={colB}")
+            plan.set_pairs(8, False)
+            assert plan.get_b_3byte(8) == 1
             plan.set_th(8, 8, 8)
             plan.run(zero_c=True)
             assert_close(plan.download_c()[:, :colB], Cref, Cabs, 1, f"3-byte B, split tasks, colB={colB}")

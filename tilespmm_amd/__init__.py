@@ -700,9 +700,9 @@ class Plan:
         return load()[1].tsp_plan_get_pairs(self.p, bm)
 
     def set_b_3byte(self, bm: int, on: bool):
-        """B in the 3-byte form for a class of a tf32 plan (64-column chunks,
-        single tiles, no panel sweep): same result, a quarter fewer bytes
-        per gathered B row."""
+        """B in the 3-byte form for a class of a tf32 plan (single tiles,
+        no panel sweep): same result, a quarter fewer bytes per gathered B
+        row."""
         _check("tsp_plan_set_b_3byte", load()[1].tsp_plan_set_b_3byte(self.p, bm, int(on)))
 
     def get_b_3byte(self, bm: int) -> int:

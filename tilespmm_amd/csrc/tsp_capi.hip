@@ -316,8 +316,8 @@ int tsp_spmm_launch_ex(int bm, int prec, int rowblkblock, int colB_p, const void
         (!tsp_pairs_supported(bm, prec, w > 0 ? w : tsp::default_chunk_width(bm, colB_p)) ||
          (prec == TSP_PREC_TF32 && !(flags & TSP_LAUNCH_OPERANDS_TF32))))
         return TSP_EINVAL;
-    // 3-byte B: tf32 values only, single tiles (the chunk width is checked by
-    // the kernel selection: only 64-column instantiations exist)
+    // 3-byte B: tf32 values only, single tiles (and no panel sweep: the
+    // panel launch does not accept the flag)
     if ((flags & TSP_LAUNCH_B_3BYTE) && (prec != TSP_PREC_TF32 || !(flags & TSP_LAUNCH_OPERANDS_TF32) ||
                                          (flags & TSP_LAUNCH_TILE_PAIRS)))
         return TSP_EINVAL;

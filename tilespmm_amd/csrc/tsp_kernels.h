@@ -16,8 +16,7 @@ constexpr int kBlockThreads = 64 * kWavesPerBlock;
 constexpr int kPrecTf32Exact = 2;
 // The same, with B's rows in the 3-byte form of pack_3byte_bits (row stride
 // colB_p * 3 bytes): 25% fewer bytes per gathered row, lossless for tf32
-// values.  Built for 64-column chunks (the kernels whose gathered registers
-// are the MFMA operands), without tile pairs or the panel sweep.
+// values.  Built without tile pairs or the panel sweep.
 constexpr int kPrecTf32B3 = 3;
 
 // Tile width BN for a row-block height BM and precision (fp16: 64->32,

@@ -118,12 +118,14 @@ __device__ __forceinline__ u4 widen_3byte(u4 p)
 // With tile pairs, the synchronised 64-column kernels are held to 5 waves in
 // 96 registers (the compiler's own choice lands one register past it); the
 // 128-column pair kernels are limited to 4 waves by their LDS panels anyway.
-// The 3-byte B kernels are held to the waves of their 4-byte counterparts
-// at depth 3 (8- and 16-row: 5 in 96 registers) and 2 (8-row: 7 in 72): the
-// widening's temporaries cost up to 6 registers more.
+// The 64-column 3-byte B kernels are held to the waves of their 4-byte
+// counterparts at depth 3 (8- and 16-row: 5 in 96 registers) and 2 (8-row: 7
+// in 72): their widening's temporaries cost up to 6 registers more.  (The
+// LDS-panel ones widen before the LDS write and need fewer registers than
+// their 4-byte counterparts.)
 template <int BM, int W, int PREC, int S, bool PK, bool SY, bool PR>
 constexpr int kMinWaves = PR ? (SY && W == 64 && S == 1 ? 5 : 1)
-                          : PREC == kPrecTf32B3 && BM <= 16 ? (S == 3 ? 5 : S == 2 && BM == 8 ? 7 : 1)
+                          : PREC == kPrecTf32B3 && BM <= 16 && W == 64 ? (S == 3 ? 5 : S == 2 && BM == 8 ? 7 : 1)
                           : BM == 64 && W == 64 && S == 1 && !SY                                      ? 3
                           : SY && PREC == TSP_PREC_FP16 && BM == 16 && W == 128 && S == 1 ? 5
                           : SY && PREC == TSP_PREC_FP16 && BM == 8 && W == 128 && S == 1  ? 5
@@ -185,9 +187,10 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     // LDS.  Each load instruction still covers 4 whole 256-byte rows.
     constexpr bool DB = !F16 && VPR == 16 && CB == VV && (SPL ? NV == 4 : NV == KS);
     // B rows in the 3-byte form: a lane's 4 values are 12 bytes at 3 bytes
-    // per value, widened just before the MFMAs that use them
+    // per value, widened just before the MFMAs that use them (DB) or before
+    // they are written to the LDS panel
     constexpr bool B3 = PREC == kPrecTf32B3;
-    static_assert(!B3 || (DB && !PR && !SY), "3-byte B: 64-column tf32 chunks, single tiles, no panel sweep");
+    static_assert(!B3 || (!PR && !SY), "3-byte B: single tiles, no panel sweep");
     constexpr int AW = F16 ? (BNU == 32 ? 4 : 2) : SPL ? 4 : KS;   // A words per row group
     using VT = typename std::conditional<F16, _Float16, float>::type;
     using RV = VT __attribute__((ext_vector_type(CB)));     // CB values of one B row
@@ -769,6 +772,7 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
                 u4 x = src[i];
+                if constexpr (B3) x = widen_3byte(x);
                 if constexpr (RND) {
                     x.x = rnd(x.x); x.y = rnd(x.y);
                     x.z = rnd(x.z); x.w = rnd(x.w);
@@ -1023,16 +1027,15 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
 }
 
 // Host-side address of one instantiation for a launch precision
-// (TSP_PREC_FP16, TSP_PREC_TF32, kPrecTf32Exact, or kPrecTf32B3 at 64-column
-// chunks without the panel sweep -- nullptr for other chunk widths); taking
-// it instantiates the kernel.
+// (TSP_PREC_FP16, TSP_PREC_TF32, kPrecTf32Exact, or kPrecTf32B3 without the
+// panel sweep -- nullptr with it); taking it instantiates the kernel.
 template <int BM, int W, int S, bool PK, bool LI, bool SY>
 const void *pick_kernel(int prec)
 {
     if (prec == TSP_PREC_FP16) return (const void *)&spmm_kernel<BM, W, TSP_PREC_FP16, S, PK, LI, SY>;
     if (prec == kPrecTf32Exact) return (const void *)&spmm_kernel<BM, W, kPrecTf32Exact, S, PK, LI, SY>;
     if (prec == kPrecTf32B3) {
-        if constexpr (W == 64 && !SY) return (const void *)&spmm_kernel<BM, W, kPrecTf32B3, S, PK, LI, SY>;
+        if constexpr (!SY) return (const void *)&spmm_kernel<BM, W, kPrecTf32B3, S, PK, LI, SY>;
         return nullptr;
     }
     return (const void *)&spmm_kernel<BM, W, TSP_PREC_TF32, S, PK, LI, SY>;

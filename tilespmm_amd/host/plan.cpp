@@ -234,11 +234,10 @@ static bool reads_split_b(const tsp_plan *p, const ClassDev &c)
 }
 
 // The class's launches read B in the 3-byte form: asked for, and a kernel
-// exists for the variant (tf32, 64-column chunks, single tiles, no panel
-// sweep).
+// exists for the variant (tf32, single tiles, no panel sweep).
 static bool b3_on(const tsp_plan *p, const ClassDev &c)
 {
-    return p->prec == TSP_PREC_TF32 && c.var_b3 && (c.var_w ? c.var_w : c.wdef) == 64 && !c.var_pr && c.panel == 0;
+    return p->prec == TSP_PREC_TF32 && c.var_b3 && !c.var_pr && c.panel == 0;
 }
 
 // The class's launches load column indices per lane: asked for, and a
@@ -1260,8 +1259,8 @@ static int tune_class(tsp_plan *p, ClassDev &c)
     //    load.  fp16 8- and 16-row classes also try tile pairs (two tiles per
     //    K = 32 MFMA) at 64- and 128-column chunks, tf32 8-row classes at 64
     //    (split-bf16 products), with the same depths and index modes (depth
-    //    1-2 on dense tiles).  tf32 classes at 64-column chunks also try B
-    //    in the 3-byte form (every depth and index mode).  The fastest option wins
+    //    1-2 on dense tiles).  tf32 classes also try B in the 3-byte form
+    //    (every width, depth and index mode).  The fastest option wins
     //    unless it is within 1% of step 3's choice at depth 1 with scalar
     //    indices (comparing each option with the best so far instead would
     //    make the pick depend on the order).
@@ -1277,7 +1276,7 @@ static int tune_class(tsp_plan *p, ClassDev &c)
     std::vector<DOpt> dopt;
     for (const WOpt &d : dw) {
         const int wd = d.w ? d.w : k.cols_per_task;
-        for (int b3 = 0; b3 <= (b3_ok && wd == 64 ? 1 : 0); ++b3)
+        for (int b3 = 0; b3 <= (b3_ok ? 1 : 0); ++b3)
             for (int li = 0; li < (c.fmt == 2 || (wd <= 128 && c.bm != 64) ? 2 : 1); ++li)
                 for (int st = 1; st <= (wd == 256 ? 2 : 3); ++st)
                     dopt.push_back({d.w, d.order, d.place, st, li, 0, b3, 1e30});
