@@ -1191,27 +1191,37 @@ static int tune_class(tsp_plan *p, ClassDev &c)
     // 3. every chunk width, each with both chunk orders when it leaves
     //    several chunks, under both placements (width and placement interact:
     //    narrow chunks gain most when interleaved); format and tasks per wave
-    //    stay as kept
+    //    stay as kept.  tf32 classes time every option with B in both forms:
+    //    the 3-byte form moves the best width (configuration 3: 64-column
+    //    chunks with 4-byte rows, 128-column ones with 3-byte rows, 3% ahead
+    //    of 64) and placement (its chunks share lines that only one XCD's L2
+    //    can reuse)
     struct WOpt {
-        int w, order, place;
+        int w, order, place, b3;
     };
+    // the 3-byte copy of B; without room for it that form is not tried
+    const bool b3_ok = p->prec == TSP_PREC_TF32 && ensure_b3(p) == TSP_OK;
     std::vector<WOpt> wo;
-    WOpt runner{-1, 0, 0};               // the next best of step 3, when close
+    WOpt runner{-1, 0, 0, 0};            // the next best of step 3, when close
     for (int place = TSP_PLACE_CONTIGUOUS; place <= TSP_PLACE_CHUNK_XCD; ++place) {
+        const auto add = [&](int w, int order) {
+            wo.push_back({w, order, place, 0});
+            if (b3_ok) wo.push_back({w, order, place, 1});
+        };
         const std::vector<int> dp = places(p->colB_p / k.cols_per_task);
         if (std::find(dp.begin(), dp.end(), place) != dp.end())
-            wo.push_back({0, place == TSP_PLACE_CHUNK_XCD ? 1 : c.var_order, place});
+            add(0, place == TSP_PLACE_CHUNK_XCD ? 1 : c.var_order);
         for (int w : {32, 64, 128, 256}) {
             if (w == k.cols_per_task || p->colB_p % w != 0 || (c.bm == 64 && w >= 128)) continue;
             const std::vector<int> wp = places(p->colB_p / w);
             if (std::find(wp.begin(), wp.end(), place) == wp.end()) continue;
             if (place == TSP_PLACE_CHUNK_XCD) {
-                wo.push_back({w, 1, place});
+                add(w, 1);
             } else if (p->colB_p / w >= 2) {
-                wo.push_back({w, 1, place});
-                wo.push_back({w, 2, place});
+                add(w, 1);
+                add(w, 2);
             } else {
-                wo.push_back({w, 0, place});
+                add(w, 0);
             }
         }
     }
@@ -1222,6 +1232,7 @@ static int tune_class(tsp_plan *p, ClassDev &c)
                 c.var_w = wo[j].w;
                 c.var_order = wo[j].order;
                 c.place = wo[j].place;
+                c.var_b3 = wo[j].b3;
                 double t = 0;
                 TSP_TRY(tune_time_class(p, c.bm, &t));
                 wms[j] = std::min(wms[j], t);
@@ -1230,10 +1241,10 @@ static int tune_class(tsp_plan *p, ClassDev &c)
         for (size_t j = 1; j < wo.size(); ++j)
             if (wms[j] < wms[bw]) bw = j;
         // keep the step-2 choice unless another option is clearly faster
-        const WOpt keep{0, pl[best].order, pl[best].place};
+        const WOpt keep{0, pl[best].order, pl[best].place, 0};
         size_t kj = 0;
         for (size_t j = 0; j < wo.size(); ++j)
-            if (wo[j].w == 0 && wo[j].place == keep.place) kj = j;
+            if (wo[j].w == 0 && wo[j].place == keep.place && wo[j].b3 == 0) kj = j;
         if (wms[bw] > 0.99 * wms[kj]) bw = kj;
         size_t br = bw;
         for (size_t j = 0; j < wo.size(); ++j)
@@ -1242,11 +1253,12 @@ static int tune_class(tsp_plan *p, ClassDev &c)
         c.var_w = wo[bw].w;
         c.var_order = wo[bw].order;
         c.place = wo[bw].place;
+        c.var_b3 = wo[bw].b3;
         if (log)
             for (size_t j = 0; j < wo.size(); ++j)
-                fprintf(stderr, "tune bm=%d chunk width %d order=%d placement=%s: %.5f ms%s\n", c.bm,
-                        wo[j].w ? wo[j].w : k.cols_per_task, wo[j].order,
-                        place_name[wo[j].place], wms[j], j == bw ? "  <- kept" : "");
+                fprintf(stderr, "tune bm=%d chunk width %d order=%d placement=%s%s: %.5f ms%s\n", c.bm,
+                        wo[j].w ? wo[j].w : k.cols_per_task, wo[j].order, place_name[wo[j].place],
+                        wo[j].b3 ? " 3-byte B" : "", wms[j], j == bw ? "  <- kept" : "");
     }
 
     // 4. pipeline depth (1-3 tiles in flight per wave) x scalar or
@@ -1268,18 +1280,18 @@ static int tune_class(tsp_plan *p, ClassDev &c)
         int w, order, place, st, li, pr, b3;
         double ms;
     };
-    std::vector<WOpt> dw{{c.var_w, c.var_order, c.place}};
+    std::vector<WOpt> dw{{c.var_w, c.var_order, c.place, c.var_b3}};
     if (runner.w >= 0) dw.push_back(runner);
     const int nli = c.fmt == 2 ? 2 : 1;
-    // the 3-byte copy of B; without room for it that form is not tried
-    const bool b3_ok = p->prec == TSP_PREC_TF32 && ensure_b3(p) == TSP_OK;
     std::vector<DOpt> dopt;
     for (const WOpt &d : dw) {
         const int wd = d.w ? d.w : k.cols_per_task;
-        for (int b3 = 0; b3 <= (b3_ok ? 1 : 0); ++b3)
+        for (int f = 0; f <= (b3_ok ? 1 : 0); ++f) {
+            const int b3 = f ? 1 - d.b3 : d.b3;      // step 3's form first
             for (int li = 0; li < (c.fmt == 2 || (wd <= 128 && c.bm != 64) ? 2 : 1); ++li)
                 for (int st = 1; st <= (wd == 256 ? 2 : 3); ++st)
                     dopt.push_back({d.w, d.order, d.place, st, li, 0, b3, 1e30});
+        }
     }
     bool pair_ok = p->prec == TSP_PREC_FP16 ? c.bm != 64 : c.bm == 8;
     // tf32 pairs read a split copy of B; without room for it they are not tried
