@@ -37,8 +37,8 @@
 //   * tf32: operands are rounded to tf32 (nearest-even, 10 mantissa bits) in
 //     registers and multiplied with v_mfma_f32_16x16x4_f32 -- a tf32 product
 //     is exact in fp32, so this is tf32 arithmetic with fp32 accumulate
-//     (CDNA4 has no xf32 MFMA); with 64-column chunks B may also come in a
-//     3-byte form (kPrecTf32B3: 12-byte loads, widened in registers);
+//     (CDNA4 has no xf32 MFMA); B may also come in a 3-byte form
+//     (kPrecTf32B3: 12-byte loads, widened in registers);
 //   * workgroups are placed on the 8 XCDs (each with its own L2) either as
 //     8 contiguous ranges of task ranges (neighbouring row-blocks share B
 //     rows) or as runs of 4 workgroups dealt to the XCDs in turn (skewed
@@ -184,7 +184,8 @@ __global__ __launch_bounds__(kBlockThreads) __attribute__((amdgpu_waves_per_eu(k
     // columns 4n .. 4n+3 with its load i, which is exactly its B operand of
     // MFMA step i (CB = 4 adjacent columns of row KS*q + i), so the gathered
     // registers feed the MFMAs directly and the panel never passes through
-    // LDS.  Each load instruction still covers 4 whole 256-byte rows.
+    // LDS.  Each load instruction still covers 4 whole 256-byte rows (192
+    // with B3).
     constexpr bool DB = !F16 && VPR == 16 && CB == VV && (SPL ? NV == 4 : NV == KS);
     // B rows in the 3-byte form: a lane's 4 values are 12 bytes at 3 bytes
     // per value, widened just before the MFMAs that use them (DB) or before
