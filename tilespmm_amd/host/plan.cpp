@@ -760,16 +760,57 @@ static int hot_gather(tsp_plan *p)
     return TSP_OK;
 }
 
+// A class of at most kTinyTiles tiles and at most 1/kTinyShare of the tiles
+// of the step's largest one runs on the main stream ahead of the others:
+// forked beside a class that fills the device it only starts as that
+// class's waves retire, and the join then waits for its tail (configuration
+// 5 with a 2-tile 16-row class beside 15.2M 8-row tiles: 3.473 ms forked,
+// 3.455 ms ahead).  A larger small class overlaps enough to stay forked
+// (configuration 5 in fp16 at colB 128, 20790 16-row tiles beside 7.7M
+// 8-row ones: 3.478 ms forked, 3.513 ms ahead).  A single class left after
+// them runs on the main stream too.
+static constexpr long long kTinyShare = 128;
+static constexpr long long kTinyTiles = 1024;
+static bool tiny_class(const tsp_plan *p, const ClassDev &c)
+{
+    long long most = 0;
+    for (const ClassDev &x : p->cls)
+        if (x.active() && x.ntasks > 0) most = std::max<long long>(most, x.m->tilenum);
+    return c.active() && c.ntasks > 0 && c.m->tilenum <= kTinyTiles && (long long)c.m->tilenum * kTinyShare <= most;
+}
+
+// The stream a step launches class c on.
+static void *step_stream(tsp_plan *p, const ClassDev &c)
+{
+    if (tiny_class(p, c)) return p->main;
+    int forked = 0;
+    for (const ClassDev &x : p->cls) forked += x.active() && x.ntasks > 0 && !tiny_class(p, x);
+    return forked == 1 ? p->main : c.stream;
+}
+
 static int fork_join_once(tsp_plan *p, int reps)
 {
     if (ClassDev *only = only_class(p)) {
         for (int r = 0; r < reps; ++r) TSP_TRY(launch_class(p, *only, p->main));
         return TSP_OK;
     }
+    // tiny classes first, then the rest: on main, or forked over the class
+    // streams when several remain
+    bool fork = false;
+    for (int pass = 0; pass < 2; ++pass)
+        for (ClassDev &c : p->cls) {
+            if (!c.active() || c.ntasks == 0 || tiny_class(p, c) != (pass == 0)) continue;
+            if (step_stream(p, c) != p->main) {
+                fork = true;
+                continue;
+            }
+            for (int r = 0; r < reps; ++r) TSP_TRY(launch_class(p, c, p->main));
+        }
+    if (!fork) return TSP_OK;
     TSP_TRY(tsp_event_record(p->ev0, p->main));
     for (int i = 0; i < 3; ++i) {
         ClassDev &c = p->cls[i];
-        if (!c.active() || c.ntasks == 0) continue;
+        if (!c.active() || c.ntasks == 0 || step_stream(p, c) == p->main) continue;
         TSP_TRY(tsp_stream_wait_event(c.stream, p->ev0));
         for (int r = 0; r < reps; ++r) TSP_TRY(launch_class(p, c));
         TSP_TRY(tsp_event_record(p->done[i], c.stream));
@@ -973,7 +1014,7 @@ extern "C" int tsp_plan_time_class(tsp_plan *p, int bm, int reps, double *ms)
     // on the stream a step launches the class on (launches of a few
     // microseconds have timed up to twice as long on a class stream as on the
     // main stream)
-    void *s = only_class(p) == c ? p->main : c->stream;
+    void *s = step_stream(p, *c);
     if (p->nhot) {                   // slots valid before the class runs alone
         TSP_TRY(hot_gather(p));
         TSP_TRY(tsp_stream_sync(p->main));
