@@ -109,26 +109,27 @@ def test_table_is_a_model_so_drop_in(tsp):
 EXTRA = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra.jsonl")
 EXTRA2 = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra2.jsonl")
 EXTRA3 = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra3.jsonl")
+EXTRA4 = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra4.jsonl")
 
 
 def all_records():
-    return records() + [json.loads(l) for f in (EXTRA, EXTRA2, EXTRA3) for l in open(f) if l.strip()]
+    return records() + [json.loads(l) for f in (EXTRA, EXTRA2, EXTRA3, EXTRA4) for l in open(f) if l.strip()]
 
 
 def test_policy_against_exhaustive_tuning(tsp):
-    """On its training sweeps (472 cases, 59 matrices) the shipped tree is
-    x1.012 of the exhaustive optimum on average and x1.35 at worst; the
-    provisional single-leaf table (candidate 24) is x1.16 (worst x3.32)."""
+    """On its training sweeps (536 cases, 67 matrices) the shipped tree is
+    x1.009 of the exhaustive optimum on average and x1.27 at worst; the
+    provisional single-leaf table (candidate 24) is x1.14 (worst x3.32)."""
     g, d = tsp.policy_candidates()
     slow = []
     recs = all_records()
-    assert len(recs) == 472 and len({r["matrix"] for r in recs}) == 59
+    assert len(recs) == 536 and len({r["matrix"] for r in recs}) == 67
     for r in recs:
         pg, pd = tsp.predict(np.array(r["features"]), r["prec"])
         a = [i for i in range(len(g)) if g[i] == np.float32(pg) and d[i] == np.float32(pd)]
         assert a, (pg, pd)
         slow.append(r["times_ms"][a[0]] / r["best_ms"])
-    assert np.mean(slow) <= 1.013 and max(slow) <= 1.35, (np.mean(slow), max(slow))
+    assert np.mean(slow) <= 1.010 and max(slow) <= 1.28, (np.mean(slow), max(slow))
     prov = [r["times_ms"][24] / r["best_ms"] for r in recs]
     assert np.mean(slow) < np.mean(prov)
 
@@ -136,11 +137,12 @@ def test_policy_against_exhaustive_tuning(tsp):
 def test_policy_leave_one_matrix_out():
     """The fit generalises to matrices it has not seen: refitting without
     each matrix in turn (policy_tune's fit as shipped: depth 4, at least 4
-    cases per leaf, no worst-case weight) and scoring the held-out matrix's
-    cases gives x1.030 on average, with 83% of the cases within x1.05.  The
-    worst held-out cases (x1.45, x1.43) are small block-sparse matrices of a
-    few microseconds per step whose best split the 11 policy features
-    cannot tell from their neighbours'."""
+    cases per leaf, worst-case weight 0.1) and scoring the held-out matrix's
+    cases gives x1.024 on average, with 87% of the cases within x1.05.  The
+    worst held-out cases (x1.95 for a banded matrix at colB 32, x1.64 for a
+    small 64-row-block matrix with scattered entries) are matrices of a few
+    microseconds per step whose best split the 11 policy features cannot
+    tell from their neighbours'."""
     import importlib.util
     spec = importlib.util.spec_from_file_location("policy_tune", os.path.join(ROOT, "tilespmm_amd", "policy_tune.py"))
     pt = importlib.util.module_from_spec(spec)
@@ -157,11 +159,11 @@ def test_policy_leave_one_matrix_out():
     for prec in (0, 1):
         rs = [r for r in recs if r["prec"] == prec]
         for m in sorted({r["matrix"] for r in rs}):
-            root, nodes = pt.fit_tree([r for r in rs if r["matrix"] != m], 4, 4, 0.0)
+            root, nodes = pt.fit_tree([r for r in rs if r["matrix"] != m], 4, 4, 0.1)
             held += [r["times_ms"][walk(root, nodes, r["features"])] / r["best_ms"] for r in rs if r["matrix"] == m]
     held = np.array(held)
-    assert held.size == 472
-    assert held.mean() <= 1.031 and (held <= 1.05).mean() >= 0.83 and held.max() <= 1.46, \
+    assert held.size == 536
+    assert held.mean() <= 1.025 and (held <= 1.05).mean() >= 0.86 and held.max() <= 1.95, \
         (held.mean(), (held <= 1.05).mean(), held.max())
 
 
@@ -172,8 +174,8 @@ def test_policy_on_held_out_config5(tsp):
     """Configuration 5 (RMAT scale 22) is not in the training sweep.  Its
     exhaustive sweep with the full shipped path (runtime tuning of every
     candidate) puts the policy's pick within a few percent of the best
-    candidate: fp16 x1.000 (colB 64) and x1.003 (colB 128), tf32 x1.008 and
-    x1.010."""
+    candidate: fp16 x1.000 (colB 64) and x1.038 (colB 128), tf32 x1.002 and
+    x1.000."""
     g, d = tsp.policy_candidates()
     recs = [json.loads(l) for l in open(HELDOUT) if l.strip()]
     assert {(r["prec"], r["colB"]) for r in recs} == {(0, 64), (0, 128), (1, 64), (1, 128)}

@@ -246,6 +246,21 @@ def corpus(which):
             ("uniform_2^17_k4", lambda rng: gen_uniform(rng, 1 << 17, 4)),
         ]
         items += [seeded(n, mk) for n, mk in extra3]
+    if which == "extra4":
+        # neighbours of the block-sparse matrices a depth-4 leave-one-matrix-out
+        # refit of all earlier sweeps served worst (16-row blocks at 2^16,
+        # 8-row blocks at 2^14-2^15)
+        extra4 = [
+            ("blocks16_2^16_d05", lambda rng: gen_blocks(rng, 1 << 16, 16, 0.005)),
+            ("blocks16_2^15_d1", lambda rng: gen_blocks(rng, 1 << 15, 16, 0.01)),
+            ("blocks16_2^14_d2", lambda rng: gen_blocks(rng, 1 << 14, 16, 0.02)),
+            ("blocks16_2^15_d05", lambda rng: gen_blocks(rng, 1 << 15, 16, 0.005)),
+            ("blocks8_2^14_d8", lambda rng: gen_blocks(rng, 1 << 14, 8, 0.08)),
+            ("blocks8_2^13_d4", lambda rng: gen_blocks(rng, 1 << 13, 8, 0.04)),
+            ("blocks8_2^15_d4", lambda rng: gen_blocks(rng, 1 << 15, 8, 0.04)),
+            ("blocks8_2^16_d1", lambda rng: gen_blocks(rng, 1 << 16, 8, 0.01)),
+        ]
+        items += [seeded(n, mk) for n, mk in extra4]
     return items
 
 
@@ -723,7 +738,7 @@ def main():
     tf.add_argument("--per-group", action="store_true", help="one weight pair per (class, prec, width)")
     s = sub.add_parser("sweep")
     s.add_argument("--configs", type=int, nargs="*", default=[])
-    s.add_argument("--corpus", choices=["small", "full", "extra", "extra2", "extra3"], default=None)
+    s.add_argument("--corpus", choices=["small", "full", "extra", "extra2", "extra3", "extra4"], default=None)
     s.add_argument("--precs", type=int, nargs="*", default=[0, 1])
     s.add_argument("--colBs", type=int, nargs="*", default=[32, 128])
     s.add_argument("--reps", type=int, default=30)
