@@ -432,9 +432,8 @@ def measure(tsp, hip, config, prec, colB, args, headline):
         if hit:
             traffic, traffic_note = hit[0].get("hbm_bytes_per_launch"), os.path.relpath(prof, ROOT)
         else:
-            traffic_note = (f"{os.path.relpath(prof, ROOT)} profiles "
-                            f"{'; '.join(e.get('kernel', '?') + ' ' + json.dumps(e.get('variant')) + ' with ' + str(e.get('hot_rows', 0)) + ' hot rows' for e in entries)}"
-                            f", not the tuned {kname} {json.dumps(run_variant)} with {hot_n}")
+            traffic_note = (f"{os.path.relpath(prof, ROOT)} profiles {len(entries)} variants of the {dom}-row "
+                            f"class, not the tuned {kname} {json.dumps(run_variant)} with {hot_n} hot rows")
     roof = {"bound": "hbm", "achieved": round(dk["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": traffic,
             "traffic_over_alg": round(traffic / dk["alg_bytes"], 3) if traffic else None,
