@@ -800,9 +800,20 @@ def test_graph_replay_matches_eager_steps(gpu, orc, prec):
     cbytes = A.rows * cbp * 4
     try:
         unsplit = (1 << 20,) * 3
-        for label, setup in (("default", lambda: None),
-                             ("hot rows", lambda: plan.set_hot_rows(1 << 20)),
-                             ("panel sweep", lambda: (plan.set_format(16, 1), plan.set_panels(16, 256, 2)))):
+        cases = [("default", lambda: None),
+                 ("hot rows", lambda: plan.set_hot_rows(1 << 20)),
+                 ("panel sweep", lambda: (plan.set_format(16, 1), plan.set_panels(16, 256, 2)))]
+        if prec == 1:
+            # B in the 3-byte form for the 64- and 8-row classes (the 16-row
+            # class stays on the panel sweep, which reads 4-byte rows): each
+            # step re-copies the hot rows into the spare rows of both forms
+            def b3_setup():
+                for bm in (64, 16, 8):
+                    plan.set_b_3byte(bm, True)
+                assert [plan.get_b_3byte(bm) for bm in (64, 16, 8)] == [1, 0, 1]
+                assert plan.get_hot_rows()[0] > 0
+            cases.append(("3-byte B rows", b3_setup))
+        for label, setup in cases:
             say(f"graph replay prec={prec}: {label}")
             plan.set_th(*unsplit)
             setup()
