@@ -110,26 +110,27 @@ EXTRA = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra.js
 EXTRA2 = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra2.jsonl")
 EXTRA3 = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra3.jsonl")
 EXTRA4 = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra4.jsonl")
+EXTRA5 = os.path.join(ROOT, "tilespmm_amd", "policy_data", "mi355x_sweep_extra5.jsonl")
 
 
 def all_records():
-    return records() + [json.loads(l) for f in (EXTRA, EXTRA2, EXTRA3, EXTRA4) for l in open(f) if l.strip()]
+    return records() + [json.loads(l) for f in (EXTRA, EXTRA2, EXTRA3, EXTRA4, EXTRA5) for l in open(f) if l.strip()]
 
 
 def test_policy_against_exhaustive_tuning(tsp):
-    """On its training sweeps (536 cases, 67 matrices) the shipped tree is
-    x1.009 of the exhaustive optimum on average and x1.27 at worst; the
-    provisional single-leaf table (candidate 24) is x1.14 (worst x3.32)."""
+    """On its training sweeps (584 cases, 73 matrices) the shipped tree is
+    x1.010 of the exhaustive optimum on average and x1.27 at worst; the
+    provisional single-leaf table (candidate 24) is x1.15 (worst x3.32)."""
     g, d = tsp.policy_candidates()
     slow = []
     recs = all_records()
-    assert len(recs) == 536 and len({r["matrix"] for r in recs}) == 67
+    assert len(recs) == 584 and len({r["matrix"] for r in recs}) == 73
     for r in recs:
         pg, pd = tsp.predict(np.array(r["features"]), r["prec"])
         a = [i for i in range(len(g)) if g[i] == np.float32(pg) and d[i] == np.float32(pd)]
         assert a, (pg, pd)
         slow.append(r["times_ms"][a[0]] / r["best_ms"])
-    assert np.mean(slow) <= 1.010 and max(slow) <= 1.28, (np.mean(slow), max(slow))
+    assert np.mean(slow) <= 1.011 and max(slow) <= 1.28, (np.mean(slow), max(slow))
     prov = [r["times_ms"][24] / r["best_ms"] for r in recs]
     assert np.mean(slow) < np.mean(prov)
 
@@ -137,12 +138,13 @@ def test_policy_against_exhaustive_tuning(tsp):
 def test_policy_leave_one_matrix_out():
     """The fit generalises to matrices it has not seen: refitting without
     each matrix in turn (policy_tune's fit as shipped: depth 4, at least 4
-    cases per leaf, worst-case weight 0.1) and scoring the held-out matrix's
-    cases gives x1.024 on average, with 87% of the cases within x1.05.  The
-    worst held-out cases (x1.95 for a banded matrix at colB 32, x1.64 for a
-    small 64-row-block matrix with scattered entries) are matrices of a few
+    cases per leaf, worst-case weight 0.3) and scoring the held-out matrix's
+    cases gives x1.032 on average, with 83% of the cases within x1.05.  The
+    worst held-out cases (x1.69 and x1.64 for small 64-row-block matrices
+    with scattered entries, x1.64 for a banded matrix) are matrices of a few
     microseconds per step whose best split the 11 policy features cannot
-    tell from their neighbours'."""
+    tell from their neighbours' (banded matrices that differ only in band
+    width have the same features)."""
     import importlib.util
     spec = importlib.util.spec_from_file_location("policy_tune", os.path.join(ROOT, "tilespmm_amd", "policy_tune.py"))
     pt = importlib.util.module_from_spec(spec)
@@ -159,11 +161,11 @@ def test_policy_leave_one_matrix_out():
     for prec in (0, 1):
         rs = [r for r in recs if r["prec"] == prec]
         for m in sorted({r["matrix"] for r in rs}):
-            root, nodes = pt.fit_tree([r for r in rs if r["matrix"] != m], 4, 4, 0.1)
+            root, nodes = pt.fit_tree([r for r in rs if r["matrix"] != m], 4, 4, 0.3)
             held += [r["times_ms"][walk(root, nodes, r["features"])] / r["best_ms"] for r in rs if r["matrix"] == m]
     held = np.array(held)
-    assert held.size == 536
-    assert held.mean() <= 1.025 and (held <= 1.05).mean() >= 0.86 and held.max() <= 1.95, \
+    assert held.size == 584
+    assert held.mean() <= 1.033 and (held <= 1.05).mean() >= 0.82 and held.max() <= 1.69, \
         (held.mean(), (held <= 1.05).mean(), held.max())
 
 

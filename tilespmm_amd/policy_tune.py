@@ -261,6 +261,19 @@ def corpus(which):
             ("blocks8_2^16_d1", lambda rng: gen_blocks(rng, 1 << 16, 8, 0.01)),
         ]
         items += [seeded(n, mk) for n, mk in extra4]
+    if which == "extra5":
+        # neighbours of the banded matrix a depth-4 leave-one-matrix-out refit
+        # of all earlier sweeps served worst (the only banded matrix at 2^16
+        # rows: band widths 64-256, 8-32 entries per row, 2^15-2^17 rows)
+        extra5 = [
+            ("banded_2^16_bw64_k16", lambda rng: gen_banded(rng, 1 << 16, 64, 16)),
+            ("banded_2^16_bw256_k16", lambda rng: gen_banded(rng, 1 << 16, 256, 16)),
+            ("banded_2^15_bw128_k16", lambda rng: gen_banded(rng, 1 << 15, 128, 16)),
+            ("banded_2^17_bw128_k16", lambda rng: gen_banded(rng, 1 << 17, 128, 16)),
+            ("banded_2^16_bw128_k8", lambda rng: gen_banded(rng, 1 << 16, 128, 8)),
+            ("banded_2^16_bw128_k32", lambda rng: gen_banded(rng, 1 << 16, 128, 32)),
+        ]
+        items += [seeded(n, mk) for n, mk in extra5]
     return items
 
 
@@ -738,7 +751,7 @@ def main():
     tf.add_argument("--per-group", action="store_true", help="one weight pair per (class, prec, width)")
     s = sub.add_parser("sweep")
     s.add_argument("--configs", type=int, nargs="*", default=[])
-    s.add_argument("--corpus", choices=["small", "full", "extra", "extra2", "extra3", "extra4"], default=None)
+    s.add_argument("--corpus", choices=["small", "full", "extra", "extra2", "extra3", "extra4", "extra5"], default=None)
     s.add_argument("--precs", type=int, nargs="*", default=[0, 1])
     s.add_argument("--colBs", type=int, nargs="*", default=[32, 128])
     s.add_argument("--reps", type=int, default=30)
